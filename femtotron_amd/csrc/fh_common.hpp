@@ -1,0 +1,110 @@
+// Shared device/host helpers for the femtohip kernels (gfx950, wave64).
+//
+// Element types: bf16 is carried as raw uint16_t bits (round-to-nearest-even
+// conversion, the same rounding torch applies when it narrows fp32 results to
+// bfloat16), fp32 as float.  Every kernel computes in fp32 registers and rounds
+// only where the Hugging Face Llama layer (transformers 5.15.0,
+// models/llama/modeling_llama.py) materialises a bf16 tensor.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "femtohip.h"
+
+namespace fh {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- bf16 bits
+__device__ __forceinline__ float bf2f(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even float -> bf16 (NaN stays a quiet NaN).
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+__device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
+
+// ------------------------------------------------------- element traits
+// Elem<T>::load8 / store8 move 8 consecutive elements between memory and
+// fp32 registers with 128-bit accesses (one dwordx4 for bf16, two for fp32).
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<uint16_t> {
+  static constexpr fh_dtype kDtype = FH_BF16;
+  __device__ __forceinline__ static void load8(const uint16_t* p, float v[8]) {
+    const uint4 q = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+  __device__ __forceinline__ static void store8(uint16_t* p, const float v[8]) {
+    uint4 q;
+    q.x = f2bf(v[0]) | (static_cast<uint32_t>(f2bf(v[1])) << 16);
+    q.y = f2bf(v[2]) | (static_cast<uint32_t>(f2bf(v[3])) << 16);
+    q.z = f2bf(v[4]) | (static_cast<uint32_t>(f2bf(v[5])) << 16);
+    q.w = f2bf(v[6]) | (static_cast<uint32_t>(f2bf(v[7])) << 16);
+    *reinterpret_cast<uint4*>(p) = q;
+  }
+  // Rounds a value to the precision a tensor of this dtype would hold.
+  __device__ __forceinline__ static float rnd(float f) { return round_bf(f); }
+  __device__ __forceinline__ static float ld1(const uint16_t* p) { return bf2f(*p); }
+  __device__ __forceinline__ static void st1(uint16_t* p, float f) { *p = f2bf(f); }
+};
+
+template <>
+struct Elem<float> {
+  static constexpr fh_dtype kDtype = FH_F32;
+  __device__ __forceinline__ static void load8(const float* p, float v[8]) {
+    const float4 a = *reinterpret_cast<const float4*>(p);
+    const float4 b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  __device__ __forceinline__ static void store8(float* p, const float v[8]) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  }
+  __device__ __forceinline__ static float rnd(float f) { return f; }
+  __device__ __forceinline__ static float ld1(const float* p) { return *p; }
+  __device__ __forceinline__ static void st1(float* p, float f) { *p = f; }
+};
+
+// ------------------------------------------------------- wave reductions
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+// ------------------------------------------------------- host-side status
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+
+inline bool aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+}  // namespace fh
+
+#define FH_REQUIRE(cond, msg)                                   \
+  do {                                                          \
+    if (!(cond)) return ::fh::fail(FH_ERR_INVALID, (msg));      \
+  } while (0)

@@ -1,0 +1,186 @@
+"""``fused_checkpoint``: a ``checkpoint_fn`` for ``apply_activation_checkpointing``.
+
+Signature-compatible with ``torch.utils.checkpoint.checkpoint`` (the contract of
+``CheckpointFn`` at femtotron/training/activation_ckpt.py:25-26).  A call whose
+module is a Llama decoder layer on a HIP device, in the configuration the
+reference runs (bf16 or fp32, no attention mask, no KV cache, no hooks, no
+biases, SiLU MLP, TP size 1), is executed by ``FusedDecoderLayerFunction`` on the
+femtohip kernels.  Any other call is handed to ``torch.utils.checkpoint.checkpoint``
+with the same arguments, i.e. it behaves exactly as the reference wrapper.
+
+On a HIP device the fused path never degrades silently: if ``libfemtohip.so`` is
+missing the call raises.
+"""
+from __future__ import annotations
+
+import threading
+from typing import Any
+
+import torch
+from torch.utils.checkpoint import checkpoint as _torch_checkpoint
+
+from . import _lib
+from .fused_layer import FusedDecoderLayerFunction, LayerShape
+
+_KNOWN_KWARGS = {"attention_mask", "position_embeddings", "position_ids", "past_key_values",
+                 "use_cache", "cache_position"}
+
+_counts_lock = threading.Lock()
+_counts = {"fused": 0, "fallback": 0}
+_last_fallback_reason: list[str] = [""]
+
+
+def dispatch_counts() -> dict[str, int]:
+    """How many checkpointed calls took the fused path vs. the stock one."""
+    with _counts_lock:
+        return dict(_counts)
+
+
+def reset_dispatch_counts() -> None:
+    with _counts_lock:
+        _counts["fused"] = 0
+        _counts["fallback"] = 0
+
+
+def last_fallback_reason() -> str:
+    return _last_fallback_reason[0]
+
+
+def _bump(key: str) -> None:
+    with _counts_lock:
+        _counts[key] += 1
+
+
+def _linear_weight(mod: Any) -> torch.Tensor | None:
+    """[out, in] weight of an nn.Linear or of femtotron's Column/RowParallelLinear at TP=1."""
+    w = getattr(mod, "weight", None)
+    if not isinstance(w, torch.Tensor) or getattr(mod, "bias", None) is not None:
+        return None
+    ws = getattr(mod, "world_size", 1)  # femtotron TP wrappers (tensor_parallel/linear.py:52-54)
+    if ws != 1:
+        return None
+    if getattr(mod, "gather_output", False) or getattr(mod, "scatter_input", False):
+        return None
+    return w
+
+
+def _has_hooks(mod: torch.nn.Module) -> bool:
+    for m in mod.modules():
+        if (m._forward_hooks or m._forward_pre_hooks or m._backward_hooks
+                or getattr(m, "_backward_pre_hooks", None)):
+            return True
+    g = torch.nn.modules.module
+    return bool(g._global_forward_hooks or g._global_forward_pre_hooks
+                or g._global_backward_hooks or getattr(g, "_global_backward_pre_hooks", None))
+
+
+def _plan(module: Any, args: tuple, kwargs: dict):
+    """Return (x, cos, sin, shape, weights) if the call can be fused, else a reason string."""
+    if len(args) != 1 or not isinstance(args[0], torch.Tensor):
+        return "hidden_states must be the only positional argument"
+    x = args[0]
+    if not x.is_cuda:
+        return "hidden_states not on a HIP device"
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        return f"dtype {x.dtype}"
+    if x.dim() != 3:
+        return "hidden_states must be [B, S, H]"
+    if set(kwargs) - _KNOWN_KWARGS:
+        return f"unsupported kwargs {sorted(set(kwargs) - _KNOWN_KWARGS)}"
+    if kwargs.get("attention_mask") is not None:
+        return "explicit attention mask"
+    if kwargs.get("past_key_values") is not None or kwargs.get("use_cache"):
+        return "KV cache"
+    pe = kwargs.get("position_embeddings")
+    if not (isinstance(pe, (tuple, list)) and len(pe) == 2):
+        return "position_embeddings (cos, sin) required"
+    cos, sin = pe
+    if torch.is_autocast_enabled():
+        return "autocast active"
+    attn = getattr(module, "self_attn", None)
+    mlp = getattr(module, "mlp", None)
+    ln1 = getattr(module, "input_layernorm", None)
+    ln2 = getattr(module, "post_attention_layernorm", None)
+    if attn is None or mlp is None or ln1 is None or ln2 is None:
+        return "not a Llama decoder layer"
+    if type(module).forward is not _llama_forward():
+        return "decoder layer forward is overridden"
+    cfg = getattr(attn, "config", None)
+    if cfg is None:
+        return "attention has no config"
+    if getattr(cfg, "_attn_implementation", "sdpa") not in ("sdpa", "eager", None):
+        return f"attention implementation {cfg._attn_implementation!r}"
+    if getattr(cfg, "hidden_act", "silu") != "silu":
+        return "MLP activation is not SiLU"
+    if module.training and float(getattr(attn, "attention_dropout", 0.0) or 0.0) > 0.0:
+        return "attention dropout"
+    ws = [_linear_weight(getattr(attn, n, None)) for n in ("q_proj", "k_proj", "v_proj", "o_proj")]
+    ws += [_linear_weight(getattr(mlp, n, None)) for n in ("gate_proj", "up_proj", "down_proj")]
+    if any(w is None for w in ws):
+        return "projection with bias or tensor-parallel size > 1"
+    w1, w2 = getattr(ln1, "weight", None), getattr(ln2, "weight", None)
+    if not isinstance(w1, torch.Tensor) or not isinstance(w2, torch.Tensor):
+        return "RMSNorm without weight"
+    weights = (*ws, w1, w2)
+    if _has_hooks(module):
+        return "module hooks installed"
+    B, S, H = x.shape
+    hd = int(attn.head_dim)
+    nh = ws[0].shape[0] // hd
+    nkv = ws[1].shape[0] // hd
+    F_ = ws[4].shape[0]
+    for t in (cos, sin):
+        if not isinstance(t, torch.Tensor) or t.device != x.device or t.dtype != x.dtype:
+            return "cos/sin must match hidden_states' device and dtype"
+        if t.dim() != 3 or t.shape[1] != S or t.shape[2] != hd or t.shape[0] not in (1, B):
+            return "cos/sin must be [1|B, S, head_dim]"
+    for t in weights:
+        if t.device != x.device or t.dtype != x.dtype or not t.is_contiguous():
+            return "weights must be contiguous, on hidden_states' device, in its dtype"
+    if ws[0].shape != (nh * hd, H) or ws[1].shape != (nkv * hd, H) or ws[2].shape != (nkv * hd, H):
+        return "unexpected q/k/v weight shapes"
+    if ws[3].shape != (H, nh * hd) or ws[5].shape != (F_, H) or ws[6].shape != (H, F_):
+        return "unexpected o/mlp weight shapes"
+    if nkv == 0 or nh % nkv:
+        return "n_heads not a multiple of n_kv_heads"
+    if hd % 16 or H % 8 or F_ % 8 or H > 8192:
+        return "head_dim % 16, hidden % 8, ffn % 8 and hidden <= 8192 required"
+    shp = LayerShape(hidden=H, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn=F_,
+                     eps1=float(ln1.variance_epsilon), eps2=float(ln2.variance_epsilon),
+                     scale=float(attn.scaling))
+    return x.contiguous(), cos.contiguous(), sin.contiguous(), shp, weights
+
+
+_LLAMA_FWD = []
+
+
+def _llama_forward():
+    if not _LLAMA_FWD:
+        from transformers.models.llama.modeling_llama import LlamaDecoderLayer
+        _LLAMA_FWD.append(LlamaDecoderLayer.forward)
+    return _LLAMA_FWD[0]
+
+
+def fused_checkpoint(function, *args, use_reentrant: bool | None = None,
+                     preserve_rng_state: bool = True, debug: bool = False, **kwargs):
+    """Drop-in for ``torch.utils.checkpoint.checkpoint`` as a ``checkpoint_fn``.
+
+    ``debug`` is accepted and has no effect on the fused path (the reference uses it
+    only to format CheckpointError messages); ``preserve_rng_state`` is moot there
+    because the fused layer draws no random numbers.  As in torch, reentrant mode
+    together with ``debug`` raises ValueError (torch/utils/checkpoint.py:499-504)."""
+    if use_reentrant and debug:
+        raise ValueError("debug=True is only supported with use_reentrant=False")
+    torch_only = {k: kwargs.pop(k) for k in ("context_fn", "determinism_check", "early_stop")
+                  if k in kwargs}
+    plan = _plan(function, args, kwargs)
+    if isinstance(plan, str):
+        _last_fallback_reason[0] = plan
+        _bump("fallback")
+        return _torch_checkpoint(function, *args, use_reentrant=use_reentrant,
+                                 preserve_rng_state=preserve_rng_state, debug=debug,
+                                 **torch_only, **kwargs)
+    _lib.lib()  # raises if the HIP library is not built: no silent fallback on GPU
+    x, cos, sin, shp, weights = plan
+    _bump("fused")
+    return FusedDecoderLayerFunction.apply(x, cos, sin, shp, *weights)

@@ -1,0 +1,161 @@
+"""Fused, activation-checkpointed Llama decoder layer (forward, recompute, backward).
+
+This is the drop-in for one ``checkpoint_fn(LlamaDecoderLayer, hidden_states, ...)``
+call of femtotron/training/activation_ckpt.py:78-86.  The forward keeps only the
+layer input (exactly what torch.utils.checkpoint's ``_NoopSaveInputs`` keeps,
+torch/utils/checkpoint.py:794-831); backward recomputes the layer forward up to
+the SwiGLU product (the down projection and final residual add are not needed,
+mirroring the non-reentrant checkpoint's early stop) and then runs the layer's
+backward.
+
+Layer arithmetic (transformers 5.15.0, models/llama/modeling_llama.py:284-325):
+    y1 = RMSNorm1(x)
+    q,k,v = y1 Wq^T, y1 Wk^T, y1 Wv^T          -> one GEMM over [Wq;Wk;Wv]
+    q,k   = RoPE(q,k)                            (in place, fh_rope_fwd)
+    o     = causal GQA attention(q,k,v)
+    h     = x + o Wo^T;  z = RMSNorm2(h)         (fh_add_rmsnorm_fwd)
+    g,u   = z Wg^T, z Wu^T                       -> one GEMM over [Wg;Wu]
+    p     = silu(g)*u                            (fh_swiglu_fwd)
+    out   = h + p Wd^T                           (fh_add)
+
+Token-major layout everywhere: activations are [T, features] with T = B*S, so
+q/k/v are column ranges of one [T, Hq+2Hkv] buffer and attention reads and
+writes heads as column blocks (no transposes).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import attention, ops
+
+
+@dataclass(frozen=True)
+class LayerShape:
+    hidden: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    ffn: int
+    eps1: float
+    eps2: float
+    scale: float
+
+    @property
+    def hq(self) -> int:
+        return self.n_heads * self.head_dim
+
+    @property
+    def hkv(self) -> int:
+        return self.n_kv_heads * self.head_dim
+
+
+def _mm_nt(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """a[M,K] @ b[N,K]^T (nn.Linear orientation)."""
+    return torch.mm(a, b.t())
+
+
+class _Acts:
+    """Recomputed activations the backward needs."""
+
+    __slots__ = ("y1", "rstd1", "qkv", "o", "lse", "h", "rstd2", "z", "gu", "p")
+
+
+def layer_forward(x2: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, shp: LayerShape,
+                  batch: int, seq: int, w: tuple, *, keep: bool):
+    """Run the layer on x2 [T, H].  keep=False returns the output [T, H];
+    keep=True (recompute) stops after the SwiGLU product and returns _Acts."""
+    wq, wk, wv, wo, wg, wu, wd, w1, w2 = w
+    T, H = x2.shape
+    dev = x2.device
+    acts = _Acts() if keep else None
+    rstd1 = torch.empty(T, dtype=torch.float32, device=dev) if keep else None
+    y1 = ops.rmsnorm_fwd(x2, w1, shp.eps1, rstd=rstd1)
+
+    wqkv = torch.cat((wq, wk, wv), 0)
+    qkv = _mm_nt(y1, wqkv)
+    ops.rope_fwd_(qkv, shp.n_heads + shp.n_kv_heads, shp.head_dim, seq, cos, sin)
+    o, lse = attention.attn_fwd(qkv, batch, seq, shp, need_lse=keep)
+    a = _mm_nt(o, wo)
+    rstd2 = torch.empty(T, dtype=torch.float32, device=dev) if keep else None
+    h, z = ops.add_rmsnorm_fwd(x2, a, w2, shp.eps2, rstd=rstd2)
+    del a
+    gu = _mm_nt(z, torch.cat((wg, wu), 0))
+    F_ = shp.ffn
+    p = ops.swiglu_fwd(gu[:, :F_], gu[:, F_:])
+    if keep:
+        acts.y1, acts.rstd1, acts.qkv, acts.o, acts.lse = y1, rstd1, qkv, o, lse
+        acts.h, acts.rstd2, acts.z, acts.gu, acts.p = h, rstd2, z, gu, p
+        return acts
+    del gu, qkv, o, y1, z
+    m = _mm_nt(p, wd)
+    return ops.add(h, m, out=m)
+
+
+def layer_backward(dout2: torch.Tensor, x2: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                   shp: LayerShape, batch: int, seq: int, w: tuple, acts: _Acts):
+    wq, wk, wv, wo, wg, wu, wd, w1, w2 = w
+    F_ = shp.ffn
+    # MLP: m = p Wd^T
+    dwd = torch.mm(dout2.t(), acts.p)
+    dp = torch.mm(dout2, wd)
+    acts.p = None
+    dgu = torch.empty_like(acts.gu)
+    ops.swiglu_bwd(dp, acts.gu[:, :F_], acts.gu[:, F_:], dgu[:, :F_], dgu[:, F_:])
+    del dp
+    acts.gu = None
+    dwgu = torch.mm(dgu.t(), acts.z)
+    dz = torch.mm(dgu, torch.cat((wg, wu), 0))
+    del dgu
+    acts.z = None
+    # post-attention norm + residual: dh = dout + RMSNorm2^T(dz)
+    dh, dw2 = ops.rmsnorm_bwd(dz, acts.h, w2, shp.eps2, rstd=acts.rstd2, dres=dout2)
+    del dz
+    acts.h = None
+    # attention output projection
+    dwo = torch.mm(dh.t(), acts.o)
+    do = torch.mm(dh, wo)
+    dqkv = attention.attn_bwd(do, acts.qkv, acts.o, acts.lse, batch, seq, shp)
+    del do
+    acts.o = acts.lse = acts.qkv = None
+    ops.rope_bwd_(dqkv, shp.n_heads + shp.n_kv_heads, shp.head_dim, seq, cos, sin)
+    wqkv = torch.cat((wq, wk, wv), 0)
+    dwqkv = torch.mm(dqkv.t(), acts.y1)
+    dy1 = torch.mm(dqkv, wqkv)
+    del dqkv
+    acts.y1 = None
+    dx, dw1 = ops.rmsnorm_bwd(dy1, x2, w1, shp.eps1, rstd=acts.rstd1, dres=dh)
+    hq, hkv = shp.hq, shp.hkv
+    dwq, dwk, dwv = dwqkv[:hq], dwqkv[hq:hq + hkv], dwqkv[hq + hkv:]
+    dwg, dwu = dwgu[:F_], dwgu[F_:]
+    return dx, (dwq, dwk, dwv, dwo, dwg, dwu, dwd, dw1, dw2)
+
+
+class FusedDecoderLayerFunction(torch.autograd.Function):
+    """autograd node for one checkpointed decoder layer.
+
+    Saved for backward: the layer input x (plus references to cos/sin and the
+    weights, which the caller keeps alive anyway).  Nothing else survives the
+    forward."""
+
+    @staticmethod
+    def forward(ctx, x, cos, sin, shp, wq, wk, wv, wo, wg, wu, wd, w1, w2):
+        B, S, H = x.shape
+        w = (wq, wk, wv, wo, wg, wu, wd, w1, w2)
+        out = layer_forward(x.reshape(B * S, H), cos, sin, shp, B, S, w, keep=False)
+        ctx.save_for_backward(x, cos, sin, *w)
+        ctx.shp = shp
+        return out.view(B, S, H)
+
+    @staticmethod
+    def backward(ctx, dout):
+        x, cos, sin, *w = ctx.saved_tensors
+        shp = ctx.shp
+        B, S, H = x.shape
+        x2 = x.reshape(B * S, H)
+        with torch.no_grad():
+            acts = layer_forward(x2, cos, sin, shp, B, S, tuple(w), keep=True)
+            dx, dws = layer_backward(dout.contiguous().view(B * S, H), x2, cos, sin, shp, B, S,
+                                     tuple(w), acts)
+        return (dx.view(B, S, H), None, None, None, *dws)

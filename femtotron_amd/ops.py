@@ -1,0 +1,208 @@
+"""Torch-tensor front end of the femtohip C ABI.
+
+Each function validates device, dtype, shape and strides on the host, then
+calls the matching ``fh_*`` entry point on the tensor's current HIP stream.
+Outputs are allocated by the caller or here with ``torch.empty`` (PyTorch's
+caching allocator); the library itself never allocates device memory.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_DT = {torch.bfloat16: _lib.FH_BF16, torch.float32: _lib.FH_F32}
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise TypeError(f"femtohip supports bfloat16 and float32, got {t.dtype}") from None
+
+
+def _require_gpu(*ts: torch.Tensor) -> None:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("femtohip ops take HIP device tensors only")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} vs {t.device}")
+
+
+def _same_dtype(ref: torch.Tensor, *ts: torch.Tensor) -> None:
+    for t in ts:
+        if t is not None and t.dtype != ref.dtype:
+            raise TypeError(f"dtype mismatch: {t.dtype} vs {ref.dtype}")
+
+
+def _rowmajor(t: torch.Tensor, name: str) -> int:
+    """Row stride of a 2-D view whose last dim is contiguous."""
+    if t.dim() != 2 or (t.size(1) > 1 and t.stride(1) != 1):
+        raise ValueError(f"{name}: expected a 2-D view with a contiguous last dim, got "
+                         f"shape {tuple(t.shape)} strides {t.stride()}")
+    return t.stride(0)
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
+def _fptr(t: torch.Tensor | None):
+    if t is None:
+        return None
+    if t.dtype != torch.float32:
+        raise TypeError("fp32 tensor expected")
+    return ctypes.cast(t.data_ptr(), ctypes.POINTER(ctypes.c_float))
+
+
+# ------------------------------------------------------------------ RMSNorm
+def rmsnorm_fwd(x: torch.Tensor, w: torch.Tensor, eps: float, *, out: torch.Tensor | None = None,
+                rstd: torch.Tensor | None = None) -> torch.Tensor:
+    """y = w * to_dtype(x * rsqrt(mean(x^2) + eps)) over the last dim of contiguous x."""
+    _require_gpu(x, w, out, rstd)
+    _same_dtype(x, w, out)
+    if not x.is_contiguous() or not w.is_contiguous():
+        raise ValueError("rmsnorm_fwd: x and w must be contiguous")
+    cols = x.size(-1)
+    rows = x.numel() // max(cols, 1)
+    if w.numel() != cols:
+        raise ValueError("rmsnorm_fwd: weight size != last dim")
+    y = torch.empty_like(x) if out is None else out
+    if rstd is not None and rstd.numel() != rows:
+        raise ValueError("rmsnorm_fwd: rstd must have one entry per row")
+    _lib.call("fh_rmsnorm_fwd", _dtype_code(x), _ptr(x), _ptr(w), _ptr(y), _fptr(rstd), rows,
+              cols, float(eps), _stream(x))
+    return y
+
+
+def add_rmsnorm_fwd(x: torch.Tensor, a: torch.Tensor, w: torch.Tensor, eps: float, *,
+                    rstd: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """h = to_dtype(x + a); y = rmsnorm(h). Returns (h, y)."""
+    _require_gpu(x, a, w, rstd)
+    _same_dtype(x, a, w)
+    if not (x.is_contiguous() and a.is_contiguous() and w.is_contiguous()):
+        raise ValueError("add_rmsnorm_fwd: inputs must be contiguous")
+    if x.shape != a.shape:
+        raise ValueError("add_rmsnorm_fwd: x and a shapes differ")
+    cols = x.size(-1)
+    rows = x.numel() // max(cols, 1)
+    if w.numel() != cols:
+        raise ValueError("add_rmsnorm_fwd: weight size != last dim")
+    h = torch.empty_like(x)
+    y = torch.empty_like(x)
+    _lib.call("fh_add_rmsnorm_fwd", _dtype_code(x), _ptr(x), _ptr(a), _ptr(w), _ptr(h), _ptr(y),
+              _fptr(rstd), rows, cols, float(eps), _stream(x))
+    return h, y
+
+
+def rmsnorm_bwd(dy: torch.Tensor, x: torch.Tensor, w: torch.Tensor, eps: float, *,
+                rstd: torch.Tensor | None = None, dres: torch.Tensor | None = None
+                ) -> tuple[torch.Tensor, torch.Tensor]:
+    """Gradients of rmsnorm_fwd: returns (dx [+ dres], dw)."""
+    _require_gpu(dy, x, w, rstd, dres)
+    _same_dtype(x, dy, w, dres)
+    for t, n in ((dy, "dy"), (x, "x"), (w, "w"), (dres, "dres")):
+        if t is not None and not t.is_contiguous():
+            raise ValueError(f"rmsnorm_bwd: {n} must be contiguous")
+    if dy.shape != x.shape or (dres is not None and dres.shape != x.shape):
+        raise ValueError("rmsnorm_bwd: shape mismatch")
+    cols = x.size(-1)
+    rows = x.numel() // max(cols, 1)
+    if w.numel() != cols:
+        raise ValueError("rmsnorm_bwd: weight size != last dim")
+    dx = torch.empty_like(x)
+    dw = torch.empty_like(w)
+    ws_bytes = _lib.lib().fh_rmsnorm_bwd_workspace_size(rows, cols)
+    ws = torch.empty(max(ws_bytes, 4) // 4, dtype=torch.float32, device=x.device)
+    _lib.call("fh_rmsnorm_bwd", _dtype_code(x), _ptr(dy), _ptr(x), _ptr(w), _fptr(rstd),
+              _ptr(dres), _ptr(dx), _ptr(dw), _ptr(ws), rows, cols, float(eps), _stream(x))
+    return dx, dw
+
+
+# --------------------------------------------------------------------- RoPE
+def _rope(name: str, qk: torch.Tensor, n_heads: int, head_dim: int, seq_len: int,
+          cos: torch.Tensor, sin: torch.Tensor) -> None:
+    _require_gpu(qk, cos, sin)
+    _same_dtype(qk, cos, sin)
+    ld = _rowmajor(qk, name)
+    if qk.size(1) < n_heads * head_dim:
+        raise ValueError(f"{name}: buffer narrower than n_heads*head_dim")
+    cos2 = cos.reshape(-1, head_dim)
+    sin2 = sin.reshape(-1, head_dim)
+    if not (cos2.is_contiguous() and sin2.is_contiguous()) or cos2.shape != sin2.shape:
+        raise ValueError(f"{name}: cos/sin must be contiguous and of equal shape")
+    tokens = qk.size(0)
+    if cos2.size(0) == seq_len:
+        per_token = 0
+        if tokens % seq_len:
+            raise ValueError(f"{name}: tokens not a multiple of seq_len")
+    elif cos2.size(0) == tokens:
+        per_token = 1
+    else:
+        raise ValueError(f"{name}: cos/sin rows ({cos2.size(0)}) match neither seq_len nor tokens")
+    _lib.call(name, _dtype_code(qk), _ptr(qk), ld, tokens, seq_len, n_heads, head_dim, _ptr(cos2),
+              _ptr(sin2), per_token, _stream(qk))
+
+
+def rope_fwd_(qk: torch.Tensor, n_heads: int, head_dim: int, seq_len: int, cos: torch.Tensor,
+              sin: torch.Tensor) -> torch.Tensor:
+    """Rotate heads 0..n_heads-1 of the [tokens, ld] view qk in place."""
+    _rope("fh_rope_fwd", qk, n_heads, head_dim, seq_len, cos, sin)
+    return qk
+
+
+def rope_bwd_(dqk: torch.Tensor, n_heads: int, head_dim: int, seq_len: int, cos: torch.Tensor,
+              sin: torch.Tensor) -> torch.Tensor:
+    _rope("fh_rope_bwd", dqk, n_heads, head_dim, seq_len, cos, sin)
+    return dqk
+
+
+# ------------------------------------------------------------------- SwiGLU
+def swiglu_fwd(g: torch.Tensor, u: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """p = to_dtype(to_dtype(silu(g)) * u) for 2-D row-major views g, u (same row stride)."""
+    _require_gpu(g, u, out)
+    _same_dtype(g, u, out)
+    ld_gu = _rowmajor(g, "swiglu_fwd.g")
+    if _rowmajor(u, "swiglu_fwd.u") != ld_gu or g.shape != u.shape:
+        raise ValueError("swiglu_fwd: g and u must share shape and row stride")
+    rows, cols = g.shape
+    p = torch.empty(rows, cols, dtype=g.dtype, device=g.device) if out is None else out
+    _lib.call("fh_swiglu_fwd", _dtype_code(g), _ptr(g), _ptr(u), ld_gu, _ptr(p),
+              _rowmajor(p, "swiglu_fwd.p"), rows, cols, _stream(g))
+    return p
+
+
+def swiglu_bwd(dp: torch.Tensor, g: torch.Tensor, u: torch.Tensor, dg: torch.Tensor,
+               du: torch.Tensor) -> None:
+    _require_gpu(dp, g, u, dg, du)
+    _same_dtype(g, dp, u, dg, du)
+    ld_gu = _rowmajor(g, "swiglu_bwd.g")
+    ld_d = _rowmajor(dg, "swiglu_bwd.dg")
+    if _rowmajor(u, "swiglu_bwd.u") != ld_gu or _rowmajor(du, "swiglu_bwd.du") != ld_d:
+        raise ValueError("swiglu_bwd: g/u and dg/du must share row strides")
+    if not (dp.shape == g.shape == u.shape == dg.shape == du.shape):
+        raise ValueError("swiglu_bwd: shape mismatch")
+    rows, cols = g.shape
+    _lib.call("fh_swiglu_bwd", _dtype_code(g), _ptr(dp), _rowmajor(dp, "swiglu_bwd.dp"), _ptr(g),
+              _ptr(u), ld_gu, _ptr(dg), _ptr(du), ld_d, rows, cols, _stream(g))
+
+
+def add(a: torch.Tensor, b: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    _require_gpu(a, b, out)
+    _same_dtype(a, b, out)
+    if not (a.is_contiguous() and b.is_contiguous()) or a.shape != b.shape:
+        raise ValueError("add: a and b must be contiguous with equal shapes")
+    o = torch.empty_like(a) if out is None else out
+    _lib.call("fh_add", _dtype_code(a), _ptr(a), _ptr(b), _ptr(o), a.numel(), _stream(a))
+    return o

@@ -1,0 +1,147 @@
+/*
+ * femtohip.h — C ABI of the MI355X (gfx950) kernels behind the fused
+ * activation-checkpointed Llama decoder layer.
+ *
+ * The reference path this library replaces is one checkpointed
+ * `LlamaDecoderLayer` call: the `checkpoint_fn` hook of
+ * femtotron/training/activation_ckpt.py:25-26,78-86 (invoked per layer from
+ * femtotron/model/llama_partial_model.py:205-215), which by default runs
+ * torch.utils.checkpoint.checkpoint around the Hugging Face layer
+ * (transformers 5.15.0, models/llama/modeling_llama.py:284-325).  The reference
+ * has no native code of its own; each entry point below names the aten op
+ * chain of that layer it stands in for.
+ *
+ * Conventions
+ *   - Every pointer is a device pointer owned by the caller; the library never
+ *     allocates or frees device memory.  Scratch space is passed in as a
+ *     `workspace` whose size the matching *_workspace_size() call returns.
+ *   - Tensors are row-major.  `ld*` arguments are row strides in elements.
+ *   - Calls are asynchronous on `stream` (a hipStream_t; 0 = null stream)
+ *     and never synchronise the host.
+ *   - Return value: FH_OK (0) or an FH_ERR_* code; fh_last_error() then holds
+ *     a message for the calling thread.  Nothing aborts the process.
+ *   - Thread-safe: the library holds no mutable global state apart from the
+ *     per-thread error string.
+ */
+#ifndef FEMTOHIP_H_
+#define FEMTOHIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FH_ABI_VERSION 1
+
+typedef enum fh_dtype {
+  FH_BF16 = 0, /* bfloat16 storage, fp32 arithmetic */
+  FH_F32 = 1   /* float32 storage and arithmetic     */
+} fh_dtype;
+
+enum {
+  FH_OK = 0,
+  FH_ERR_INVALID = 1,     /* bad shape / stride / alignment / dtype */
+  FH_ERR_LAUNCH = 2,      /* hipLaunchKernel (or a HIP call) failed  */
+  FH_ERR_UNSUPPORTED = 3  /* valid but not implemented configuration */
+};
+
+/* Library ABI version (FH_ABI_VERSION of the build). */
+int fh_abi_version(void);
+
+/* Message describing the last failing call on this thread ("" if none). */
+const char* fh_last_error(void);
+
+/* ------------------------------------------------------------------ RMSNorm
+ * Replaces LlamaRMSNorm.forward (modeling_llama.py:62-67):
+ *   y = w * to_dtype(x_f32 * rsqrt(mean(x_f32^2) + eps))
+ * x, y: [rows, cols]; w: [cols].  rstd (nullable): fp32 [rows] receives
+ * rsqrt(mean(x^2)+eps).  cols % 8 == 0, cols <= 8192, 16-byte aligned rows.
+ */
+int fh_rmsnorm_fwd(fh_dtype dt, const void* x, const void* w, void* y,
+                   float* rstd, int64_t rows, int64_t cols, float eps,
+                   hipStream_t stream);
+
+/* Residual add followed by RMSNorm: the `residual + hidden_states` at
+ * modeling_llama.py:317 feeding post_attention_layernorm (:320).
+ *   h = to_dtype(x + a);  y = rmsnorm(h) as above.
+ * h may alias neither x nor a.  rstd nullable.
+ */
+int fh_add_rmsnorm_fwd(fh_dtype dt, const void* x, const void* a,
+                       const void* w, void* h, void* y, float* rstd,
+                       int64_t rows, int64_t cols, float eps,
+                       hipStream_t stream);
+
+/* Bytes of fp32 workspace fh_rmsnorm_bwd needs for (rows, cols). */
+size_t fh_rmsnorm_bwd_workspace_size(int64_t rows, int64_t cols);
+
+/* Backward of LlamaRMSNorm (autograd of modeling_llama.py:62-67), fused with
+ * the residual-branch gradient of the add at modeling_llama.py:317/323:
+ *   dn  = to_dtype(dy * w)
+ *   dx  = to_dtype(r * (dn - n * mean(dn * n)) + dres)   (n = x*r, r = rstd)
+ *   dw  = sum_rows dy * to_dtype(n)
+ * rstd nullable (recomputed from x and eps); dres nullable (no residual).
+ * dw: [cols] in dtype dt, overwritten.  workspace: see above.
+ */
+int fh_rmsnorm_bwd(fh_dtype dt, const void* dy, const void* x, const void* w,
+                   const float* rstd, const void* dres, void* dx, void* dw,
+                   void* workspace, int64_t rows, int64_t cols, float eps,
+                   hipStream_t stream);
+
+/* --------------------------------------------------------------------- RoPE
+ * In-place rotate-half rotary embedding, replacing apply_rotary_pos_emb +
+ * rotate_half (modeling_llama.py:130-160) for q and k together:
+ *   out[i]      = x[i]*cos[i]      - x[i+d/2]*sin[i]
+ *   out[i+d/2]  = x[i+d/2]*cos[i+d/2] + x[i]*sin[i+d/2]        (i < d/2)
+ * with the same bf16 rounding points as the reference (each product, then
+ * the sum).  qk: [tokens, ld]; heads 0..n_heads-1 at columns h*head_dim.
+ * Token t is (batch t / seq_len, position t % seq_len).  cos/sin:
+ * [seq_len, head_dim] (cos_per_token == 0, i.e. shape [1,S,hd]) or
+ * [tokens, head_dim] (cos_per_token != 0, shape [B,S,hd]).
+ * head_dim % 16 == 0.
+ */
+int fh_rope_fwd(fh_dtype dt, void* qk, int64_t ld, int64_t tokens,
+                int64_t seq_len, int64_t n_heads, int64_t head_dim,
+                const void* cos, const void* sin, int cos_per_token,
+                hipStream_t stream);
+
+/* Backward of fh_rope_fwd (rotation by the transposed matrix), in place on
+ * the gradient buffer with the same layout arguments. */
+int fh_rope_bwd(fh_dtype dt, void* dqk, int64_t ld, int64_t tokens,
+                int64_t seq_len, int64_t n_heads, int64_t head_dim,
+                const void* cos, const void* sin, int cos_per_token,
+                hipStream_t stream);
+
+/* ------------------------------------------------------------------- SwiGLU
+ * Replaces `act_fn(gate_proj(x)) * up_proj(x)` (modeling_llama.py:174-176,
+ * act_fn = SiLU, activations.py:93-103):  p = to_dtype(to_dtype(silu(g)) * u)
+ * g, u: [rows, cols] with row stride ld_gu; p: row stride ld_p.
+ * cols % 8 == 0.
+ */
+int fh_swiglu_fwd(fh_dtype dt, const void* g, const void* u, int64_t ld_gu,
+                  void* p, int64_t ld_p, int64_t rows, int64_t cols,
+                  hipStream_t stream);
+
+/* Backward of fh_swiglu_fwd:
+ *   du = dp * to_dtype(silu(g))
+ *   dg = to_dtype(dp*u) * sig(g) * (1 + g*(1 - sig(g)))
+ * dg, du share row stride ld_dgu (they may be the two halves of one buffer).
+ */
+int fh_swiglu_bwd(fh_dtype dt, const void* dp, int64_t ld_dp, const void* g,
+                  const void* u, int64_t ld_gu, void* dg, void* du,
+                  int64_t ld_dgu, int64_t rows, int64_t cols,
+                  hipStream_t stream);
+
+/* Elementwise residual add out = to_dtype(a + b) over n elements
+ * (modeling_llama.py:323).  n % 8 == 0; out may alias a or b. */
+int fh_add(fh_dtype dt, const void* a, const void* b, void* out, int64_t n,
+           hipStream_t stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* FEMTOHIP_H_ */

@@ -1,0 +1,257 @@
+"""Parity of each femtohip memory-bound kernel with the oracle (GPU).
+
+The HIP kernels run on cuda:0 through the C ABI (femtotron_amd.ops); the
+checkers are oracle/torch_llama.py on the CPU (same bf16 rounding points as the
+reference, so RoPE and the adds are bit-exact) and the fp64 closed forms.
+Sizes: small ragged cases plus BASELINE config 2 (T=4096, H=4096, 32x128 RoPE
+heads, F=14336), where the CPU oracle still finishes in seconds.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import closed_form as cf
+from oracle import torch_llama as ot
+from tests.helpers import assert_close, randn
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+BF16_ULP = 2.0 ** -7  # one bf16 ulp relative to the value (8 significant bits)
+
+
+def _ops():
+    from femtotron_amd import ops
+    return ops
+
+
+def _dev(t):
+    return t.to(DEV)
+
+
+def _max_ulp_diff(a: torch.Tensor, b: torch.Tensor) -> int:
+    ai = a.detach().cpu().contiguous().view(torch.int16).to(torch.int32)
+    bi = b.detach().cpu().contiguous().view(torch.int16).to(torch.int32)
+    # same-sign values: integer distance of the bit patterns
+    return int((ai - bi).abs().max()) if ai.numel() else 0
+
+
+# ---------------------------------------------------------------- RMSNorm
+@pytest.mark.parametrize("rows,cols", [(7, 256), (64, 688), (33, 2048), (4096, 4096), (5, 8), (3, 8192)])
+def test_rmsnorm_fwd_bf16(rows, cols):
+    x = randn((rows, cols), 1).bfloat16()
+    w = (1 + randn((cols,), 2, 0.02)).bfloat16()
+    rstd = torch.empty(rows, dtype=torch.float32, device=DEV)
+    y = _ops().rmsnorm_fwd(_dev(x), _dev(w), 1e-5, rstd=rstd)
+    ref = ot.rmsnorm(x, w, 1e-5)
+    # identical rounding points; only the fp32 sum order differs, which can move
+    # the rounded normalised value by 1 ulp and the rounded product by 2
+    assert_close(y, ref, 2 * BF16_ULP, 1e-6, "y")
+    r_ref = torch.rsqrt(x.float().pow(2).mean(-1) + 1e-5)
+    assert_close(rstd, r_ref, 1e-5, 0, "rstd")
+
+
+@pytest.mark.parametrize("rows,cols", [(7, 256), (129, 2048)])
+def test_rmsnorm_fwd_fp32_closed_form(rows, cols):
+    x = randn((rows, cols), 3)
+    w = 1 + randn((cols,), 4, 0.02)
+    y = _ops().rmsnorm_fwd(_dev(x), _dev(w), 1e-5)
+    ref = cf.rmsnorm_fwd(x.double().numpy(), w.double().numpy(), 1e-5)
+    assert_close(y, torch.from_numpy(ref), 1e-5, 1e-6, "y fp32")
+
+
+@pytest.mark.parametrize("rows,cols", [(9, 256), (4096, 4096)])
+def test_add_rmsnorm_fwd_bf16(rows, cols):
+    x = randn((rows, cols), 5).bfloat16()
+    a = randn((rows, cols), 6).bfloat16()
+    w = (1 + randn((cols,), 7, 0.02)).bfloat16()
+    h, y = _ops().add_rmsnorm_fwd(_dev(x), _dev(a), _dev(w), 1e-5)
+    assert torch.equal(h.cpu(), x + a)  # bf16 add: bit-exact
+    assert_close(y, ot.rmsnorm(x + a, w, 1e-5), 2 * BF16_ULP, 1e-6, "y")
+
+
+@pytest.mark.parametrize("rows,cols,res,with_rstd", [(7, 256, False, False), (33, 688, True, True),
+                                                     (4096, 4096, True, False), (2000, 2048, False, True),
+                                                     (1, 8, True, False)])
+def test_rmsnorm_bwd_bf16(rows, cols, res, with_rstd):
+    x = randn((rows, cols), 8).bfloat16()
+    w = (1 + randn((cols,), 9, 0.02)).bfloat16()
+    dy = randn((rows, cols), 10).bfloat16()
+    dres = randn((rows, cols), 11).bfloat16() if res else None
+    ops = _ops()
+    rstd = None
+    if with_rstd:
+        rstd = torch.empty(rows, dtype=torch.float32, device=DEV)
+        ops.rmsnorm_fwd(_dev(x), _dev(w), 1e-5, rstd=rstd)
+    dx, dw = ops.rmsnorm_bwd(_dev(dy), _dev(x), _dev(w), 1e-5, rstd=rstd,
+                             dres=None if dres is None else _dev(dres))
+    # checker: oracle autograd in fp32 on the same bf16 values (exact math)
+    xf = x.float().requires_grad_(True)
+    wf = w.float().requires_grad_(True)
+    ot.rmsnorm(xf, wf, 1e-5).backward(dy.float())
+    dx_ref = xf.grad + (dres.float() if res else 0)
+    # The reference rounds dy*w (and, with a residual, the norm-branch gradient)
+    # to bf16 before the final sum, so the deviation is bounded by a few ulps of
+    # the summands, not of their (possibly cancelling) sum.
+    terms = xf.grad.abs() + (dres.float().abs() if res else 0)
+    err = (dx.float().cpu() - dx_ref).abs()
+    bound = 2e-3 + 2e-2 * dx_ref.abs() + 4 * BF16_ULP * terms
+    assert bool((err <= bound).all()), f"dx: max excess {(err - bound).max():.3e}"
+    # dw sums dy * bf16(n) over rows (the reference rounds n to bf16 before the
+    # weight multiply); against the exact fp32 value that rounding contributes
+    # independent errors of ~1e-3 per row, hence an atol growing as sqrt(rows).
+    assert_close(dw, wf.grad, 2e-2, 5e-3 * max(1.0, rows ** 0.5), "dw")
+    # closed form in fp64 agrees with the same checker (guards the checker itself)
+    cdx, cdw = cf.rmsnorm_bwd(dy.double().numpy(), x.double().numpy(), w.double().numpy(), 1e-5)
+    assert np.allclose(cdx + (dres.double().numpy() if res else 0), dx_ref.double().numpy(), atol=1e-4)
+
+
+def test_rmsnorm_bwd_dw_exact_when_n_is_representable():
+    """x in {-1, +1} and eps = 0 make r = 1 and n = x exactly, so bf16(n) = n and
+    dw must equal the fp64 sum_rows dy*x up to the final bf16 rounding."""
+    rows, cols = 3000, 2048
+    x = torch.where(randn((rows, cols), 50) > 0, 1.0, -1.0).bfloat16()
+    dy = randn((rows, cols), 51).bfloat16()
+    w = (1 + randn((cols,), 52, 0.02)).bfloat16()
+    dx, dw = _ops().rmsnorm_bwd(_dev(dy), _dev(x), _dev(w), 0.0)
+    ref = (dy.double() * x.double()).sum(0)
+    assert_close(dw, ref, 2 * BF16_ULP, 1e-6, "dw exact")
+    cdx, _ = cf.rmsnorm_bwd(dy.double().numpy(), x.double().numpy(), w.double().numpy(), 0.0)
+    assert_close(dx, torch.from_numpy(cdx), 2e-2, 2e-3, "dx")
+
+
+def test_rmsnorm_bwd_fp32_closed_form():
+    rows, cols = 100, 256
+    x, dy = randn((rows, cols), 12), randn((rows, cols), 13)
+    w = 1 + randn((cols,), 14, 0.1)
+    dx, dw = _ops().rmsnorm_bwd(_dev(dy), _dev(x), _dev(w), 1e-5)
+    cdx, cdw = cf.rmsnorm_bwd(dy.double().numpy(), x.double().numpy(), w.double().numpy(), 1e-5)
+    assert_close(dx, torch.from_numpy(cdx), 1e-5, 1e-5, "dx")
+    assert_close(dw, torch.from_numpy(cdw), 1e-5, 1e-4, "dw")
+
+
+def test_rmsnorm_bwd_empty_and_deterministic():
+    ops = _ops()
+    x = torch.empty(0, 256, dtype=torch.bfloat16, device=DEV)
+    w = torch.ones(256, dtype=torch.bfloat16, device=DEV)
+    dx, dw = ops.rmsnorm_bwd(x, x, w, 1e-5)
+    assert dx.shape == (0, 256) and torch.count_nonzero(dw) == 0
+    xb = _dev(randn((3000, 2048), 15).bfloat16())
+    dyb = _dev(randn((3000, 2048), 16).bfloat16())
+    wb = _dev((1 + randn((2048,), 17, 0.02)).bfloat16())
+    a = ops.rmsnorm_bwd(dyb, xb, wb, 1e-5)
+    b = ops.rmsnorm_bwd(dyb, xb, wb, 1e-5)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])  # run-to-run bitwise
+
+
+# --------------------------------------------------------------------- RoPE
+@pytest.mark.parametrize("B,S,nh,nkv,hd,theta", [(2, 128, 8, 4, 32, 1e4), (1, 4096, 32, 0, 128, 5e5),
+                                                 (2, 64, 32, 4, 64, 1e4), (1, 33, 4, 4, 16, 1e4)])
+def test_rope_fwd_bwd_bit_exact(B, S, nh, nkv, hd, theta):
+    ops = _ops()
+    T = B * S
+    width = (nh + 2 * nkv) * hd  # q | k | v columns, like the qkv buffer
+    buf = randn((T, width), 20).bfloat16()
+    cos, sin = ot.rope_cos_sin(S, hd, theta, torch.bfloat16)
+    g = _dev(buf.clone())
+    ops.rope_fwd_(g, nh + nkv, hd, S, _dev(cos), _dev(sin))
+    q = buf[:, :nh * hd].reshape(B, S, nh, hd).transpose(1, 2)
+    if nkv:
+        k = buf[:, nh * hd:(nh + nkv) * hd].reshape(B, S, nkv, hd).transpose(1, 2)
+    else:
+        k = q[:, :0]
+    qr, kr = ot.rope(q, k, cos, sin)
+    ref = buf.clone()
+    ref[:, :nh * hd] = qr.transpose(1, 2).reshape(T, nh * hd)
+    if nkv:
+        ref[:, nh * hd:(nh + nkv) * hd] = kr.transpose(1, 2).reshape(T, nkv * hd)
+    assert torch.equal(g.cpu(), ref), "rope fwd differs from the reference rounding"
+    # backward: autograd of the oracle rope in bf16
+    dq = randn(q.shape, 21).bfloat16()
+    qq = q.clone().requires_grad_(True)
+    ot.rope(qq, qq[:, :0], cos, sin)[0].backward(dq)
+    gb = torch.zeros(T, width, dtype=torch.bfloat16)
+    gb[:, :nh * hd] = dq.transpose(1, 2).reshape(T, nh * hd)
+    gd = _dev(gb)
+    ops.rope_bwd_(gd, nh, hd, S, _dev(cos), _dev(sin))
+    assert torch.equal(gd.cpu()[:, :nh * hd], qq.grad.transpose(1, 2).reshape(T, nh * hd))
+
+
+def test_rope_per_token_cos_and_roundtrip_full_size():
+    ops = _ops()
+    B, S, nh, hd = 2, 256, 8, 64
+    T = B * S
+    x = randn((T, nh * hd), 22).bfloat16()
+    cos1, sin1 = ot.rope_cos_sin(S, hd, 1e4, torch.bfloat16)
+    cosb, sinb = cos1.expand(B, S, hd).contiguous(), sin1.expand(B, S, hd).contiguous()
+    a, b = _dev(x.clone()), _dev(x.clone())
+    ops.rope_fwd_(a, nh, hd, S, _dev(cos1), _dev(sin1))
+    ops.rope_fwd_(b, nh, hd, S, _dev(cosb), _dev(sinb))
+    assert torch.equal(a, b)
+    # fp32 round trip (rotation then its transpose) is the identity
+    xf = _dev(randn((T, nh * hd), 23))
+    c32, s32 = ot.rope_cos_sin(S, hd, 1e4, torch.float32)
+    y = xf.clone()
+    ops.rope_fwd_(y, nh, hd, S, _dev(c32), _dev(s32))
+    ops.rope_bwd_(y, nh, hd, S, _dev(c32), _dev(s32))
+    assert_close(y, xf, 1e-5, 1e-5, "roundtrip")
+
+
+# ------------------------------------------------------------------- SwiGLU
+@pytest.mark.parametrize("rows,cols", [(256, 688), (4096, 14336), (3, 8)])
+def test_swiglu_fwd_bwd_bf16(rows, cols):
+    ops = _ops()
+    gu = randn((rows, 2 * cols), 30).bfloat16()
+    g, u = gu[:, :cols], gu[:, cols:]
+    dgu = _dev(gu)
+    p = ops.swiglu_fwd(dgu[:, :cols], dgu[:, cols:])
+    ref = torch.nn.functional.silu(g) * u
+    assert_close(p, ref, BF16_ULP, 1e-6, "p")
+    dp = randn((rows, cols), 31).bfloat16()
+    out = torch.empty_like(dgu)
+    ops.swiglu_bwd(_dev(dp), dgu[:, :cols], dgu[:, cols:], out[:, :cols], out[:, cols:])
+    gg = g.float().requires_grad_(True)
+    uu = u.float().requires_grad_(True)
+    (torch.nn.functional.silu(gg) * uu).backward(dp.float())
+    assert_close(out[:, :cols], gg.grad, 2e-2, 2e-3, "dg")
+    assert_close(out[:, cols:], uu.grad, 2e-2, 2e-3, "du")
+
+
+def test_swiglu_fp32_closed_form():
+    ops = _ops()
+    g, u, dp = randn((64, 64), 32), randn((64, 64), 33), randn((64, 64), 34)
+    p = ops.swiglu_fwd(_dev(g), _dev(u))
+    assert_close(p, torch.from_numpy(cf.swiglu_fwd(g.double().numpy(), u.double().numpy())), 1e-5, 1e-6, "p")
+    dg, du = torch.empty_like(_dev(g)), torch.empty_like(_dev(g))
+    ops.swiglu_bwd(_dev(dp), _dev(g), _dev(u), dg, du)
+    cdg, cdu = cf.swiglu_bwd(dp.double().numpy(), g.double().numpy(), u.double().numpy())
+    assert_close(dg, torch.from_numpy(cdg), 1e-5, 1e-6, "dg")
+    assert_close(du, torch.from_numpy(cdu), 1e-5, 1e-6, "du")
+
+
+def test_add_bit_exact_and_in_place():
+    ops = _ops()
+    a, b = randn((1000, 64), 40).bfloat16(), randn((1000, 64), 41).bfloat16()
+    da, db = _dev(a), _dev(b)
+    assert torch.equal(ops.add(da, db).cpu(), a + b)
+    ops.add(da, db, out=db)
+    assert torch.equal(db.cpu(), a + b)
+
+
+# ------------------------------------------------------------- error paths
+def test_invalid_arguments_raise():
+    from femtotron_amd._lib import FemtoHipError
+    ops = _ops()
+    x = torch.zeros(4, 12, dtype=torch.bfloat16, device=DEV)  # cols % 8 != 0
+    with pytest.raises(FemtoHipError, match="multiple of 8"):
+        ops.rmsnorm_fwd(x, torch.ones(12, dtype=torch.bfloat16, device=DEV), 1e-5)
+    with pytest.raises(TypeError):
+        ops.rmsnorm_fwd(x.half(), torch.ones(12, dtype=torch.half, device=DEV), 1e-5)
+    with pytest.raises(ValueError):
+        ops.rmsnorm_fwd(x.cpu(), torch.ones(12, dtype=torch.bfloat16), 1e-5)
+    q = torch.zeros(4, 48, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(FemtoHipError, match="head_dim"):
+        ops.rope_fwd_(q, 2, 24, 4, torch.zeros(1, 4, 24, dtype=torch.bfloat16, device=DEV),
+                      torch.zeros(1, 4, 24, dtype=torch.bfloat16, device=DEV))
