@@ -1,0 +1,689 @@
+// Causal GQA flash attention, forward and backward, for gfx950.
+//
+// Replaces F.scaled_dot_product_attention(q, k, v, is_causal=True,
+// enable_gqa=True, scale=head_dim^-0.5) as called by sdpa_attention_forward
+// (transformers 5.15.0 integrations/sdpa_attention.py:79-166) from
+// LlamaAttention.forward (models/llama/modeling_llama.py:235-281), and its
+// autograd backward.  Query head h reads kv head h / (n_heads / n_kv_heads)
+// (repeat_kv, modeling_llama.py:179-188).
+//
+// Layout: token-major.  Row t = b*S + s of q/k/v/o holds all heads of one
+// token (head h at columns h*HD..h*HD+HD-1), so q, k, v are column ranges of
+// the layer's fused [T, Hq+2Hkv] projection output and o feeds the o_proj GEMM
+// directly; no transposes ever touch HBM.
+//
+// bf16 kernels use v_mfma_f32_32x32x16_bf16.  Lane i of an MFMA operand holds
+// row/col i%32 and K-slice 8*(i/32)..+7; lane i of the fp32 accumulator holds
+// column i%32 and rows 8*(j/4) + 4*(i/32) + j%4, j = 0..15.  The softmax is
+// formed on S^T (keys x queries) so each lane owns one query: row max / sum are
+// in-lane plus one exchange with lane i^32, rescaling the output is a per-lane
+// scalar, and P^T feeds the next MFMA straight from registers.  That P operand
+// carries its K index (the key) in the permuted order {4h..4h+3, 8+4h..8+4h+3}
+// (h = i/32) of the accumulator layout; the matching operand is fetched with
+// two ds_read_b64_tr_b16 transpose reads in exactly that order, so tiles stay in
+// natural row-major layout in LDS.
+#include <math.h>
+
+#include "fh_common.hpp"
+
+namespace fh {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) z[j] = 0.f;
+  return z;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ bf16x8 ld_frag(const uint16_t* p) {
+  return as_bf16x8(*reinterpret_cast<const uint4*>(p));
+}
+
+// Operand whose K index runs down the rows of a row-major LDS tile X (stride
+// ld): lane i gets X[row0 + {4h+0..3, 8+4h+0..3}][col0 + i%32], h = i/32.
+__device__ __forceinline__ bf16x8 ld_frag_tr(const uint16_t* X, int ld, int row0, int col0,
+                                             int lane) {
+  const int hl = lane >> 5, L = lane & 15, mh = (lane >> 4) & 1;
+  const uint16_t* p0 = X + (row0 + 4 * hl + (L >> 2)) * ld + col0 + 16 * mh + 4 * (L & 3);
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0 + 8 * ld));
+  uint4 r;
+  r.x = static_cast<uint16_t>(a[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(a[1])) << 16);
+  r.y = static_cast<uint16_t>(a[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(a[3])) << 16);
+  r.z = static_cast<uint16_t>(b[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(b[1])) << 16);
+  r.w = static_cast<uint16_t>(b[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(b[3])) << 16);
+  return as_bf16x8(r);
+}
+
+// Accumulator entries j0..j0+7 rounded to bf16 as an MFMA operand.
+__device__ __forceinline__ bf16x8 pack_frag(const f32x16& acc, int j0) {
+  uint4 r;
+  r.x = f2bf(acc[j0 + 0]) | (static_cast<uint32_t>(f2bf(acc[j0 + 1])) << 16);
+  r.y = f2bf(acc[j0 + 2]) | (static_cast<uint32_t>(f2bf(acc[j0 + 3])) << 16);
+  r.z = f2bf(acc[j0 + 4]) | (static_cast<uint32_t>(f2bf(acc[j0 + 5])) << 16);
+  r.w = f2bf(acc[j0 + 6]) | (static_cast<uint32_t>(f2bf(acc[j0 + 7])) << 16);
+  return as_bf16x8(r);
+}
+
+// Row (M index) of accumulator entry j for lane half hl.
+__device__ __forceinline__ int acc_row(int j, int hl) { return 8 * (j >> 2) + 4 * hl + (j & 3); }
+
+// Cooperative copy of `rows` rows x HD columns (bf16) from a token-major
+// source (row stride ld) into an LDS tile with row stride LDST; rows at or
+// beyond `valid` are zero-filled.  16-byte chunks, consecutive threads on
+// consecutive chunks of a row.
+template <int HD, int LDST>
+__device__ __forceinline__ void copy_tile(uint16_t* dst, const uint16_t* src, int64_t ld, int rows,
+                                          int valid, int tid, int nthreads) {
+  constexpr int CPR = HD / 8;
+  for (int c = tid; c < rows * CPR; c += nthreads) {
+    const int r = c / CPR, col = (c - r * CPR) * 8;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (r < valid) v = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(r) * ld + col);
+    *reinterpret_cast<uint4*>(dst + r * LDST + col) = v;
+  }
+}
+
+// Stores a transposed accumulator tile (rows = head dims d, column = this
+// lane's token) scaled by `mul` into row `row` of a token-major output.
+template <int HD>
+__device__ __forceinline__ void store_rows_T(uint16_t* out_row, const f32x16 (&acc)[HD / 32],
+                                             float mul, int hl) {
+#pragma unroll
+  for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint2 w;
+      w.x = f2bf(acc[dt][4 * g] * mul) | (static_cast<uint32_t>(f2bf(acc[dt][4 * g + 1] * mul)) << 16);
+      w.y = f2bf(acc[dt][4 * g + 2] * mul) | (static_cast<uint32_t>(f2bf(acc[dt][4 * g + 3] * mul)) << 16);
+      *reinterpret_cast<uint2*>(out_row + dt * 32 + 8 * g + 4 * hl) = w;
+    }
+}
+
+// ------------------------------------------------------------ forward (bf16)
+// Block = 4 waves x 32 queries of one (batch, head); loop over 64-key blocks.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_fwd(
+    const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
+    const uint16_t* __restrict__ v, int64_t ldv, uint16_t* __restrict__ o, int64_t ldo,
+    float* __restrict__ lse, int S, int nh, int group, float scale_log2) {
+  constexpr int BM = 128, BN = 64, LDST = HD + 8, NS = HD / 16, ND = HD / 32;
+  __shared__ __align__(16) uint16_t sk[BN * LDST];
+  __shared__ __align__(16) uint16_t sv[BN * LDST];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hl = lane >> 5, l32 = lane & 31;
+  const int bh = blockIdx.y, b = bh / nh, h = bh - b * nh, kvh = h / group;
+  const int q0 = (gridDim.x - 1 - blockIdx.x) * BM;  // heaviest (latest) query blocks first
+  const int qw = q0 + wave * 32, qi = qw + l32;
+  const int64_t tok0 = static_cast<int64_t>(b) * S;
+
+  bf16x8 qf[NS];
+  {
+    const uint16_t* qrow = q + (tok0 + qi) * ldq + static_cast<int64_t>(h) * HD + 8 * hl;
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      qf[s] = qi < S ? ld_frag(qrow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
+  }
+  f32x16 oacc[ND];
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt) oacc[dt] = zero16();
+  float m = -INFINITY, l = 0.f;
+
+  const int kend = min(S, q0 + BM);
+  const int nkb = (kend + BN - 1) / BN;
+  const uint16_t* kb_ptr = k + tok0 * ldk + static_cast<int64_t>(kvh) * HD;
+  const uint16_t* vb_ptr = v + tok0 * ldv + static_cast<int64_t>(kvh) * HD;
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int k0 = kb * BN;
+    __syncthreads();
+    copy_tile<HD, LDST>(sk, kb_ptr + static_cast<int64_t>(k0) * ldk, ldk, BN, S - k0, tid, 256);
+    copy_tile<HD, LDST>(sv, vb_ptr + static_cast<int64_t>(k0) * ldv, ldv, BN, S - k0, tid, 256);
+    __syncthreads();
+    if (k0 > qw + 31) continue;  // the whole block lies after this wave's last query
+
+    f32x16 sacc[BN / 32];
+#pragma unroll
+    for (int t = 0; t < BN / 32; ++t) {
+      sacc[t] = zero16();
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+        sacc[t] = mfma(ld_frag(sk + (32 * t + l32) * LDST + 16 * s + 8 * hl), qf[s], sacc[t]);
+    }
+    const bool need_mask = (k0 + BN - 1 > qw) || (k0 + BN > S);
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < BN / 32; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float x = sacc[t][j] * scale_log2;
+        if (need_mask) {
+          const int key = k0 + 32 * t + acc_row(j, hl);
+          if (key > qi || key >= S) x = -INFINITY;
+        }
+        sacc[t][j] = x;
+        mloc = fmaxf(mloc, x);
+      }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    const float mnew = fmaxf(m, mloc);  // finite: key 0 is visible to every query
+    const float alpha = exp2f(m - mnew);
+    m = mnew;
+    float lsum = 0.f;
+#pragma unroll
+    for (int t = 0; t < BN / 32; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float p = exp2f(sacc[t][j] - mnew);
+        sacc[t][j] = p;
+        lsum += p;
+      }
+    l = l * alpha + lsum;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
+#pragma unroll
+    for (int s = 0; s < BN / 16; ++s) {
+      const bf16x8 pf = pack_frag(sacc[s >> 1], 8 * (s & 1));
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt)
+        oacc[dt] = mfma(ld_frag_tr(sv, LDST, 16 * s, 32 * dt, lane), pf, oacc[dt]);
+    }
+  }
+  l += __shfl_xor(l, 32, 64);
+  if (qi < S) {
+    store_rows_T<HD>(o + (tok0 + qi) * ldo + static_cast<int64_t>(h) * HD, oacc, 1.f / l, hl);
+    if (lse != nullptr && hl == 0) lse[static_cast<int64_t>(bh) * S + qi] = (m + log2f(l)) * kLn2;
+  }
+}
+
+// --------------------------------------------- backward: delta = rowsum(dO*O)
+template <typename T>
+__global__ __launch_bounds__(256) void k_attn_delta(const T* __restrict__ o, int64_t ldo,
+                                                    const T* __restrict__ dO, int64_t lddo,
+                                                    float* __restrict__ delta, int S, int nh,
+                                                    int hd, int64_t tokens) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= tokens * nh) return;
+  const int64_t t = idx / nh;
+  const int h = static_cast<int>(idx - t * nh);
+  const T* orow = o + t * ldo + static_cast<int64_t>(h) * hd;
+  const T* grow = dO + t * lddo + static_cast<int64_t>(h) * hd;
+  float acc = 0.f;
+  for (int d = 0; d < hd; d += 8) {
+    float a[8], g[8];
+    Elem<T>::load8(orow + d, a);
+    Elem<T>::load8(grow + d, g);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc = fmaf(a[j], g[j], acc);
+  }
+  const int64_t b = t / S;
+  const int s = static_cast<int>(t - b * S);
+  delta[(b * nh + h) * S + s] = acc;
+}
+
+// ------------------------------------------------------- backward: dQ (bf16)
+// Same tiling as the forward: block = 128 queries of one (batch, head).
+//   S^T = K Q^T, P^T = exp(S^T - lse), dP^T = V dO^T,
+//   dS^T = P^T (dP^T - delta), dQ^T += K^T dS^T, dQ = scale * dQ.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_bwd_dq(
+    const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
+    const uint16_t* __restrict__ v, int64_t ldv, const uint16_t* __restrict__ dO, int64_t lddo,
+    const float* __restrict__ lse, const float* __restrict__ delta, uint16_t* __restrict__ dq,
+    int64_t lddq, int S, int nh, int group, float scale_log2, float scale) {
+  constexpr int BM = 128, BN = 64, LDST = HD + 8, NS = HD / 16, ND = HD / 32;
+  __shared__ __align__(16) uint16_t sk[BN * LDST];
+  __shared__ __align__(16) uint16_t sv[BN * LDST];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hl = lane >> 5, l32 = lane & 31;
+  const int bh = blockIdx.y, b = bh / nh, h = bh - b * nh, kvh = h / group;
+  const int q0 = (gridDim.x - 1 - blockIdx.x) * BM;
+  const int qw = q0 + wave * 32, qi = qw + l32;
+  const int64_t tok0 = static_cast<int64_t>(b) * S;
+
+  bf16x8 qf[NS], gf[NS];
+  float lse2 = 0.f, dl = 0.f;
+  {
+    const uint16_t* qrow = q + (tok0 + qi) * ldq + static_cast<int64_t>(h) * HD + 8 * hl;
+    const uint16_t* grow = dO + (tok0 + qi) * lddo + static_cast<int64_t>(h) * HD + 8 * hl;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      qf[s] = qi < S ? ld_frag(qrow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
+      gf[s] = qi < S ? ld_frag(grow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
+    }
+    if (qi < S) {
+      lse2 = lse[static_cast<int64_t>(bh) * S + qi] * kLog2e;
+      dl = delta[static_cast<int64_t>(bh) * S + qi];
+    }
+  }
+  f32x16 dqacc[ND];
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt) dqacc[dt] = zero16();
+
+  const int kend = min(S, q0 + BM);
+  const int nkb = (kend + BN - 1) / BN;
+  const uint16_t* kb_ptr = k + tok0 * ldk + static_cast<int64_t>(kvh) * HD;
+  const uint16_t* vb_ptr = v + tok0 * ldv + static_cast<int64_t>(kvh) * HD;
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int k0 = kb * BN;
+    __syncthreads();
+    copy_tile<HD, LDST>(sk, kb_ptr + static_cast<int64_t>(k0) * ldk, ldk, BN, S - k0, tid, 256);
+    copy_tile<HD, LDST>(sv, vb_ptr + static_cast<int64_t>(k0) * ldv, ldv, BN, S - k0, tid, 256);
+    __syncthreads();
+    if (k0 > qw + 31) continue;
+
+    f32x16 sacc[BN / 32], pacc[BN / 32];
+#pragma unroll
+    for (int t = 0; t < BN / 32; ++t) {
+      sacc[t] = zero16();
+      pacc[t] = zero16();
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        sacc[t] = mfma(ld_frag(sk + (32 * t + l32) * LDST + 16 * s + 8 * hl), qf[s], sacc[t]);
+        pacc[t] = mfma(ld_frag(sv + (32 * t + l32) * LDST + 16 * s + 8 * hl), gf[s], pacc[t]);
+      }
+    }
+    const bool need_mask = (k0 + BN - 1 > qw) || (k0 + BN > S);
+#pragma unroll
+    for (int t = 0; t < BN / 32; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float p = exp2f(sacc[t][j] * scale_log2 - lse2);
+        if (need_mask) {
+          const int key = k0 + 32 * t + acc_row(j, hl);
+          if (key > qi || key >= S) p = 0.f;
+        }
+        sacc[t][j] = p * (pacc[t][j] - dl);  // dS^T
+      }
+#pragma unroll
+    for (int s = 0; s < BN / 16; ++s) {
+      const bf16x8 df = pack_frag(sacc[s >> 1], 8 * (s & 1));
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt)
+        dqacc[dt] = mfma(ld_frag_tr(sk, LDST, 16 * s, 32 * dt, lane), df, dqacc[dt]);
+    }
+  }
+  if (qi < S) store_rows_T<HD>(dq + (tok0 + qi) * lddq + static_cast<int64_t>(h) * HD, dqacc, scale, hl);
+}
+
+// ---------------------------------------------------- backward: dK, dV (bf16)
+// Block = 4 waves x 32 keys of one (batch, kv head); K and V of the wave's keys
+// stay in registers.  Loop over the query heads of the group and over query
+// tiles of BQ at or after the block's first key:
+//   S = Q K^T, P = exp(S - lse), dP = dO V^T, dS = P (dP - delta),
+//   dV^T += dO^T P,  dK^T += Q^T dS,  dK = scale * dK.
+// Every kv head's gradient is complete inside one block: no atomics.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_bwd_dkdv(
+    const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
+    const uint16_t* __restrict__ v, int64_t ldv, const uint16_t* __restrict__ dO, int64_t lddo,
+    const float* __restrict__ lse, const float* __restrict__ delta, uint16_t* __restrict__ dk,
+    int64_t lddk, uint16_t* __restrict__ dv, int64_t lddv, int S, int nh, int nkv, int group,
+    float scale_log2, float scale) {
+  constexpr int BKN = 128, BQ = (HD >= 128 ? 32 : 64), LDST = HD + 8, NS = HD / 16, ND = HD / 32;
+  constexpr int NQT = BQ / 32;
+  __shared__ __align__(16) uint16_t sq[BQ * LDST];
+  __shared__ __align__(16) uint16_t sg[BQ * LDST];
+  __shared__ __align__(16) float slse[BQ];
+  __shared__ __align__(16) float sdl[BQ];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hl = lane >> 5, l32 = lane & 31;
+  const int bk = blockIdx.y, b = bk / nkv, kvh = bk - b * nkv;
+  const int kblk0 = blockIdx.x * BKN;  // key block 0 has the most work; launched first
+  const int kw = kblk0 + wave * 32, ki = kw + l32;
+  const int64_t tok0 = static_cast<int64_t>(b) * S;
+
+  bf16x8 kf[NS], vf[NS];
+  {
+    const uint16_t* krow = k + (tok0 + ki) * ldk + static_cast<int64_t>(kvh) * HD + 8 * hl;
+    const uint16_t* vrow = v + (tok0 + ki) * ldv + static_cast<int64_t>(kvh) * HD + 8 * hl;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      kf[s] = ki < S ? ld_frag(krow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
+      vf[s] = ki < S ? ld_frag(vrow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
+    }
+  }
+  f32x16 dkacc[ND], dvacc[ND];
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt) {
+    dkacc[dt] = zero16();
+    dvacc[dt] = zero16();
+  }
+
+  const int qt_begin = kblk0 / BQ;
+  const int nqt = (S + BQ - 1) / BQ;
+  for (int hh = 0; hh < group; ++hh) {
+    const int h = kvh * group + hh;
+    const int64_t row_lse = (static_cast<int64_t>(b) * nh + h) * S;
+    const uint16_t* qh = q + tok0 * ldq + static_cast<int64_t>(h) * HD;
+    const uint16_t* gh = dO + tok0 * lddo + static_cast<int64_t>(h) * HD;
+    for (int qt = qt_begin; qt < nqt; ++qt) {
+      const int q0 = qt * BQ;
+      __syncthreads();
+      copy_tile<HD, LDST>(sq, qh + static_cast<int64_t>(q0) * ldq, ldq, BQ, S - q0, tid, 256);
+      copy_tile<HD, LDST>(sg, gh + static_cast<int64_t>(q0) * lddo, lddo, BQ, S - q0, tid, 256);
+      if (tid < BQ) {
+        const bool ok = q0 + tid < S;
+        slse[tid] = ok ? lse[row_lse + q0 + tid] * kLog2e : 0.f;
+        sdl[tid] = ok ? delta[row_lse + q0 + tid] : 0.f;
+      }
+      __syncthreads();
+      if (q0 + BQ - 1 < kw) continue;  // every query precedes this wave's first key
+
+      const bool need_mask = (q0 < kw + 31) || (q0 + BQ > S) || (kw + 32 > S);
+#pragma unroll
+      for (int u = 0; u < NQT; ++u) {
+        f32x16 sacc = zero16(), pacc = zero16();
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          sacc = mfma(ld_frag(sq + (32 * u + l32) * LDST + 16 * s + 8 * hl), kf[s], sacc);
+          pacc = mfma(ld_frag(sg + (32 * u + l32) * LDST + 16 * s + 8 * hl), vf[s], pacc);
+        }
+        // lane holds rows q = 32u + acc_row(j, hl) of column key ki
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 L4 = *reinterpret_cast<const float4*>(slse + 32 * u + 8 * g + 4 * hl);
+          const float4 D4 = *reinterpret_cast<const float4*>(sdl + 32 * u + 8 * g + 4 * hl);
+          const float Lv[4] = {L4.x, L4.y, L4.z, L4.w};
+          const float Dv[4] = {D4.x, D4.y, D4.z, D4.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int j = 4 * g + e;
+            float p = exp2f(sacc[j] * scale_log2 - Lv[e]);
+            if (need_mask) {
+              const int qa = q0 + 32 * u + 8 * g + 4 * hl + e;
+              if (ki > qa || qa >= S || ki >= S) p = 0.f;
+            }
+            sacc[j] = p;                     // P
+            pacc[j] = p * (pacc[j] - Dv[e]);  // dS
+          }
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const bf16x8 pf = pack_frag(sacc, 8 * s2);
+          const bf16x8 df = pack_frag(pacc, 8 * s2);
+#pragma unroll
+          for (int dt = 0; dt < ND; ++dt) {
+            dvacc[dt] = mfma(ld_frag_tr(sg, LDST, 32 * u + 16 * s2, 32 * dt, lane), pf, dvacc[dt]);
+            dkacc[dt] = mfma(ld_frag_tr(sq, LDST, 32 * u + 16 * s2, 32 * dt, lane), df, dkacc[dt]);
+          }
+        }
+      }
+    }
+  }
+  if (ki < S) {
+    store_rows_T<HD>(dk + (tok0 + ki) * lddk + static_cast<int64_t>(kvh) * HD, dkacc, scale, hl);
+    store_rows_T<HD>(dv + (tok0 + ki) * lddv + static_cast<int64_t>(kvh) * HD, dvacc, 1.f, hl);
+  }
+}
+
+// --------------------------------------------------------- fp32 reference-precision kernels
+// Plain fp32 FMA kernels (one thread per output row) for fp32 models; the same
+// algorithm (online softmax forward with lse, delta-based backward) as above.
+template <int HD>
+__global__ __launch_bounds__(128) void k_attn_fwd_f32(
+    const float* __restrict__ q, int64_t ldq, const float* __restrict__ k, int64_t ldk,
+    const float* __restrict__ v, int64_t ldv, float* __restrict__ o, int64_t ldo,
+    float* __restrict__ lse, int S, int nh, int group, float scale, int64_t rows) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= rows) return;  // rows = B*nh*S, idx = (b*nh + h)*S + s
+  const int s = static_cast<int>(idx % S);
+  const int64_t bh = idx / S;
+  const int h = static_cast<int>(bh % nh);
+  const int64_t b = bh / nh;
+  const int kvh = h / group;
+  const float* qr = q + (b * S + s) * ldq + static_cast<int64_t>(h) * HD;
+  float qv[HD], acc[HD];
+  for (int d = 0; d < HD; ++d) { qv[d] = qr[d]; acc[d] = 0.f; }
+  float m = -INFINITY, l = 0.f;
+  for (int j = 0; j <= s; ++j) {
+    const float* kr = k + (b * S + j) * ldk + static_cast<int64_t>(kvh) * HD;
+    const float* vr = v + (b * S + j) * ldv + static_cast<int64_t>(kvh) * HD;
+    float x = 0.f;
+    for (int d = 0; d < HD; ++d) x = fmaf(qv[d], kr[d], x);
+    x *= scale;
+    const float mn = fmaxf(m, x);
+    const float a = expf(m - mn), p = expf(x - mn);
+    l = l * a + p;
+    for (int d = 0; d < HD; ++d) acc[d] = acc[d] * a + p * vr[d];
+    m = mn;
+  }
+  float* orow = o + (b * S + s) * ldo + static_cast<int64_t>(h) * HD;
+  for (int d = 0; d < HD; ++d) orow[d] = acc[d] / l;
+  if (lse != nullptr) lse[idx] = m + logf(l);
+}
+
+template <int HD>
+__global__ __launch_bounds__(128) void k_attn_bwd_dq_f32(
+    const float* __restrict__ q, int64_t ldq, const float* __restrict__ k, int64_t ldk,
+    const float* __restrict__ v, int64_t ldv, const float* __restrict__ dO, int64_t lddo,
+    const float* __restrict__ lse, const float* __restrict__ delta, float* __restrict__ dq,
+    int64_t lddq, int S, int nh, int group, float scale, int64_t rows) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= rows) return;
+  const int s = static_cast<int>(idx % S);
+  const int64_t bh = idx / S;
+  const int h = static_cast<int>(bh % nh);
+  const int64_t b = bh / nh;
+  const int kvh = h / group;
+  const float* qr = q + (b * S + s) * ldq + static_cast<int64_t>(h) * HD;
+  const float* gr = dO + (b * S + s) * lddo + static_cast<int64_t>(h) * HD;
+  float qv[HD], gv[HD], acc[HD];
+  for (int d = 0; d < HD; ++d) { qv[d] = qr[d]; gv[d] = gr[d]; acc[d] = 0.f; }
+  const float L = lse[idx], D = delta[idx];
+  for (int j = 0; j <= s; ++j) {
+    const float* kr = k + (b * S + j) * ldk + static_cast<int64_t>(kvh) * HD;
+    const float* vr = v + (b * S + j) * ldv + static_cast<int64_t>(kvh) * HD;
+    float x = 0.f, dp = 0.f;
+    for (int d = 0; d < HD; ++d) {
+      x = fmaf(qv[d], kr[d], x);
+      dp = fmaf(gv[d], vr[d], dp);
+    }
+    const float ds = expf(x * scale - L) * (dp - D);
+    for (int d = 0; d < HD; ++d) acc[d] = fmaf(ds, kr[d], acc[d]);
+  }
+  float* out = dq + (b * S + s) * lddq + static_cast<int64_t>(h) * HD;
+  for (int d = 0; d < HD; ++d) out[d] = acc[d] * scale;
+}
+
+template <int HD>
+__global__ __launch_bounds__(128) void k_attn_bwd_dkdv_f32(
+    const float* __restrict__ q, int64_t ldq, const float* __restrict__ k, int64_t ldk,
+    const float* __restrict__ v, int64_t ldv, const float* __restrict__ dO, int64_t lddo,
+    const float* __restrict__ lse, const float* __restrict__ delta, float* __restrict__ dk,
+    int64_t lddk, float* __restrict__ dv, int64_t lddv, int S, int nh, int nkv, int group,
+    float scale, int64_t rows) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= rows) return;  // rows = B*nkv*S, idx = (b*nkv + kvh)*S + j
+  const int j = static_cast<int>(idx % S);
+  const int64_t bk = idx / S;
+  const int kvh = static_cast<int>(bk % nkv);
+  const int64_t b = bk / nkv;
+  const float* kr = k + (b * S + j) * ldk + static_cast<int64_t>(kvh) * HD;
+  const float* vr = v + (b * S + j) * ldv + static_cast<int64_t>(kvh) * HD;
+  float kv[HD], vv[HD], ak[HD], av[HD];
+  for (int d = 0; d < HD; ++d) { kv[d] = kr[d]; vv[d] = vr[d]; ak[d] = 0.f; av[d] = 0.f; }
+  for (int hh = 0; hh < group; ++hh) {
+    const int h = kvh * group + hh;
+    const int64_t row = (b * nh + h) * S;
+    for (int s = j; s < S; ++s) {
+      const float* qr = q + (b * S + s) * ldq + static_cast<int64_t>(h) * HD;
+      const float* gr = dO + (b * S + s) * lddo + static_cast<int64_t>(h) * HD;
+      float x = 0.f, dp = 0.f;
+      for (int d = 0; d < HD; ++d) {
+        x = fmaf(qr[d], kv[d], x);
+        dp = fmaf(gr[d], vv[d], dp);
+      }
+      const float p = expf(x * scale - lse[row + s]);
+      const float ds = p * (dp - delta[row + s]);
+      for (int d = 0; d < HD; ++d) {
+        av[d] = fmaf(p, gr[d], av[d]);
+        ak[d] = fmaf(ds, qr[d], ak[d]);
+      }
+    }
+  }
+  float* ok = dk + (b * S + j) * lddk + static_cast<int64_t>(kvh) * HD;
+  float* ov = dv + (b * S + j) * lddv + static_cast<int64_t>(kvh) * HD;
+  for (int d = 0; d < HD; ++d) { ok[d] = ak[d] * scale; ov[d] = av[d]; }
+}
+
+// ------------------------------------------------------------------- host
+struct Dims {
+  int64_t B, S, nh, nkv, hd;
+};
+
+int check_dims(fh_dtype dt, const Dims& d) {
+  FH_REQUIRE(dt == FH_BF16 || dt == FH_F32, "attention: dtype must be FH_BF16 or FH_F32");
+  FH_REQUIRE(d.B >= 0 && d.S >= 0, "attention: negative batch/seq_len");
+  FH_REQUIRE(d.nh > 0 && d.nkv > 0 && d.nh % d.nkv == 0,
+             "attention: n_heads must be a positive multiple of n_kv_heads");
+  FH_REQUIRE(d.hd == 32 || d.hd == 64 || d.hd == 128, "attention: head_dim must be 32, 64 or 128");
+  FH_REQUIRE(d.S <= (int64_t(1) << 30) && d.B * d.nh <= 65535 && d.B * d.nkv <= 65535,
+             "attention: grid too large");
+  return FH_OK;
+}
+
+int check_ld(int64_t ld, int64_t heads, int64_t hd, const char* what) {
+  if (ld < heads * hd || ld % 8 != 0)
+    return fail(FH_ERR_INVALID, std::string("attention: ") + what +
+                                    " row stride must be >= heads*head_dim and a multiple of 8");
+  return FH_OK;
+}
+
+template <typename F>
+int dispatch_hd(int64_t hd, F&& f) {
+  if (hd == 32) return f(std::integral_constant<int, 32>{});
+  if (hd == 64) return f(std::integral_constant<int, 64>{});
+  return f(std::integral_constant<int, 128>{});
+}
+
+}  // namespace
+}  // namespace fh
+
+using namespace fh;
+
+extern "C" size_t fh_attn_bwd_workspace_size(int64_t batch, int64_t seq_len, int64_t n_heads) {
+  if (batch <= 0 || seq_len <= 0 || n_heads <= 0) return 0;
+  return static_cast<size_t>(batch * seq_len * n_heads) * sizeof(float);
+}
+
+extern "C" int fh_attn_fwd(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t ldk,
+                           const void* v, int64_t ldv, void* o, int64_t ldo, float* lse,
+                           int64_t batch, int64_t seq_len, int64_t n_heads, int64_t n_kv_heads,
+                           int64_t head_dim, float scale, hipStream_t stream) {
+  const Dims d{batch, seq_len, n_heads, n_kv_heads, head_dim};
+  if (int e = check_dims(dt, d)) return e;
+  if (batch == 0 || seq_len == 0) return FH_OK;
+  if (int e = check_ld(ldq, n_heads, head_dim, "q")) return e;
+  if (int e = check_ld(ldk, n_kv_heads, head_dim, "k")) return e;
+  if (int e = check_ld(ldv, n_kv_heads, head_dim, "v")) return e;
+  if (int e = check_ld(ldo, n_heads, head_dim, "o")) return e;
+  FH_REQUIRE(q && k && v && o, "attn_fwd: null pointer");
+  FH_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o),
+             "attn_fwd: pointers must be 16-byte aligned");
+  const int S = static_cast<int>(seq_len), nh = static_cast<int>(n_heads);
+  const int group = static_cast<int>(n_heads / n_kv_heads);
+  if (dt == FH_BF16) {
+    const dim3 grid(static_cast<unsigned>((seq_len + 127) / 128), static_cast<unsigned>(batch * n_heads));
+    dispatch_hd(head_dim, [&](auto hdc) {
+      hipLaunchKernelGGL((k_attn_fwd<hdc()>), grid, dim3(256), 0, stream,
+                         static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(k), ldk,
+                         static_cast<const uint16_t*>(v), ldv, static_cast<uint16_t*>(o), ldo, lse,
+                         S, nh, group, scale * kLog2e);
+      return 0;
+    });
+  } else {
+    const int64_t rows = batch * n_heads * seq_len;
+    dispatch_hd(head_dim, [&](auto hdc) {
+      hipLaunchKernelGGL((k_attn_fwd_f32<hdc()>), dim3(static_cast<unsigned>((rows + 127) / 128)),
+                         dim3(128), 0, stream, static_cast<const float*>(q), ldq,
+                         static_cast<const float*>(k), ldk, static_cast<const float*>(v), ldv,
+                         static_cast<float*>(o), ldo, lse, S, nh, group, scale, rows);
+      return 0;
+    });
+  }
+  return check_launch("fh_attn_fwd");
+}
+
+extern "C" int fh_attn_bwd(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t ldk,
+                           const void* v, int64_t ldv, const void* o, int64_t ldo,
+                           const void* dout, int64_t lddo, const float* lse, void* dq,
+                           int64_t lddq, void* dk, int64_t lddk, void* dv, int64_t lddv,
+                           void* workspace, int64_t batch, int64_t seq_len, int64_t n_heads,
+                           int64_t n_kv_heads, int64_t head_dim, float scale, hipStream_t stream) {
+  const Dims d{batch, seq_len, n_heads, n_kv_heads, head_dim};
+  if (int e = check_dims(dt, d)) return e;
+  if (batch == 0 || seq_len == 0) return FH_OK;
+  struct LdCheck {
+    int64_t ld, heads;
+    const char* what;
+  };
+  const LdCheck lds[] = {{ldq, n_heads, "q"},   {ldk, n_kv_heads, "k"}, {ldv, n_kv_heads, "v"},
+                         {ldo, n_heads, "o"},   {lddo, n_heads, "dout"}, {lddq, n_heads, "dq"},
+                         {lddk, n_kv_heads, "dk"}, {lddv, n_kv_heads, "dv"}};
+  for (const LdCheck& c : lds)
+    if (int e = check_ld(c.ld, c.heads, head_dim, c.what)) return e;
+  FH_REQUIRE(q && k && v && o && dout && lse && dq && dk && dv && workspace,
+             "attn_bwd: null pointer");
+  FH_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o) && aligned16(dout) &&
+                 aligned16(dq) && aligned16(dk) && aligned16(dv) && aligned16(workspace),
+             "attn_bwd: pointers must be 16-byte aligned");
+  const int S = static_cast<int>(seq_len), nh = static_cast<int>(n_heads);
+  const int nkv = static_cast<int>(n_kv_heads), group = static_cast<int>(n_heads / n_kv_heads);
+  float* delta = static_cast<float*>(workspace);
+  const int64_t tokens = batch * seq_len;
+  const unsigned dblocks = static_cast<unsigned>((tokens * n_heads + 255) / 256);
+  if (dt == FH_BF16) {
+    hipLaunchKernelGGL((k_attn_delta<uint16_t>), dim3(dblocks), dim3(256), 0, stream,
+                       static_cast<const uint16_t*>(o), ldo, static_cast<const uint16_t*>(dout),
+                       lddo, delta, S, nh, static_cast<int>(head_dim), tokens);
+    const dim3 gq(static_cast<unsigned>((seq_len + 127) / 128), static_cast<unsigned>(batch * n_heads));
+    const dim3 gk(static_cast<unsigned>((seq_len + 127) / 128), static_cast<unsigned>(batch * n_kv_heads));
+    dispatch_hd(head_dim, [&](auto hdc) {
+      hipLaunchKernelGGL((k_attn_bwd_dkdv<hdc()>), gk, dim3(256), 0, stream,
+                         static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(k), ldk,
+                         static_cast<const uint16_t*>(v), ldv, static_cast<const uint16_t*>(dout),
+                         lddo, lse, delta, static_cast<uint16_t*>(dk), lddk,
+                         static_cast<uint16_t*>(dv), lddv, S, nh, nkv, group, scale * kLog2e,
+                         scale);
+      hipLaunchKernelGGL((k_attn_bwd_dq<hdc()>), gq, dim3(256), 0, stream,
+                         static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(k), ldk,
+                         static_cast<const uint16_t*>(v), ldv, static_cast<const uint16_t*>(dout),
+                         lddo, lse, delta, static_cast<uint16_t*>(dq), lddq, S, nh, group,
+                         scale * kLog2e, scale);
+      return 0;
+    });
+  } else {
+    hipLaunchKernelGGL((k_attn_delta<float>), dim3(dblocks), dim3(256), 0, stream,
+                       static_cast<const float*>(o), ldo, static_cast<const float*>(dout), lddo,
+                       delta, S, nh, static_cast<int>(head_dim), tokens);
+    const int64_t qrows = batch * n_heads * seq_len, krows = batch * n_kv_heads * seq_len;
+    dispatch_hd(head_dim, [&](auto hdc) {
+      hipLaunchKernelGGL((k_attn_bwd_dq_f32<hdc()>), dim3(static_cast<unsigned>((qrows + 127) / 128)),
+                         dim3(128), 0, stream, static_cast<const float*>(q), ldq,
+                         static_cast<const float*>(k), ldk, static_cast<const float*>(v), ldv,
+                         static_cast<const float*>(dout), lddo, lse, delta, static_cast<float*>(dq),
+                         lddq, S, nh, group, scale, qrows);
+      hipLaunchKernelGGL((k_attn_bwd_dkdv_f32<hdc()>), dim3(static_cast<unsigned>((krows + 127) / 128)),
+                         dim3(128), 0, stream, static_cast<const float*>(q), ldq,
+                         static_cast<const float*>(k), ldk, static_cast<const float*>(v), ldv,
+                         static_cast<const float*>(dout), lddo, lse, delta,
+                         static_cast<float*>(dk), lddk, static_cast<float*>(dv), lddv, S, nh, nkv,
+                         group, scale, krows);
+      return 0;
+    });
+  }
+  return check_launch("fh_attn_bwd");
+}

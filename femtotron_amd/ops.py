@@ -206,3 +206,42 @@ def add(a: torch.Tensor, b: torch.Tensor, *, out: torch.Tensor | None = None) ->
     o = torch.empty_like(a) if out is None else out
     _lib.call("fh_add", _dtype_code(a), _ptr(a), _ptr(b), _ptr(o), a.numel(), _stream(a))
     return o
+
+
+# ---------------------------------------------------------------- attention
+def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, batch: int, seq_len: int,
+             n_heads: int, n_kv_heads: int, head_dim: int, scale: float, *,
+             need_lse: bool = True) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Causal GQA attention on token-major [T, *] views (head h at columns h*head_dim).
+    Returns (o [T, n_heads*head_dim], lse fp32 [batch, n_heads, seq_len] or None)."""
+    _require_gpu(q, k, v)
+    _same_dtype(q, k, v)
+    T = batch * seq_len
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        if t.size(0) != T:
+            raise ValueError(f"attn_fwd: {n} has {t.size(0)} rows, expected {T}")
+    o = torch.empty(T, n_heads * head_dim, dtype=q.dtype, device=q.device)
+    lse = (torch.empty(batch, n_heads, seq_len, dtype=torch.float32, device=q.device)
+           if need_lse else None)
+    _lib.call("fh_attn_fwd", _dtype_code(q), _ptr(q), _rowmajor(q, "q"), _ptr(k), _rowmajor(k, "k"),
+              _ptr(v), _rowmajor(v, "v"), _ptr(o), o.stride(0), _fptr(lse), batch, seq_len,
+              n_heads, n_kv_heads, head_dim, float(scale), _stream(q))
+    return o, lse
+
+
+def attn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
+             dout: torch.Tensor, lse: torch.Tensor, dq: torch.Tensor, dk: torch.Tensor,
+             dv: torch.Tensor, batch: int, seq_len: int, n_heads: int, n_kv_heads: int,
+             head_dim: int, scale: float) -> None:
+    """Writes dq, dk, dv (token-major views, may be column ranges of one buffer)."""
+    _require_gpu(q, k, v, o, dout, lse, dq, dk, dv)
+    _same_dtype(q, k, v, o, dout, dq, dk, dv)
+    if lse.dtype != torch.float32 or not lse.is_contiguous() or lse.numel() != batch * n_heads * seq_len:
+        raise ValueError("attn_bwd: lse must be contiguous fp32 [batch, n_heads, seq_len]")
+    ws_bytes = _lib.lib().fh_attn_bwd_workspace_size(batch, seq_len, n_heads)
+    ws = torch.empty(max(ws_bytes, 4) // 4, dtype=torch.float32, device=q.device)
+    _lib.call("fh_attn_bwd", _dtype_code(q), _ptr(q), _rowmajor(q, "q"), _ptr(k), _rowmajor(k, "k"),
+              _ptr(v), _rowmajor(v, "v"), _ptr(o), _rowmajor(o, "o"), _ptr(dout),
+              _rowmajor(dout, "dout"), _fptr(lse), _ptr(dq), _rowmajor(dq, "dq"), _ptr(dk),
+              _rowmajor(dk, "dk"), _ptr(dv), _rowmajor(dv, "dv"), _ptr(ws), batch, seq_len,
+              n_heads, n_kv_heads, head_dim, float(scale), _stream(q))

@@ -140,6 +140,37 @@ int fh_swiglu_bwd(fh_dtype dt, const void* dp, int64_t ld_dp, const void* g,
 int fh_add(fh_dtype dt, const void* a, const void* b, void* out, int64_t n,
            hipStream_t stream);
 
+/* ---------------------------------------------------------------- attention
+ * Causal GQA softmax attention, replacing F.scaled_dot_product_attention(
+ * q, k, v, is_causal=True, enable_gqa=True, scale) as called from
+ * sdpa_attention_forward (transformers integrations/sdpa_attention.py:79-166)
+ * by LlamaAttention (modeling_llama.py:235-281), forward and backward.
+ * Token-major layouts: row t = b*seq_len + s; query head h occupies columns
+ * h*head_dim.. of q/o/dout/dq (row strides ldq, ldo, ...), kv head j columns
+ * j*head_dim.. of k/v/dk/dv; q head h reads kv head h / (n_heads/n_kv_heads).
+ * head_dim in {32, 64, 128}; strides multiples of 8; 16-byte aligned bases.
+ * FH_BF16 runs on MFMA (fp32 softmax/accumulation); FH_F32 in fp32 FMA.
+ * lse: fp32 [batch, n_heads, seq_len], natural-log row log-sum-exp of the
+ * scaled scores (nullable in the forward).
+ */
+int fh_attn_fwd(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t ldk,
+                const void* v, int64_t ldv, void* o, int64_t ldo, float* lse,
+                int64_t batch, int64_t seq_len, int64_t n_heads, int64_t n_kv_heads,
+                int64_t head_dim, float scale, hipStream_t stream);
+
+/* Bytes of workspace fh_attn_bwd needs (the fp32 rowsum(dO*O) per query). */
+size_t fh_attn_bwd_workspace_size(int64_t batch, int64_t seq_len, int64_t n_heads);
+
+/* Gradients of fh_attn_fwd given o, lse and dout: writes dq, dk, dv (each
+ * fully overwritten; the kv-head gradients already summed over the query
+ * heads sharing them). */
+int fh_attn_bwd(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t ldk,
+                const void* v, int64_t ldv, const void* o, int64_t ldo,
+                const void* dout, int64_t lddo, const float* lse, void* dq,
+                int64_t lddq, void* dk, int64_t lddk, void* dv, int64_t lddv,
+                void* workspace, int64_t batch, int64_t seq_len, int64_t n_heads,
+                int64_t n_kv_heads, int64_t head_dim, float scale, hipStream_t stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif
