@@ -1,0 +1,320 @@
+#!/usr/bin/env python
+"""Benchmark: activation-checkpointed fwd+bwd tokens/s of the TinyLlama-1.1B-shaped
+model on one MI355X, through the fused HIP checkpoint path.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+One step = forward (embed, 22 checkpointed decoder layers, final norm, lm_head,
+shifted fp32 cross-entropy) + backward (per-layer recompute + layer backward)
+over one synthetic micro-batch of 8 x 2048 token ids already resident in HBM.
+Prints ONE JSON line.  Besides tokens/s it reports:
+  * roofline: the fused memory-bound kernel with the largest share of step time,
+    its algorithmic bytes per launch / its mean launch time (HIP events on the
+    launch stream) against the 8 TB/s HBM peak, and every other fused kernel;
+  * attention kernels against the 2.5 PFLOP/s dense bf16 MFMA peak;
+  * peak activation bytes per token of the fused path and of the reference path
+    (Hugging Face layers under torch.utils.checkpoint, debug=True) on the same GPU;
+  * cpu_baseline: the reference-equivalent path (oracle/torch_llama.py under
+    torch.utils.checkpoint with debug=True, fp32) on the host cores, on a bounded
+    sample of the same model.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "ckpt'd fwd+bwd tokens/s @1 GPU (TinyLlama-1.1B); fused-kernel HBM GB/s % of peak"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+TINYLLAMA = dict(hidden=2048, heads=32, kv=4, ffn=5632, vocab=32000, layers=22, theta=10000.0,
+                 batch=8, seq=2048)
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=TINYLLAMA["layers"],
+                    help="decoder layers (default: the full 22 of TinyLlama-1.1B)")
+    ap.add_argument("--kernel-iters", type=int, default=20)
+    ap.add_argument("--reference-steps", type=int, default=2,
+                    help="timed steps of the reference path on the GPU (0 to skip)")
+    ap.add_argument("--cpu-sample-tokens", type=int, default=512,
+                    help="tokens (one sequence) of the CPU baseline sample (0 to skip)")
+    return ap.parse_args()
+
+
+def llama_config(c: dict, layers: int):
+    from transformers import LlamaConfig
+    cfg = LlamaConfig(hidden_size=c["hidden"], intermediate_size=c["ffn"],
+                      num_attention_heads=c["heads"], num_key_value_heads=c["kv"],
+                      num_hidden_layers=layers, vocab_size=c["vocab"], rms_norm_eps=1e-5,
+                      hidden_act="silu", max_position_embeddings=max(2048, c["seq"]),
+                      tie_word_embeddings=False, rope_theta=c["theta"], attention_dropout=0.0)
+    cfg._attn_implementation = "sdpa"
+    return cfg
+
+
+def time_steps(torch, model, ids, steps: int, warmup: int) -> float:
+    params = [p for p in model.parameters() if p.requires_grad]
+
+    def step():
+        for p in params:
+            p.grad = None
+        model(ids, labels=ids)["loss"].backward()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def activation_bytes_per_token(torch, model, ids) -> float:
+    """(max_memory_allocated during one fwd+bwd - memory_allocated before the
+    forward) / tokens, with the gradients of a previous step already allocated
+    (femtotron/test/integration/test_zero_ac.py:125-139 measures the same way)."""
+    model(ids, labels=ids)["loss"].backward()  # grads exist afterwards
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    model(ids, labels=ids)["loss"].backward()
+    torch.cuda.synchronize()
+    return (torch.cuda.max_memory_allocated() - base) / ids.numel()
+
+
+def event_ms(torch, fn, iters: int) -> float:
+    """Mean launch time of fn() with HIP events on the current (launch) stream."""
+    fn()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(iters):
+        fn(i)
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def kernel_table(torch, iters: int):
+    """Fused kernels at the TinyLlama step's shapes.  Each launch reads a
+    different buffer set (working set > 1 GiB) so the 256 MiB MALL cannot serve
+    repeats: the bytes come from HBM as in the step."""
+    from femtotron_amd import ops
+    c = TINYLLAMA
+    T, H, F = c["batch"] * c["seq"], c["hidden"], c["ffn"]
+    nh, nkv, hd = c["heads"], c["kv"], c["hidden"] // c["heads"]
+    Hq, Hkv = nh * hd, nkv * hd
+    dev = "cuda"
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(7)
+
+    def rnd(*shape):
+        return torch.randn(*shape, device=dev, dtype=bf, generator=g)
+
+    def sets(n, make):
+        return [make() for _ in range(n)]
+
+    w = (1 + 0.02 * rnd(H)).contiguous()
+    rows = []
+
+    def add_row(name, kernel, launches_per_step, bytes_per_launch, ms):
+        gbs = bytes_per_launch / (ms * 1e-3) / 1e9
+        rows.append(dict(kernel=name, symbol=kernel, launches_per_step=launches_per_step,
+                         bytes_per_launch=int(bytes_per_launch), ms_per_launch=round(ms, 5),
+                         achieved_gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4)))
+
+    L = c["layers"]
+    # rmsnorm_fwd: x -> y   (4TH bytes)
+    xs = sets(8, lambda: rnd(T, H))
+    ys = sets(8, lambda: torch.empty(T, H, device=dev, dtype=bf))
+    rs = torch.empty(T, device=dev, dtype=torch.float32)
+    ms = event_ms(torch, lambda i=0: ops.rmsnorm_fwd(xs[i % 8], w, 1e-5, out=ys[i % 8], rstd=rs), iters)
+    add_row("rmsnorm_fwd", "k_rmsnorm_fwd", 2 * L, 4 * T * H, ms)
+    # add_rmsnorm_fwd: x, a -> h, y   (8TH)
+    as_ = sets(8, lambda: rnd(T, H))
+    ms = event_ms(torch, lambda i=0: ops.add_rmsnorm_fwd(xs[i % 8], as_[i % 8], w, 1e-5, rstd=rs), iters)
+    add_row("add_rmsnorm_fwd", "k_rmsnorm_fwd (ADD)", 2 * L, 8 * T * H, ms)
+    # rmsnorm_bwd with residual: dy, x, dres -> dx   (8TH)
+    ms = event_ms(torch, lambda i=0: ops.rmsnorm_bwd(ys[i % 8], xs[i % 8], w, 1e-5, rstd=rs,
+                                                       dres=as_[i % 8]), iters)
+    add_row("rmsnorm_bwd", "k_rmsnorm_bwd", 2 * L, 8 * T * H, ms)
+    del as_
+    # residual add: h + m -> out   (6TH)
+    ms = event_ms(torch, lambda i=0: ops.add(xs[i % 8], ys[i % 8], out=ys[(i + 1) % 8]), iters)
+    add_row("residual_add", "k_add", L, 6 * T * H, ms)
+    del xs, ys
+    # rope on q and k of the qkv buffer   (4T(Hq+Hkv))
+    qkvs = sets(6, lambda: rnd(T, Hq + 2 * Hkv))
+    cos = torch.cos(torch.arange(c["seq"] * hd, device=dev, dtype=torch.float32)).to(bf).view(1, c["seq"], hd)
+    sin = torch.sin(torch.arange(c["seq"] * hd, device=dev, dtype=torch.float32)).to(bf).view(1, c["seq"], hd)
+    ms = event_ms(torch, lambda i=0: ops.rope_fwd_(qkvs[i % 6], nh + nkv, hd, c["seq"], cos, sin), iters)
+    add_row("rope_fwd", "k_rope<fwd>", 2 * L, 4 * T * (Hq + Hkv), ms)
+    ms = event_ms(torch, lambda i=0: ops.rope_bwd_(qkvs[i % 6], nh + nkv, hd, c["seq"], cos, sin), iters)
+    add_row("rope_bwd", "k_rope<bwd>", L, 4 * T * (Hq + Hkv), ms)
+    # SwiGLU: g,u -> p (6TF);  dp,g,u -> dg,du (10TF)
+    gus = sets(3, lambda: rnd(T, 2 * F))
+    ps = sets(3, lambda: torch.empty(T, F, device=dev, dtype=bf))
+    ms = event_ms(torch, lambda i=0: ops.swiglu_fwd(gus[i % 3][:, :F], gus[i % 3][:, F:], out=ps[i % 3]), iters)
+    add_row("swiglu_fwd", "k_swiglu_fwd", 2 * L, 6 * T * F, ms)
+    dgus = sets(3, lambda: torch.empty(T, 2 * F, device=dev, dtype=bf))
+    ms = event_ms(torch, lambda i=0: ops.swiglu_bwd(ps[i % 3], gus[i % 3][:, :F], gus[i % 3][:, F:],
+                                                      dgus[i % 3][:, :F], dgus[i % 3][:, F:]), iters)
+    add_row("swiglu_bwd", "k_swiglu_bwd", L, 10 * T * F, ms)
+    del gus, ps, dgus
+
+    # attention (MFMA-bound): causal flop count 4*B*nh*S^2*hd/2 forward
+    B, S = c["batch"], c["seq"]
+    qkv = qkvs[0]
+    q, k, v = qkv[:, :Hq], qkv[:, Hq:Hq + Hkv], qkv[:, Hq + Hkv:]
+    fwd_flop = 4 * B * nh * S * S * hd / 2
+    o, lse = ops.attn_fwd(q, k, v, B, S, nh, nkv, hd, hd ** -0.5)
+    ms_f = event_ms(torch, lambda i=0: ops.attn_fwd(q, k, v, B, S, nh, nkv, hd, hd ** -0.5), iters)
+    do = rnd(T, Hq)
+    dqkv = torch.empty_like(qkv)
+    ms_b = event_ms(torch, lambda i=0: ops.attn_bwd(q, k, v, o, do, lse, dqkv[:, :Hq], dqkv[:, Hq:Hq + Hkv],
+                                                      dqkv[:, Hq + Hkv:], B, S, nh, nkv, hd, hd ** -0.5),
+                    max(3, iters // 4))
+    # backward: dK/dV kernel 4 products + dQ kernel 3 products (the dQ kernel
+    # recomputes S and dP); algorithmic = the 5 products of attention backward
+    bwd_flop = 2.5 * fwd_flop
+    mfma = [dict(kernel="attn_fwd", symbol="k_attn_fwd<64>", launches_per_step=2 * L,
+                 flop_per_launch=fwd_flop, ms_per_launch=round(ms_f, 4),
+                 achieved_tflops=round(fwd_flop / ms_f / 1e9, 1),
+                 frac=round(fwd_flop / ms_f / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)),
+            dict(kernel="attn_bwd", symbol="k_attn_bwd_dkdv<64> + k_attn_bwd_dq<64> + k_attn_delta",
+                 launches_per_step=L, flop_per_launch=bwd_flop, ms_per_launch=round(ms_b, 4),
+                 achieved_tflops=round(bwd_flop / ms_b / 1e9, 1),
+                 frac=round(bwd_flop / ms_b / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4))]
+    return rows, mfma
+
+
+def cpu_baseline(torch, n_tokens: int) -> dict:
+    """Reference-equivalent path on the host: oracle Llama (HF layer math) with
+    every layer under torch.utils.checkpoint(use_reentrant=False, debug=True), fp32."""
+    from oracle.torch_llama import OracleLlama
+    c = TINYLLAMA
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    try:
+        orc = OracleLlama(vocab=c["vocab"], hidden=c["hidden"], n_layers=c["layers"], n_heads=c["heads"],
+                          n_kv=c["kv"], ffn=c["ffn"], theta=c["theta"])
+        ids = torch.randint(0, c["vocab"], (1, n_tokens), generator=torch.Generator().manual_seed(2000))
+        t0 = time.perf_counter()
+        _, loss = orc.forward(ids, ids, checkpoint=True, debug=True)
+        loss.backward()
+        dt = time.perf_counter() - t0
+    finally:
+        torch.set_num_threads(prev)
+    return {"value": round(n_tokens / dt, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"1 fwd+bwd of the full 22-layer TinyLlama-1.1B-shaped model on 1 x {n_tokens} "
+                      f"tokens, fp32, oracle/torch_llama.py layers under torch.utils.checkpoint("
+                      f"use_reentrant=False, debug=True) as the reference wrapper calls it; "
+                      f"{dt:.1f} s on {cores} threads"}
+
+
+def main() -> int:
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (TP = PP = DP = 1); "
+              "run it with --gpus 1", file=sys.stderr)
+        return 2
+    import torch
+
+    from femtotron_amd import dispatch_counts, fused_checkpoint, reset_dispatch_counts
+    from femtotron_amd.model import build_llama_model, init_llama_weights_
+    from femtotron_amd.scripts.presets import get_ac_policy
+    from femtotron_amd.training import apply_activation_checkpointing, remove_activation_checkpointing
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    c = TINYLLAMA
+    B, S = c["batch"], c["seq"]
+    T = B * S
+    log(f"building TinyLlama-shaped model ({args.layers} layers), bf16, weights N(0, 0.02)")
+    model = build_llama_model(llama_config(c, args.layers))
+    model = init_llama_weights_(model, device="cuda", dtype=torch.bfloat16, generator_device="cuda")
+    policy = get_ac_policy("llama_decoder_layer")
+    apply_activation_checkpointing(model, policy, checkpoint_fn=fused_checkpoint)
+    ids = torch.randint(0, c["vocab"], (B, S), generator=torch.Generator().manual_seed(2000)).cuda()
+
+    reset_dispatch_counts()
+    log(f"fused path: {args.warmup} warm-up + {args.steps} timed steps")
+    sec = time_steps(torch, model, ids, args.steps, args.warmup)
+    counts = dispatch_counts()
+    assert counts["fallback"] == 0 and counts["fused"] == args.layers * (args.steps + args.warmup), counts
+    tok_s = T / sec
+    log(f"fused: {sec * 1e3:.2f} ms/step, {tok_s:.0f} tokens/s")
+    act_fused = activation_bytes_per_token(torch, model, ids)
+
+    log("per-kernel HIP-event timings at the step's shapes")
+    rows, mfma = kernel_table(torch, args.kernel_iters)
+    for r in rows:
+        r["ms_per_step"] = round(r["ms_per_launch"] * r["launches_per_step"] * args.layers / c["layers"], 4)
+    dom = max(rows, key=lambda r: r["ms_per_step"])
+    roofline = {"bound": "hbm", "kernel": dom["kernel"], "achieved": dom["achieved_gbs"],
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["frac"], "traffic": None,
+                "bytes_per_launch": dom["bytes_per_launch"]}
+
+    ref = None
+    if args.reference_steps > 0:
+        log("reference path on the same GPU: HF layers under torch.utils.checkpoint(debug=True)")
+        remove_activation_checkpointing(model)
+        apply_activation_checkpointing(model, policy)  # default checkpoint_fn = torch's
+        torch.cuda.empty_cache()
+        rsec = time_steps(torch, model, ids, args.reference_steps, 1)
+        act_ref = activation_bytes_per_token(torch, model, ids)
+        ref = {"tokens_per_s": round(T / rsec, 1), "ms_per_step": round(rsec * 1e3, 2),
+               "activation_bytes_per_token": round(act_ref, 1),
+               "speedup_fused_vs_reference": round(rsec / sec, 2)}
+        log(f"reference: {rsec * 1e3:.1f} ms/step")
+    del model
+    torch.cuda.empty_cache()
+
+    cpu = None
+    if args.cpu_sample_tokens > 0:
+        log(f"cpu baseline: {args.cpu_sample_tokens} tokens on the host")
+        cpu = cpu_baseline(torch, args.cpu_sample_tokens)
+
+    out = {
+        "metric": METRIC, "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (token ids uniform over the vocab, CPU Generator(2000); random-init "
+                "weights N(0, 0.02))",
+        "config": {"workload": "TinyLlama-1.1B-shaped checkpointed fwd+bwd (BASELINE config 3)",
+                   "layers": args.layers, "hidden": c["hidden"], "heads": c["heads"],
+                   "kv_heads": c["kv"], "ffn": c["ffn"], "vocab": c["vocab"], "micro_batch": B,
+                   "seq_len": S, "tokens_per_step": T, "activation_checkpointing": "every layer",
+                   "parallelism": "single GPU (TP=PP=DP=1)"},
+        "roofline": roofline,
+        "fused_kernels_hbm": rows,
+        "attention_mfma": mfma,
+        "activation_bytes_per_token": round(act_fused, 1),
+        "reference_gpu": ref,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

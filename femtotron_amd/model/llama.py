@@ -102,14 +102,23 @@ def reset_rotary_inv_freq_(model: nn.Module) -> None:
 
 
 def init_llama_weights_(model: nn.Module, *, device: torch.device | str, dtype: torch.dtype,
-                        std: float = 0.02, seed: int = 42) -> nn.Module:
+                        std: float = 0.02, seed: int = 42, generator_device: str = "cpu") -> nn.Module:
     """Materialise ``model`` on ``device`` with every parameter ~ N(0, std) drawn
-    in registration order from CPU Generator(seed), then cast to ``dtype``."""
+    in registration order, then cast to ``dtype``.
+
+    generator_device="cpu" (default) draws from CPU Generator(seed): identical
+    weights on every machine.  generator_device="cuda" draws on the device from a
+    seeded device generator (fast for billion-parameter models; the values then
+    depend on the device's random-number kernels)."""
     model = model.to_empty(device=device)
-    gen = torch.Generator(device="cpu").manual_seed(seed)
+    gen = torch.Generator(device=generator_device).manual_seed(seed)
     with torch.no_grad():
         for p in model.parameters():
-            if p.requires_grad:
+            if not p.requires_grad:
+                continue
+            if generator_device == "cpu":
                 p.copy_(torch.empty(p.shape, dtype=torch.float32).normal_(0.0, std, generator=gen))
+            else:
+                p.normal_(0.0, std, generator=gen)
     reset_rotary_inv_freq_(model)
     return model.to(dtype)
