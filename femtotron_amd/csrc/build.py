@@ -35,6 +35,10 @@ COMMON_FLAGS = [
     "-Wno-unused-function",
     # Packed fp32 (v_pk_*_f32) code generation stays off for all device code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the attention softmax rescales its output
+    # accumulators every key block, which in AGPRs costs a read and a write
+    # per register per block.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]

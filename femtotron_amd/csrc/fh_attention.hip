@@ -41,6 +41,21 @@ __device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// 2^x on the transcendental unit (v_exp_f32).  Denormal results flush to
+// zero, which is harmless for softmax weights (the row maximum is 2^0).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// max over lanes i and i^32 (v_permlane32_swap exchanges the two row halves).
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
 #pragma unroll
@@ -83,24 +98,49 @@ __device__ __forceinline__ bf16x8 pack_frag(const f32x16& acc, int j0) {
 // Row (M index) of accumulator entry j for lane half hl.
 __device__ __forceinline__ int acc_row(int j, int hl) { return 8 * (j >> 2) + 4 * hl + (j & 3); }
 
-// Cooperative copy of `rows` rows x HD columns (bf16) from a token-major
-// source (row stride ld) into an LDS tile with row stride LDST; rows at or
-// beyond `valid` are zero-filled.  16-byte chunks, consecutive threads on
-// consecutive chunks of a row.
-template <int HD, int LDST>
-__device__ __forceinline__ void copy_tile(uint16_t* dst, const uint16_t* src, int64_t ld, int rows,
-                                          int valid, int tid, int nthreads) {
-  constexpr int CPR = HD / 8;
-  for (int c = tid; c < rows * CPR; c += nthreads) {
-    const int r = c / CPR, col = (c - r * CPR) * 8;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (r < valid) v = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(r) * ld + col);
-    *reinterpret_cast<uint4*>(dst + r * LDST + col) = v;
+// Per-thread registers holding one ROWS x HD bf16 tile in flight from global
+// memory to LDS (the software pipeline's prefetch stage): load() issues the
+// 16-byte global loads (rows at or beyond `valid` read as zero), store() writes
+// them to an LDS tile of row stride LDST.  Consecutive threads take
+// consecutive 16-byte chunks of a row.
+template <int ROWS, int HD, int LDST, int NT>
+struct TileRegs {
+  static constexpr int CPR = HD / 8;
+  static constexpr int CHUNKS = ROWS * CPR;
+  static constexpr int N = (CHUNKS + NT - 1) / NT;
+  uint4 r[N];
+  __device__ __forceinline__ void load(const uint16_t* src, int64_t ld, int valid, int tid) {
+    if (valid >= ROWS) {  // whole tile in range (the common case): no per-row guard
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const int c = tid + i * NT;
+        const int row = c / CPR, col = (c - row * CPR) * 8;
+        if (CHUNKS % NT == 0 || c < CHUNKS)
+          r[i] = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(row) * ld + col);
+      }
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int c = tid + i * NT;
+      const int row = c / CPR, col = (c - row * CPR) * 8;
+      r[i] = make_uint4(0, 0, 0, 0);
+      if ((CHUNKS % NT == 0 || c < CHUNKS) && row < valid)
+        r[i] = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(row) * ld + col);
+    }
   }
-}
+  __device__ __forceinline__ void store(uint16_t* dst, int tid) const {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int c = tid + i * NT;
+      const int row = c / CPR, col = (c - row * CPR) * 8;
+      if (CHUNKS % NT == 0 || c < CHUNKS) *reinterpret_cast<uint4*>(dst + row * LDST + col) = r[i];
+    }
+  }
+};
 
 // Stores a transposed accumulator tile (rows = head dims d, column = this
-// lane's token) scaled by `mul` into row `row` of a token-major output.
+// lane's token) scaled by `mul` into one token-major output row.
 template <int HD>
 __device__ __forceinline__ void store_rows_T(uint16_t* out_row, const f32x16 (&acc)[HD / 32],
                                              float mul, int hl) {
@@ -115,102 +155,154 @@ __device__ __forceinline__ void store_rows_T(uint16_t* out_row, const f32x16 (&a
     }
 }
 
+// Query tiles (of 32) per wave in the forward.  Two tiles would let every K/V
+// fragment read from LDS feed two MFMAs, but the extra registers cost a wave
+// of occupancy and measured slower at head_dim 64 (447 vs 384 us for the
+// TinyLlama attention shape), so one tile for every head_dim.
+template <int HD>
+struct FwdTiles {
+  static constexpr int QT = 1;
+};
+
 // ------------------------------------------------------------ forward (bf16)
-// Block = 4 waves x 32 queries of one (batch, head); loop over 64-key blocks.
+// Block = 4 waves x (32*QT) queries of one (batch, head); loop over 64-key
+// blocks, double-buffered in LDS: the next block's K/V are loaded into
+// registers while the current one is multiplied, then written to the other
+// LDS stage; one barrier per block.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_fwd(
     const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
     const uint16_t* __restrict__ v, int64_t ldv, uint16_t* __restrict__ o, int64_t ldo,
     float* __restrict__ lse, int S, int nh, int group, float scale_log2) {
-  constexpr int BM = 128, BN = 64, LDST = HD + 8, NS = HD / 16, ND = HD / 32;
-  __shared__ __align__(16) uint16_t sk[BN * LDST];
-  __shared__ __align__(16) uint16_t sv[BN * LDST];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hl = lane >> 5, l32 = lane & 31;
+  constexpr int QT = FwdTiles<HD>::QT;
+  constexpr int BM = 4 * 32 * QT, BN = 64, LDST = HD + 8, NS = HD / 16, ND = HD / 32;
+  __shared__ __align__(16) uint16_t sk[2][BN * LDST];
+  __shared__ __align__(16) uint16_t sv[2][BN * LDST];
+  const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const int bh = blockIdx.y, b = bh / nh, h = bh - b * nh, kvh = h / group;
   const int q0 = (gridDim.x - 1 - blockIdx.x) * BM;  // heaviest (latest) query blocks first
-  const int qw = q0 + wave * 32, qi = qw + l32;
+  const int qw = q0 + wave * 32 * QT;                 // first query of this wave
   const int64_t tok0 = static_cast<int64_t>(b) * S;
 
-  bf16x8 qf[NS];
-  {
+  bf16x8 qf[QT][NS];
+#pragma unroll
+  for (int u = 0; u < QT; ++u) {
+    const int qi = qw + 32 * u + l32;
     const uint16_t* qrow = q + (tok0 + qi) * ldq + static_cast<int64_t>(h) * HD + 8 * hl;
 #pragma unroll
     for (int s = 0; s < NS; ++s)
-      qf[s] = qi < S ? ld_frag(qrow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
+      qf[u][s] = qi < S ? ld_frag(qrow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
   }
-  f32x16 oacc[ND];
+  f32x16 oacc[QT][ND];
+  float m[QT], l[QT];
 #pragma unroll
-  for (int dt = 0; dt < ND; ++dt) oacc[dt] = zero16();
-  float m = -INFINITY, l = 0.f;
+  for (int u = 0; u < QT; ++u) {
+    m[u] = -INFINITY;
+    l[u] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) oacc[u][dt] = zero16();
+  }
 
   const int kend = min(S, q0 + BM);
   const int nkb = (kend + BN - 1) / BN;
   const uint16_t* kb_ptr = k + tok0 * ldk + static_cast<int64_t>(kvh) * HD;
   const uint16_t* vb_ptr = v + tok0 * ldv + static_cast<int64_t>(kvh) * HD;
+  TileRegs<BN, HD, LDST, 256> pk, pv;
+  pk.load(kb_ptr, ldk, S, tid);
+  pv.load(vb_ptr, ldv, S, tid);
+  pk.store(sk[0], tid);
+  pv.store(sv[0], tid);
+  __syncthreads();
   for (int kb = 0; kb < nkb; ++kb) {
-    const int k0 = kb * BN;
-    __syncthreads();
-    copy_tile<HD, LDST>(sk, kb_ptr + static_cast<int64_t>(k0) * ldk, ldk, BN, S - k0, tid, 256);
-    copy_tile<HD, LDST>(sv, vb_ptr + static_cast<int64_t>(k0) * ldv, ldv, BN, S - k0, tid, 256);
-    __syncthreads();
-    if (k0 > qw + 31) continue;  // the whole block lies after this wave's last query
-
-    f32x16 sacc[BN / 32];
-#pragma unroll
-    for (int t = 0; t < BN / 32; ++t) {
-      sacc[t] = zero16();
-#pragma unroll
-      for (int s = 0; s < NS; ++s)
-        sacc[t] = mfma(ld_frag(sk + (32 * t + l32) * LDST + 16 * s + 8 * hl), qf[s], sacc[t]);
+    const int k0 = kb * BN, st = kb & 1;
+    const bool more = kb + 1 < nkb;
+    if (more) {
+      pk.load(kb_ptr + static_cast<int64_t>(k0 + BN) * ldk, ldk, S - k0 - BN, tid);
+      pv.load(vb_ptr + static_cast<int64_t>(k0 + BN) * ldv, ldv, S - k0 - BN, tid);
     }
-    const bool need_mask = (k0 + BN - 1 > qw) || (k0 + BN > S);
-    float mloc = -INFINITY;
+    if (k0 <= qw + 32 * QT - 1) {  // some key of the block precedes some query of the wave
+      const uint16_t* K = sk[st];
+      const uint16_t* V = sv[st];
+      f32x16 sacc[BN / 32][QT];
 #pragma unroll
-    for (int t = 0; t < BN / 32; ++t)
+      for (int t = 0; t < BN / 32; ++t) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        float x = sacc[t][j] * scale_log2;
-        if (need_mask) {
-          const int key = k0 + 32 * t + acc_row(j, hl);
-          if (key > qi || key >= S) x = -INFINITY;
+        for (int u = 0; u < QT; ++u) sacc[t][u] = zero16();
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          const bf16x8 a = ld_frag(K + (32 * t + l32) * LDST + 16 * s + 8 * hl);
+#pragma unroll
+          for (int u = 0; u < QT; ++u) sacc[t][u] = mfma(a, qf[u][s], sacc[t][u]);
         }
-        sacc[t][j] = x;
-        mloc = fmaxf(mloc, x);
       }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float mnew = fmaxf(m, mloc);  // finite: key 0 is visible to every query
-    const float alpha = exp2f(m - mnew);
-    m = mnew;
-    float lsum = 0.f;
+      const bool need_mask = (k0 + BN - 1 > qw) || (k0 + BN > S);
 #pragma unroll
-    for (int t = 0; t < BN / 32; ++t)
+      for (int u = 0; u < QT; ++u) {
+        const int qi = qw + 32 * u + l32;
+        float mloc = -INFINITY;
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const float p = exp2f(sacc[t][j] - mnew);
-        sacc[t][j] = p;
-        lsum += p;
+        for (int t = 0; t < BN / 32; ++t)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            float x = sacc[t][u][j] * scale_log2;
+            if (need_mask) {
+              const int key = k0 + 32 * t + acc_row(j, hl);
+              x = ((key > qi) | (key >= S)) ? -INFINITY : x;
+            }
+            sacc[t][u][j] = x;
+            mloc = fmaxf(mloc, x);
+          }
+        mloc = xor32_max(mloc);
+        const float mnew = fmaxf(m[u], mloc);  // finite: key 0 is visible to every query
+        const float alpha = fast_exp2(m[u] - mnew);
+        m[u] = mnew;
+        float lsum = 0.f;
+#pragma unroll
+        for (int t = 0; t < BN / 32; ++t)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const float p = fast_exp2(sacc[t][u][j] - mnew);
+            sacc[t][u][j] = p;
+            lsum += p;
+          }
+        l[u] = l[u] * alpha + lsum;
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) oacc[u][dt][j] *= alpha;
       }
-    l = l * alpha + lsum;
 #pragma unroll
-    for (int dt = 0; dt < ND; ++dt)
+      for (int s = 0; s < BN / 16; ++s) {
+        bf16x8 pf[QT];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
+        for (int u = 0; u < QT; ++u) pf[u] = pack_frag(sacc[s >> 1][u], 8 * (s & 1));
 #pragma unroll
-    for (int s = 0; s < BN / 16; ++s) {
-      const bf16x8 pf = pack_frag(sacc[s >> 1], 8 * (s & 1));
+        for (int dt = 0; dt < ND; ++dt) {
+          const bf16x8 a = ld_frag_tr(V, LDST, 16 * s, 32 * dt, lane);
 #pragma unroll
-      for (int dt = 0; dt < ND; ++dt)
-        oacc[dt] = mfma(ld_frag_tr(sv, LDST, 16 * s, 32 * dt, lane), pf, oacc[dt]);
+          for (int u = 0; u < QT; ++u) oacc[u][dt] = mfma(a, pf[u], oacc[u][dt]);
+        }
+      }
     }
+    if (more) {
+      pk.store(sk[st ^ 1], tid);
+      pv.store(sv[st ^ 1], tid);
+    }
+    __syncthreads();
   }
-  l += __shfl_xor(l, 32, 64);
-  if (qi < S) {
-    store_rows_T<HD>(o + (tok0 + qi) * ldo + static_cast<int64_t>(h) * HD, oacc, 1.f / l, hl);
-    if (lse != nullptr && hl == 0) lse[static_cast<int64_t>(bh) * S + qi] = (m + log2f(l)) * kLn2;
+#pragma unroll
+  for (int u = 0; u < QT; ++u) {
+    const int qi = qw + 32 * u + l32;
+    const float lt = xor32_sum(l[u]);
+    if (qi < S) {
+      store_rows_T<HD>(o + (tok0 + qi) * ldo + static_cast<int64_t>(h) * HD, oacc[u], 1.f / lt, hl);
+      if (lse != nullptr && hl == 0) lse[static_cast<int64_t>(bh) * S + qi] = (m[u] + log2f(lt)) * kLn2;
+    }
   }
 }
 
-// --------------------------------------------- backward: delta = rowsum(dO*O)
+// --------------------------------------- backward: delta = rowsum(dO*O), fp32
 template <typename T>
 __global__ __launch_bounds__(256) void k_attn_delta(const T* __restrict__ o, int64_t ldo,
                                                     const T* __restrict__ dO, int64_t lddo,
@@ -236,19 +328,24 @@ __global__ __launch_bounds__(256) void k_attn_delta(const T* __restrict__ o, int
 }
 
 // ------------------------------------------------------- backward: dQ (bf16)
-// Same tiling as the forward: block = 128 queries of one (batch, head).
+// Same tiling as the forward with one 32-query tile per wave:
 //   S^T = K Q^T, P^T = exp(S^T - lse), dP^T = V dO^T,
 //   dS^T = P^T (dP^T - delta), dQ^T += K^T dS^T, dQ = scale * dQ.
+// The prologue also forms delta = rowsum(dO * O) of its queries (the lane
+// holds half of each row; one exchange with lane i^32 completes it) and
+// stores it for the dK/dV kernel, which runs next on the same stream.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_bwd_dq(
     const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
-    const uint16_t* __restrict__ v, int64_t ldv, const uint16_t* __restrict__ dO, int64_t lddo,
-    const float* __restrict__ lse, const float* __restrict__ delta, uint16_t* __restrict__ dq,
-    int64_t lddq, int S, int nh, int group, float scale_log2, float scale) {
+    const uint16_t* __restrict__ v, int64_t ldv, const uint16_t* __restrict__ o, int64_t ldo,
+    const uint16_t* __restrict__ dO, int64_t lddo, const float* __restrict__ lse,
+    float* __restrict__ delta, uint16_t* __restrict__ dq, int64_t lddq, int S, int nh, int group,
+    float scale_log2, float scale) {
   constexpr int BM = 128, BN = 64, LDST = HD + 8, NS = HD / 16, ND = HD / 32;
-  __shared__ __align__(16) uint16_t sk[BN * LDST];
-  __shared__ __align__(16) uint16_t sv[BN * LDST];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hl = lane >> 5, l32 = lane & 31;
+  __shared__ __align__(16) uint16_t sk[2][BN * LDST];
+  __shared__ __align__(16) uint16_t sv[2][BN * LDST];
+  const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const int bh = blockIdx.y, b = bh / nh, h = bh - b * nh, kvh = h / group;
   const int q0 = (gridDim.x - 1 - blockIdx.x) * BM;
   const int qw = q0 + wave * 32, qi = qw + l32;
@@ -257,16 +354,31 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(
   bf16x8 qf[NS], gf[NS];
   float lse2 = 0.f, dl = 0.f;
   {
-    const uint16_t* qrow = q + (tok0 + qi) * ldq + static_cast<int64_t>(h) * HD + 8 * hl;
-    const uint16_t* grow = dO + (tok0 + qi) * lddo + static_cast<int64_t>(h) * HD + 8 * hl;
+    const int64_t col = static_cast<int64_t>(h) * HD + 8 * hl;
+    const uint16_t* qrow = q + (tok0 + qi) * ldq + col;
+    const uint16_t* grow = dO + (tok0 + qi) * lddo + col;
+    const uint16_t* orow = o + (tok0 + qi) * ldo + col;
+    float part = 0.f;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      qf[s] = qi < S ? ld_frag(qrow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
-      gf[s] = qi < S ? ld_frag(grow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
+      uint4 gz = make_uint4(0, 0, 0, 0), oz = make_uint4(0, 0, 0, 0);
+      qf[s] = as_bf16x8(gz);
+      if (qi < S) {
+        qf[s] = ld_frag(qrow + 16 * s);
+        gz = *reinterpret_cast<const uint4*>(grow + 16 * s);
+        oz = *reinterpret_cast<const uint4*>(orow + 16 * s);
+      }
+      gf[s] = as_bf16x8(gz);
+      float gv[8], ov[8];
+      Elem<uint16_t>::load8(reinterpret_cast<const uint16_t*>(&gz), gv);
+      Elem<uint16_t>::load8(reinterpret_cast<const uint16_t*>(&oz), ov);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part = fmaf(gv[e], ov[e], part);
     }
+    dl = xor32_sum(part);
     if (qi < S) {
       lse2 = lse[static_cast<int64_t>(bh) * S + qi] * kLog2e;
-      dl = delta[static_cast<int64_t>(bh) * S + qi];
+      if (hl == 0) delta[static_cast<int64_t>(bh) * S + qi] = dl;
     }
   }
   f32x16 dqacc[ND];
@@ -277,82 +389,108 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(
   const int nkb = (kend + BN - 1) / BN;
   const uint16_t* kb_ptr = k + tok0 * ldk + static_cast<int64_t>(kvh) * HD;
   const uint16_t* vb_ptr = v + tok0 * ldv + static_cast<int64_t>(kvh) * HD;
+  TileRegs<BN, HD, LDST, 256> pk, pv;
+  pk.load(kb_ptr, ldk, S, tid);
+  pv.load(vb_ptr, ldv, S, tid);
+  pk.store(sk[0], tid);
+  pv.store(sv[0], tid);
+  __syncthreads();
   for (int kb = 0; kb < nkb; ++kb) {
-    const int k0 = kb * BN;
-    __syncthreads();
-    copy_tile<HD, LDST>(sk, kb_ptr + static_cast<int64_t>(k0) * ldk, ldk, BN, S - k0, tid, 256);
-    copy_tile<HD, LDST>(sv, vb_ptr + static_cast<int64_t>(k0) * ldv, ldv, BN, S - k0, tid, 256);
-    __syncthreads();
-    if (k0 > qw + 31) continue;
-
-    f32x16 sacc[BN / 32], pacc[BN / 32];
-#pragma unroll
-    for (int t = 0; t < BN / 32; ++t) {
-      sacc[t] = zero16();
-      pacc[t] = zero16();
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        sacc[t] = mfma(ld_frag(sk + (32 * t + l32) * LDST + 16 * s + 8 * hl), qf[s], sacc[t]);
-        pacc[t] = mfma(ld_frag(sv + (32 * t + l32) * LDST + 16 * s + 8 * hl), gf[s], pacc[t]);
-      }
+    const int k0 = kb * BN, st = kb & 1;
+    const bool more = kb + 1 < nkb;
+    if (more) {
+      pk.load(kb_ptr + static_cast<int64_t>(k0 + BN) * ldk, ldk, S - k0 - BN, tid);
+      pv.load(vb_ptr + static_cast<int64_t>(k0 + BN) * ldv, ldv, S - k0 - BN, tid);
     }
-    const bool need_mask = (k0 + BN - 1 > qw) || (k0 + BN > S);
+    if (k0 <= qw + 31) {
+      const uint16_t* K = sk[st];
+      const uint16_t* V = sv[st];
+      const bool need_mask = (k0 + BN - 1 > qw) || (k0 + BN > S);
 #pragma unroll
-    for (int t = 0; t < BN / 32; ++t)
+      for (int t = 0; t < BN / 32; ++t) {
+        f32x16 sacc = zero16(), pacc = zero16();
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        float p = exp2f(sacc[t][j] * scale_log2 - lse2);
-        if (need_mask) {
-          const int key = k0 + 32 * t + acc_row(j, hl);
-          if (key > qi || key >= S) p = 0.f;
+        for (int s = 0; s < NS; ++s) {
+          sacc = mfma(ld_frag(K + (32 * t + l32) * LDST + 16 * s + 8 * hl), qf[s], sacc);
+          pacc = mfma(ld_frag(V + (32 * t + l32) * LDST + 16 * s + 8 * hl), gf[s], pacc);
         }
-        sacc[t][j] = p * (pacc[t][j] - dl);  // dS^T
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          float p = fast_exp2(sacc[j] * scale_log2 - lse2);
+          if (need_mask) {
+            const int key = k0 + 32 * t + acc_row(j, hl);
+            p = ((key > qi) | (key >= S)) ? 0.f : p;
+          }
+          sacc[j] = p * (pacc[j] - dl);  // dS^T
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const bf16x8 df = pack_frag(sacc, 8 * s2);
+#pragma unroll
+          for (int dt = 0; dt < ND; ++dt)
+            dqacc[dt] = mfma(ld_frag_tr(K, LDST, 32 * t + 16 * s2, 32 * dt, lane), df, dqacc[dt]);
+        }
       }
-#pragma unroll
-    for (int s = 0; s < BN / 16; ++s) {
-      const bf16x8 df = pack_frag(sacc[s >> 1], 8 * (s & 1));
-#pragma unroll
-      for (int dt = 0; dt < ND; ++dt)
-        dqacc[dt] = mfma(ld_frag_tr(sk, LDST, 16 * s, 32 * dt, lane), df, dqacc[dt]);
     }
+    if (more) {
+      pk.store(sk[st ^ 1], tid);
+      pv.store(sv[st ^ 1], tid);
+    }
+    __syncthreads();
   }
   if (qi < S) store_rows_T<HD>(dq + (tok0 + qi) * lddq + static_cast<int64_t>(h) * HD, dqacc, scale, hl);
 }
 
 // ---------------------------------------------------- backward: dK, dV (bf16)
-// Block = 4 waves x 32 keys of one (batch, kv head); K and V of the wave's keys
-// stay in registers.  Loop over the query heads of the group and over query
-// tiles of BQ at or after the block's first key:
+// Block = 8 waves of 32 keys each, for one (batch, kv head).  Causal work per
+// key block grows with the number of later queries, so a block pairs key
+// block j (waves 0-3) with key block nkb-1-j (waves 4-7): every SIMD hosts one
+// wave of each and all blocks carry the same work.  K and V of a wave's keys
+// stay in registers; the loop runs over the group's query heads and BQ-query
+// tiles (double-buffered in LDS, prefetched through registers):
 //   S = Q K^T, P = exp(S - lse), dP = dO V^T, dS = P (dP - delta),
 //   dV^T += dO^T P,  dK^T += Q^T dS,  dK = scale * dK.
-// Every kv head's gradient is complete inside one block: no atomics.
+// Each kv head's gradient is complete inside one block: no atomics.
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_bwd_dkdv(
+struct DkdvTiles {
+  static constexpr int BQ = HD <= 64 ? 64 : 32;
+  static constexpr int NWH = HD <= 64 ? 4 : 2;  // waves per key block (two key blocks per block)
+  static constexpr int NT = 2 * NWH * 64;
+};
+
+template <int HD>
+__global__ __launch_bounds__(DkdvTiles<HD>::NT) void k_attn_bwd_dkdv(
     const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
     const uint16_t* __restrict__ v, int64_t ldv, const uint16_t* __restrict__ dO, int64_t lddo,
     const float* __restrict__ lse, const float* __restrict__ delta, uint16_t* __restrict__ dk,
     int64_t lddk, uint16_t* __restrict__ dv, int64_t lddv, int S, int nh, int nkv, int group,
     float scale_log2, float scale) {
-  constexpr int BKN = 128, BQ = (HD >= 128 ? 32 : 64), LDST = HD + 8, NS = HD / 16, ND = HD / 32;
+  constexpr int NWH = DkdvTiles<HD>::NWH, NT = DkdvTiles<HD>::NT;
+  constexpr int BKN = NWH * 32, BQ = DkdvTiles<HD>::BQ, LDST = HD + 8, NS = HD / 16, ND = HD / 32;
   constexpr int NQT = BQ / 32;
-  __shared__ __align__(16) uint16_t sq[BQ * LDST];
-  __shared__ __align__(16) uint16_t sg[BQ * LDST];
-  __shared__ __align__(16) float slse[BQ];
-  __shared__ __align__(16) float sdl[BQ];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hl = lane >> 5, l32 = lane & 31;
+  __shared__ __align__(16) uint16_t sq[2][BQ * LDST];
+  __shared__ __align__(16) uint16_t sg[2][BQ * LDST];
+  __shared__ __align__(16) float slse[2][BQ];
+  __shared__ __align__(16) float sdl[2][BQ];
+  const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const int bk = blockIdx.y, b = bk / nkv, kvh = bk - b * nkv;
-  const int kblk0 = blockIdx.x * BKN;  // key block 0 has the most work; launched first
-  const int kw = kblk0 + wave * 32, ki = kw + l32;
+  const int nkb = (S + BKN - 1) / BKN;
+  const int jlo = blockIdx.x, jhi = nkb - 1 - blockIdx.x;
+  const bool upper = wave >= NWH;
+  const bool has_keys = !upper || jhi > jlo;
+  const int kw = (upper ? jhi : jlo) * BKN + (wave % NWH) * 32, ki = kw + l32;
   const int64_t tok0 = static_cast<int64_t>(b) * S;
 
   bf16x8 kf[NS], vf[NS];
   {
+    const bool ok = has_keys && ki < S;
     const uint16_t* krow = k + (tok0 + ki) * ldk + static_cast<int64_t>(kvh) * HD + 8 * hl;
     const uint16_t* vrow = v + (tok0 + ki) * ldv + static_cast<int64_t>(kvh) * HD + 8 * hl;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      kf[s] = ki < S ? ld_frag(krow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
-      vf[s] = ki < S ? ld_frag(vrow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
+      kf[s] = ok ? ld_frag(krow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
+      vf[s] = ok ? ld_frag(vrow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
     }
   }
   f32x16 dkacc[ND], dvacc[ND];
@@ -362,51 +500,71 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dkdv(
     dvacc[dt] = zero16();
   }
 
-  const int qt_begin = kblk0 / BQ;
-  const int nqt = (S + BQ - 1) / BQ;
-  for (int hh = 0; hh < group; ++hh) {
-    const int h = kvh * group + hh;
-    const int64_t row_lse = (static_cast<int64_t>(b) * nh + h) * S;
-    const uint16_t* qh = q + tok0 * ldq + static_cast<int64_t>(h) * HD;
-    const uint16_t* gh = dO + tok0 * lddo + static_cast<int64_t>(h) * HD;
-    for (int qt = qt_begin; qt < nqt; ++qt) {
-      const int q0 = qt * BQ;
-      __syncthreads();
-      copy_tile<HD, LDST>(sq, qh + static_cast<int64_t>(q0) * ldq, ldq, BQ, S - q0, tid, 256);
-      copy_tile<HD, LDST>(sg, gh + static_cast<int64_t>(q0) * lddo, lddo, BQ, S - q0, tid, 256);
-      if (tid < BQ) {
-        const bool ok = q0 + tid < S;
-        slse[tid] = ok ? lse[row_lse + q0 + tid] * kLog2e : 0.f;
-        sdl[tid] = ok ? delta[row_lse + q0 + tid] : 0.f;
-      }
-      __syncthreads();
-      if (q0 + BQ - 1 < kw) continue;  // every query precedes this wave's first key
-
+  // iteration space: (query head of the group) x (query tiles from the first key of block jlo)
+  const int qt0 = (jlo * BKN) / BQ;
+  const int nqt = (S + BQ - 1) / BQ - qt0;
+  const int n_it = group * nqt;
+  TileRegs<BQ, HD, LDST, NT> pq, pg;
+  float pl = 0.f, pd = 0.f;  // lse / delta of the tile in flight (threads 0..BQ-1)
+  auto fetch = [&](int it) {
+    const int hh = it / nqt, qt = qt0 + (it - hh * nqt);
+    const int h = kvh * group + hh, qs = qt * BQ;
+    const int64_t col = static_cast<int64_t>(h) * HD;
+    pq.load(q + (tok0 + qs) * ldq + col, ldq, S - qs, tid);
+    pg.load(dO + (tok0 + qs) * lddo + col, lddo, S - qs, tid);
+    if (tid < BQ) {
+      const int64_t row = (static_cast<int64_t>(b) * nh + h) * S + qs + tid;
+      const bool ok = qs + tid < S;
+      pl = ok ? lse[row] * kLog2e : 0.f;
+      pd = ok ? delta[row] : 0.f;
+    }
+  };
+  auto commit = [&](int st) {
+    pq.store(sq[st], tid);
+    pg.store(sg[st], tid);
+    if (tid < BQ) {
+      slse[st][tid] = pl;
+      sdl[st][tid] = pd;
+    }
+  };
+  if (n_it > 0) {
+    fetch(0);
+    commit(0);
+  }
+  __syncthreads();
+  for (int it = 0; it < n_it; ++it) {
+    const int st = it & 1;
+    const bool more = it + 1 < n_it;
+    if (more) fetch(it + 1);
+    const int q0 = (qt0 + it % nqt) * BQ;
+    if (has_keys && q0 + BQ - 1 >= kw) {  // some query of the tile reaches this wave's keys
+      const uint16_t* Q = sq[st];
+      const uint16_t* G = sg[st];
       const bool need_mask = (q0 < kw + 31) || (q0 + BQ > S) || (kw + 32 > S);
 #pragma unroll
       for (int u = 0; u < NQT; ++u) {
         f32x16 sacc = zero16(), pacc = zero16();
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-          sacc = mfma(ld_frag(sq + (32 * u + l32) * LDST + 16 * s + 8 * hl), kf[s], sacc);
-          pacc = mfma(ld_frag(sg + (32 * u + l32) * LDST + 16 * s + 8 * hl), vf[s], pacc);
+          sacc = mfma(ld_frag(Q + (32 * u + l32) * LDST + 16 * s + 8 * hl), kf[s], sacc);
+          pacc = mfma(ld_frag(G + (32 * u + l32) * LDST + 16 * s + 8 * hl), vf[s], pacc);
         }
-        // lane holds rows q = 32u + acc_row(j, hl) of column key ki
+        // this lane holds rows q = q0 + 32u + acc_row(j, hl) of column key ki
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const float4 L4 = *reinterpret_cast<const float4*>(slse + 32 * u + 8 * g + 4 * hl);
-          const float4 D4 = *reinterpret_cast<const float4*>(sdl + 32 * u + 8 * g + 4 * hl);
+          const float4 L4 = *reinterpret_cast<const float4*>(&slse[st][32 * u + 8 * g + 4 * hl]);
+          const float4 D4 = *reinterpret_cast<const float4*>(&sdl[st][32 * u + 8 * g + 4 * hl]);
           const float Lv[4] = {L4.x, L4.y, L4.z, L4.w};
           const float Dv[4] = {D4.x, D4.y, D4.z, D4.w};
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int j = 4 * g + e;
-            float p = exp2f(sacc[j] * scale_log2 - Lv[e]);
+            float p = fast_exp2(sacc[j] * scale_log2 - Lv[e]);
             if (need_mask) {
               const int qa = q0 + 32 * u + 8 * g + 4 * hl + e;
-              if (ki > qa || qa >= S || ki >= S) p = 0.f;
+              p = ((ki > qa) | (qa >= S) | (ki >= S)) ? 0.f : p;
             }
-            sacc[j] = p;                     // P
+            sacc[j] = p;                      // P
             pacc[j] = p * (pacc[j] - Dv[e]);  // dS
           }
         }
@@ -416,14 +574,16 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dkdv(
           const bf16x8 df = pack_frag(pacc, 8 * s2);
 #pragma unroll
           for (int dt = 0; dt < ND; ++dt) {
-            dvacc[dt] = mfma(ld_frag_tr(sg, LDST, 32 * u + 16 * s2, 32 * dt, lane), pf, dvacc[dt]);
-            dkacc[dt] = mfma(ld_frag_tr(sq, LDST, 32 * u + 16 * s2, 32 * dt, lane), df, dkacc[dt]);
+            dvacc[dt] = mfma(ld_frag_tr(G, LDST, 32 * u + 16 * s2, 32 * dt, lane), pf, dvacc[dt]);
+            dkacc[dt] = mfma(ld_frag_tr(Q, LDST, 32 * u + 16 * s2, 32 * dt, lane), df, dkacc[dt]);
           }
         }
       }
     }
+    if (more) commit(st ^ 1);
+    __syncthreads();
   }
-  if (ki < S) {
+  if (has_keys && ki < S) {
     store_rows_T<HD>(dk + (tok0 + ki) * lddk + static_cast<int64_t>(kvh) * HD, dkacc, scale, hl);
     store_rows_T<HD>(dv + (tok0 + ki) * lddv + static_cast<int64_t>(kvh) * HD, dvacc, 1.f, hl);
   }
@@ -596,8 +756,10 @@ extern "C" int fh_attn_fwd(fh_dtype dt, const void* q, int64_t ldq, const void* 
   const int S = static_cast<int>(seq_len), nh = static_cast<int>(n_heads);
   const int group = static_cast<int>(n_heads / n_kv_heads);
   if (dt == FH_BF16) {
-    const dim3 grid(static_cast<unsigned>((seq_len + 127) / 128), static_cast<unsigned>(batch * n_heads));
     dispatch_hd(head_dim, [&](auto hdc) {
+      constexpr int BM = 4 * 32 * FwdTiles<hdc()>::QT;
+      const dim3 grid(static_cast<unsigned>((seq_len + BM - 1) / BM),
+                      static_cast<unsigned>(batch * n_heads));
       hipLaunchKernelGGL((k_attn_fwd<hdc()>), grid, dim3(256), 0, stream,
                          static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(k), ldk,
                          static_cast<const uint16_t*>(v), ldv, static_cast<uint16_t*>(o), ldo, lse,
@@ -643,29 +805,29 @@ extern "C" int fh_attn_bwd(fh_dtype dt, const void* q, int64_t ldq, const void* 
   const int S = static_cast<int>(seq_len), nh = static_cast<int>(n_heads);
   const int nkv = static_cast<int>(n_kv_heads), group = static_cast<int>(n_heads / n_kv_heads);
   float* delta = static_cast<float*>(workspace);
-  const int64_t tokens = batch * seq_len;
-  const unsigned dblocks = static_cast<unsigned>((tokens * n_heads + 255) / 256);
   if (dt == FH_BF16) {
-    hipLaunchKernelGGL((k_attn_delta<uint16_t>), dim3(dblocks), dim3(256), 0, stream,
-                       static_cast<const uint16_t*>(o), ldo, static_cast<const uint16_t*>(dout),
-                       lddo, delta, S, nh, static_cast<int>(head_dim), tokens);
+    // dQ first: its prologue writes delta = rowsum(dO*O), which dK/dV reads.
     const dim3 gq(static_cast<unsigned>((seq_len + 127) / 128), static_cast<unsigned>(batch * n_heads));
-    const dim3 gk(static_cast<unsigned>((seq_len + 127) / 128), static_cast<unsigned>(batch * n_kv_heads));
     dispatch_hd(head_dim, [&](auto hdc) {
-      hipLaunchKernelGGL((k_attn_bwd_dkdv<hdc()>), gk, dim3(256), 0, stream,
+      using DT = DkdvTiles<hdc()>;
+      const int64_t nkb = (seq_len + DT::NWH * 32 - 1) / (DT::NWH * 32);
+      const dim3 gk(static_cast<unsigned>((nkb + 1) / 2), static_cast<unsigned>(batch * n_kv_heads));
+      hipLaunchKernelGGL((k_attn_bwd_dq<hdc()>), gq, dim3(256), 0, stream,
+                         static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(k), ldk,
+                         static_cast<const uint16_t*>(v), ldv, static_cast<const uint16_t*>(o), ldo,
+                         static_cast<const uint16_t*>(dout), lddo, lse, delta,
+                         static_cast<uint16_t*>(dq), lddq, S, nh, group, scale * kLog2e, scale);
+      hipLaunchKernelGGL((k_attn_bwd_dkdv<hdc()>), gk, dim3(DT::NT), 0, stream,
                          static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(k), ldk,
                          static_cast<const uint16_t*>(v), ldv, static_cast<const uint16_t*>(dout),
                          lddo, lse, delta, static_cast<uint16_t*>(dk), lddk,
                          static_cast<uint16_t*>(dv), lddv, S, nh, nkv, group, scale * kLog2e,
                          scale);
-      hipLaunchKernelGGL((k_attn_bwd_dq<hdc()>), gq, dim3(256), 0, stream,
-                         static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(k), ldk,
-                         static_cast<const uint16_t*>(v), ldv, static_cast<const uint16_t*>(dout),
-                         lddo, lse, delta, static_cast<uint16_t*>(dq), lddq, S, nh, group,
-                         scale * kLog2e, scale);
       return 0;
     });
   } else {
+    const int64_t tokens = batch * seq_len;
+    const unsigned dblocks = static_cast<unsigned>((tokens * n_heads + 255) / 256);
     hipLaunchKernelGGL((k_attn_delta<float>), dim3(dblocks), dim3(256), 0, stream,
                        static_cast<const float*>(o), ldo, static_cast<const float*>(dout), lddo,
                        delta, S, nh, static_cast<int>(head_dim), tokens);
