@@ -39,6 +39,19 @@ struct Elem;
 template <>
 struct Elem<uint16_t> {
   static constexpr fh_dtype kDtype = FH_BF16;
+  // 8 elements as loaded (kept packed in registers until needed).
+  using Raw = uint4;
+  __device__ __forceinline__ static Raw ldraw(const uint16_t* p) {
+    return *reinterpret_cast<const uint4*>(p);
+  }
+  __device__ __forceinline__ static void unpack(const Raw& q, float v[8]) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
   __device__ __forceinline__ static void load8(const uint16_t* p, float v[8]) {
     const uint4 q = *reinterpret_cast<const uint4*>(p);
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
@@ -65,6 +78,16 @@ struct Elem<uint16_t> {
 template <>
 struct Elem<float> {
   static constexpr fh_dtype kDtype = FH_F32;
+  struct Raw {
+    float4 a, b;
+  };
+  __device__ __forceinline__ static Raw ldraw(const float* p) {
+    return Raw{*reinterpret_cast<const float4*>(p), *reinterpret_cast<const float4*>(p + 4)};
+  }
+  __device__ __forceinline__ static void unpack(const Raw& q, float v[8]) {
+    v[0] = q.a.x; v[1] = q.a.y; v[2] = q.a.z; v[3] = q.a.w;
+    v[4] = q.b.x; v[5] = q.b.y; v[6] = q.b.z; v[7] = q.b.w;
+  }
   __device__ __forceinline__ static void load8(const float* p, float v[8]) {
     const float4 a = *reinterpret_cast<const float4*>(p);
     const float4 b = *reinterpret_cast<const float4*>(p + 4);

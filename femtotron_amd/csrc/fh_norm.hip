@@ -14,61 +14,90 @@ namespace {
 
 constexpr int kRowsPerBlock = 4;  // 4 waves = 256 threads
 
+// Rows per wave kept in flight (FH_NORM_FWD_ROWS).  One row per wave, i.e.
+// more waves, measured faster than two rows per wave at T=16384, H=2048
+// (4.76 vs 4.39 TB/s).
+#ifndef FH_NORM_FWD_ROWS
+#define FH_NORM_FWD_ROWS 1
+#endif
+template <int NV>
+struct FwdRows {
+  static constexpr int R = NV <= 4 ? FH_NORM_FWD_ROWS : 1;
+};
+
 template <typename T, int NV, bool ADD>
 __global__ __launch_bounds__(256) void k_rmsnorm_fwd(
     const T* __restrict__ x, const T* __restrict__ a, const T* __restrict__ w,
     T* __restrict__ h, T* __restrict__ y, float* __restrict__ rstd,
     int64_t rows, int cols, float eps) {
+  constexpr int R = FwdRows<NV>::R;
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
-  if (row >= rows) return;  // uniform per wave
-  const int64_t base = row * cols;
+  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6)) * R;
+  if (row0 >= rows) return;  // uniform per wave
 
-  float v[NV][8];
-  float ss = 0.f;
+  float v[R][NV][8];
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int c = (i * kWave + lane) * 8;
-    if (c < cols) {
-      Elem<T>::load8(x + base + c, v[i]);
-      if constexpr (ADD) {
-        float b[8];
-        Elem<T>::load8(a + base + c, b);
+  for (int k = 0; k < R; ++k) {
+    const int64_t base = (row0 + k) * cols;
+    const bool ok = row0 + k < rows;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[i][j] = Elem<T>::rnd(v[i][j] + b[j]);
-        Elem<T>::store8(h + base + c, v[i]);
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * kWave + lane) * 8;
+      if (ok && c < cols) {
+        Elem<T>::load8(x + base + c, v[k][i]);
+        if constexpr (ADD) {
+          float b[8];
+          Elem<T>::load8(a + base + c, b);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[k][i][j] = Elem<T>::rnd(v[k][i][j] + b[j]);
+          Elem<T>::store8(h + base + c, v[k][i]);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[k][i][j] = 0.f;
       }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) ss = fmaf(v[i][j], v[i][j], ss);
     }
   }
-  ss = wave_sum(ss);
-  const float r = rsqrtf(ss / static_cast<float>(cols) + eps);
-
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int c = (i * kWave + lane) * 8;
-    if (c < cols) {
-      float wv[8], o[8];
-      Elem<T>::load8(w + c, wv);
+  for (int k = 0; k < R; ++k) {
+    if (row0 + k >= rows) break;  // uniform per wave
+    const int64_t base = (row0 + k) * cols;
+    float ss = 0.f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] = Elem<T>::rnd(wv[j] * Elem<T>::rnd(v[i][j] * r));
-      Elem<T>::store8(y + base + c, o);
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss = fmaf(v[k][i][j], v[k][i][j], ss);
+    ss = wave_sum(ss);
+    const float r = rsqrtf(ss / static_cast<float>(cols) + eps);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * kWave + lane) * 8;
+      if (c < cols) {
+        float wv[8], o[8];
+        Elem<T>::load8(w + c, wv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = Elem<T>::rnd(wv[j] * Elem<T>::rnd(v[k][i][j] * r));
+        Elem<T>::store8(y + base + c, o);
+      }
     }
+    if (rstd != nullptr && lane == 0) rstd[row0 + k] = r;
   }
-  if (rstd != nullptr && lane == 0) rstd[row] = r;
 }
 
-// Backward.  Each wave walks rows row0, row0 + 4*gridDim.x, ... and keeps
-// its share of the weight gradient in registers; the 4 waves of a block are
-// then summed in a fixed order through LDS into one fp32 partial row per
-// block (deterministic), which k_reduce_cols folds into dw.
+// Backward.  Each wave walks row pairs (row0, row0 + S), (row0 + 2S, ...) with
+// S = 4*gridDim.x, issuing all loads of a pair (x, dy and the residual
+// gradient, kept packed until used) before the first reduction, and keeps its
+// share of the weight gradient in registers; the 4 waves of a block are then
+// summed in a fixed order through LDS into one fp32 partial row per block
+// (deterministic), which k_reduce_cols folds into dw.
 template <typename T, int NV, bool RES, bool HAVE_RSTD>
 __global__ __launch_bounds__(256) void k_rmsnorm_bwd(
     const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ w,
     const float* __restrict__ rstd, const T* __restrict__ dres,
     T* __restrict__ dx, float* __restrict__ part, int64_t rows, int cols,
     float eps) {
+  using Raw = typename Elem<T>::Raw;
+  constexpr int R = NV <= 4 ? 2 : 1;
   extern __shared__ float lds_acc[];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
@@ -80,66 +109,86 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd(
     for (int j = 0; j < 8; ++j) acc[i][j] = 0.f;
 
   const float inv_cols = 1.f / static_cast<float>(cols);
-  for (int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + wave; row < rows;
-       row += static_cast<int64_t>(gridDim.x) * kRowsPerBlock) {
-    const int64_t base = row * cols;
-    float xv[NV][8], gv[NV][8];
-    float ss = 0.f;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kRowsPerBlock;
+  for (int64_t row0 = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + wave; row0 < rows;
+       row0 += R * stride) {
+    Raw xr[R][NV], gr[R][NV], rr[R][NV];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int c = (i * kWave + lane) * 8;
-      if (c < cols) {
-        Elem<T>::load8(x + base + c, xv[i]);
-        Elem<T>::load8(dy + base + c, gv[i]);
-        if constexpr (!HAVE_RSTD) {
+    for (int k = 0; k < R; ++k) {
+      const int64_t row = row0 + k * stride;
+      const int64_t base = row * cols;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) ss = fmaf(xv[i][j], xv[i][j], ss);
+      for (int i = 0; i < NV; ++i) {
+        const int c = (i * kWave + lane) * 8;
+        if (row < rows && c < cols) {
+          xr[k][i] = Elem<T>::ldraw(x + base + c);
+          gr[k][i] = Elem<T>::ldraw(dy + base + c);
+          if constexpr (RES) rr[k][i] = Elem<T>::ldraw(dres + base + c);
         }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const int64_t row = row0 + k * stride;
+      if (row >= rows) break;  // uniform per wave
+      const int64_t base = row * cols;
+      float r;
+      if constexpr (HAVE_RSTD) {
+        r = rstd[row];
       } else {
+        float ss = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xv[i][j] = gv[i][j] = 0.f;
+        for (int i = 0; i < NV; ++i) {
+          if ((i * kWave + lane) * 8 < cols) {
+            float xv[8];
+            Elem<T>::unpack(xr[k][i], xv);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ss = fmaf(xv[j], xv[j], ss);
+          }
+        }
+        r = rsqrtf(wave_sum(ss) * inv_cols + eps);
       }
-    }
-    float r;
-    if constexpr (HAVE_RSTD) {
-      r = rstd[row];
-    } else {
-      r = rsqrtf(wave_sum(ss) * inv_cols + eps);
-    }
-    // dn = to_dtype(dy*w) is the gradient arriving at the bf16 normalised
-    // value; dot = mean(dn * n) over the row.
-    float dot = 0.f;
+      // dn = to_dtype(dy*w) is the gradient arriving at the bf16 normalised
+      // value; dot = mean(dn * n) over the row.
+      float dot = 0.f;
+      float dn[NV][8];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int c = (i * kWave + lane) * 8;
-      if (c < cols) {
-        float wv[8];
-        Elem<T>::load8(w + c, wv);
+      for (int i = 0; i < NV; ++i) {
+        const int c = (i * kWave + lane) * 8;
+        if (c < cols) {
+          float wv[8], xv[8], gv[8];
+          Elem<T>::load8(w + c, wv);
+          Elem<T>::unpack(xr[k][i], xv);
+          Elem<T>::unpack(gr[k][i], gv);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float n = xv[i][j] * r;
-          const float dn = Elem<T>::rnd(gv[i][j] * wv[j]);
-          acc[i][j] = fmaf(gv[i][j], Elem<T>::rnd(n), acc[i][j]);
-          dot = fmaf(dn, n, dot);
-          gv[i][j] = dn;  // keep dn, dy is no longer needed
+          for (int j = 0; j < 8; ++j) {
+            const float n = xv[j] * r;
+            dn[i][j] = Elem<T>::rnd(gv[j] * wv[j]);
+            acc[i][j] = fmaf(gv[j], Elem<T>::rnd(n), acc[i][j]);
+            dot = fmaf(dn[i][j], n, dot);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) dn[i][j] = 0.f;
         }
       }
-    }
-    dot = wave_sum(dot) * inv_cols;
+      dot = wave_sum(dot) * inv_cols;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int c = (i * kWave + lane) * 8;
-      if (c < cols) {
-        float o[8];
+      for (int i = 0; i < NV; ++i) {
+        const int c = (i * kWave + lane) * 8;
+        if (c < cols) {
+          float xv[8], o[8];
+          Elem<T>::unpack(xr[k][i], xv);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = r * (gv[i][j] - xv[i][j] * r * dot);
-        if constexpr (RES) {
-          float rv[8];
-          Elem<T>::load8(dres + base + c, rv);
+          for (int j = 0; j < 8; ++j) o[j] = r * (dn[i][j] - xv[j] * r * dot);
+          if constexpr (RES) {
+            float rv[8];
+            Elem<T>::unpack(rr[k][i], rv);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) o[j] += rv[j];
+            for (int j = 0; j < 8; ++j) o[j] += rv[j];
+          }
+          Elem<T>::store8(dx + base + c, o);
         }
-        Elem<T>::store8(dx + base + c, o);
       }
     }
   }
@@ -186,7 +235,13 @@ __global__ __launch_bounds__(1024) void k_reduce_cols(const float* __restrict__ 
   }
 }
 
-constexpr int kMaxBwdBlocks = 1024;
+// Backward grid cap: fewer blocks mean fewer fp32 dw partial rows for
+// k_reduce_cols; 512 blocks measured best at T=16384, H=2048 (4.05 TB/s for
+// both kernels together vs 3.43 at 1024 and 3.74 at 256).
+#ifndef FH_NORM_BWD_BLOCKS
+#define FH_NORM_BWD_BLOCKS 512
+#endif
+constexpr int kMaxBwdBlocks = FH_NORM_BWD_BLOCKS;
 
 int bwd_blocks(int64_t rows) {
   const int64_t need = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
@@ -196,7 +251,8 @@ int bwd_blocks(int64_t rows) {
 template <typename T, int NV>
 void launch_fwd(const void* x, const void* a, const void* w, void* h, void* y, float* rstd,
                 int64_t rows, int cols, float eps, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock));
+  const int64_t per_block = static_cast<int64_t>(kRowsPerBlock) * FwdRows<NV>::R;
+  const dim3 grid(static_cast<unsigned>((rows + per_block - 1) / per_block));
   if (a != nullptr) {
     hipLaunchKernelGGL((k_rmsnorm_fwd<T, NV, true>), grid, dim3(256), 0, s,
                        static_cast<const T*>(x), static_cast<const T*>(a),
