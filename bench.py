@@ -263,7 +263,6 @@ def main() -> int:
     assert counts["fallback"] == 0 and counts["fused"] == args.layers * (args.steps + args.warmup), counts
     tok_s = T / sec
     log(f"fused: {sec * 1e3:.2f} ms/step, {tok_s:.0f} tokens/s")
-    act_fused = activation_bytes_per_token(torch, model, ids)
 
     log("per-kernel HIP-event timings at the step's shapes")
     rows, mfma = kernel_table(torch, args.kernel_iters)
@@ -274,18 +273,29 @@ def main() -> int:
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["frac"], "traffic": None,
                 "bytes_per_launch": dom["bytes_per_launch"]}
 
+    def use(fused: bool):
+        remove_activation_checkpointing(model)
+        if fused:
+            apply_activation_checkpointing(model, policy, checkpoint_fn=fused_checkpoint)
+        else:
+            apply_activation_checkpointing(model, policy)  # default checkpoint_fn = torch's
+        torch.cuda.empty_cache()
+
     ref = None
     if args.reference_steps > 0:
         log("reference path on the same GPU: HF layers under torch.utils.checkpoint(debug=True)")
-        remove_activation_checkpointing(model)
-        apply_activation_checkpointing(model, policy)  # default checkpoint_fn = torch's
-        torch.cuda.empty_cache()
+        use(False)
         rsec = time_steps(torch, model, ids, args.reference_steps, 1)
-        act_ref = activation_bytes_per_token(torch, model, ids)
         ref = {"tokens_per_s": round(T / rsec, 1), "ms_per_step": round(rsec * 1e3, 2),
-               "activation_bytes_per_token": round(act_ref, 1),
                "speedup_fused_vs_reference": round(rsec / sec, 2)}
         log(f"reference: {rsec * 1e3:.1f} ms/step")
+    # Activation memory, measured back to back for both paths in the same
+    # allocator state (each after one step of its own to allocate gradients).
+    use(True)
+    act_fused = activation_bytes_per_token(torch, model, ids)
+    if ref is not None:
+        use(False)
+        ref["activation_bytes_per_token"] = round(activation_bytes_per_token(torch, model, ids), 1)
     del model
     torch.cuda.empty_cache()
 
