@@ -55,6 +55,11 @@ def parse_args():
                     help="timed steps of the reference path on the GPU (0 to skip)")
     ap.add_argument("--cpu-sample-tokens", type=int, default=512,
                     help="tokens (one sequence) of the CPU baseline sample (0 to skip)")
+    ap.add_argument("--profile-kernel", default=None,
+                    help="launch only this fused kernel (swiglu_fwd, swiglu_bwd, rmsnorm_fwd, "
+                         "add_rmsnorm_fwd, rmsnorm_bwd, rope_fwd, residual_add, attn_fwd, attn_bwd) at "
+                         "the step's shape, after a 1 GiB device copy that calibrates HBM byte "
+                         "counters, for rocprofv3 --pmc runs; prints one JSON line and exits")
     return ap.parse_args()
 
 
@@ -98,6 +103,17 @@ def activation_bytes_per_token(torch, model, ids) -> float:
     model(ids, labels=ids)["loss"].backward()
     torch.cuda.synchronize()
     return (torch.cuda.max_memory_allocated() - base) / ids.numel()
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` measured by rocprofv3 --pmc FETCH_SIZE and
+    WRITE_SIZE runs (calibrated against a 1 GiB copy), as recorded in
+    profiles/hbm_traffic.json; None if that kernel was not measured."""
+    path = ROOT / "profiles" / "hbm_traffic.json"
+    try:
+        return json.loads(path.read_text())["kernels"][kernel]["traffic_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def event_ms(torch, fn, iters: int) -> float:
@@ -206,6 +222,74 @@ def kernel_table(torch, iters: int):
     return rows, mfma
 
 
+def profile_kernel(torch, name: str, launches: int = 10) -> dict:
+    """A 1 GiB device-to-device copy (known traffic: 1 GiB read + 1 GiB written),
+    then `launches` launches of one fused kernel at the TinyLlama step's shape,
+    each on a fresh buffer set.  Under rocprofv3 --pmc FETCH_SIZE (or WRITE_SIZE)
+    the copy's reading calibrates the counter's units."""
+    from femtotron_amd import ops
+    c = TINYLLAMA
+    T, H, F = c["batch"] * c["seq"], c["hidden"], c["ffn"]
+    nh, nkv, hd = c["heads"], c["kv"], c["hidden"] // c["heads"]
+    Hq, Hkv = nh * hd, nkv * hd
+    dev, bf = "cuda", torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(3)
+
+    def rnd(*shape):
+        return torch.randn(*shape, device=dev, dtype=bf, generator=g)
+
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    n = launches
+    if name in ("swiglu_fwd", "swiglu_bwd"):
+        gus = [rnd(T, 2 * F) for _ in range(n)]
+        if name == "swiglu_fwd":
+            fn = lambda i: ops.swiglu_fwd(gus[i][:, :F], gus[i][:, F:])
+            nbytes = 6 * T * F
+        else:
+            dps = [rnd(T, F) for _ in range(n)]
+            out = torch.empty(T, 2 * F, device=dev, dtype=bf)
+            fn = lambda i: ops.swiglu_bwd(dps[i], gus[i][:, :F], gus[i][:, F:], out[:, :F], out[:, F:])
+            nbytes = 10 * T * F
+    elif name in ("rmsnorm_fwd", "add_rmsnorm_fwd", "rmsnorm_bwd", "residual_add"):
+        xs = [rnd(T, H) for _ in range(n)]
+        as_ = [rnd(T, H) for _ in range(n)]
+        w = (1 + 0.02 * rnd(H)).contiguous()
+        fn = {"rmsnorm_fwd": lambda i: ops.rmsnorm_fwd(xs[i], w, 1e-5),
+              "add_rmsnorm_fwd": lambda i: ops.add_rmsnorm_fwd(xs[i], as_[i], w, 1e-5),
+              "rmsnorm_bwd": lambda i: ops.rmsnorm_bwd(as_[i], xs[i], w, 1e-5, dres=as_[(i + 1) % n]),
+              "residual_add": lambda i: ops.add(xs[i], as_[i])}[name]
+        nbytes = {"rmsnorm_fwd": 4, "add_rmsnorm_fwd": 8, "rmsnorm_bwd": 8, "residual_add": 6}[name] * T * H
+    elif name == "rope_fwd":
+        qkvs = [rnd(T, Hq + 2 * Hkv) for _ in range(n)]
+        cos = rnd(1, c["seq"], hd)
+        sin = rnd(1, c["seq"], hd)
+        fn = lambda i: ops.rope_fwd_(qkvs[i], nh + nkv, hd, c["seq"], cos, sin)
+        nbytes = 4 * T * (Hq + Hkv)
+    elif name in ("attn_fwd", "attn_bwd"):
+        qkv = rnd(T, Hq + 2 * Hkv)
+        q, k, v = qkv[:, :Hq], qkv[:, Hq:Hq + Hkv], qkv[:, Hq + Hkv:]
+        o, lse = ops.attn_fwd(q, k, v, c["batch"], c["seq"], nh, nkv, hd, hd ** -0.5)
+        do = rnd(T, Hq)
+        dqkv = torch.empty_like(qkv)
+        if name == "attn_fwd":
+            fn = lambda i: ops.attn_fwd(q, k, v, c["batch"], c["seq"], nh, nkv, hd, hd ** -0.5)
+        else:
+            fn = lambda i: ops.attn_bwd(q, k, v, o, do, lse, dqkv[:, :Hq], dqkv[:, Hq:Hq + Hkv],
+                                        dqkv[:, Hq + Hkv:], c["batch"], c["seq"], nh, nkv, hd, hd ** -0.5)
+        nbytes = None
+    else:
+        raise SystemExit(f"unknown kernel {name!r}")
+    torch.cuda.synchronize()
+    for i in range(n):
+        fn(i)
+    torch.cuda.synchronize()
+    return {"profile_kernel": name, "launches": n, "algorithmic_bytes_per_launch": nbytes,
+            "calibration_copy_bytes": 1 << 30, "shape": {"tokens": T, "hidden": H, "ffn": F}}
+
+
 def cpu_baseline(torch, n_tokens: int) -> dict:
     """Reference-equivalent path on the host: oracle Llama (HF layer math) with
     every layer under torch.utils.checkpoint(use_reentrant=False, debug=True), fp32."""
@@ -240,6 +324,10 @@ def main() -> int:
         return 2
     import torch
 
+    if args.profile_kernel:
+        print(json.dumps(profile_kernel(torch, args.profile_kernel)), flush=True)
+        return 0
+
     from femtotron_amd import dispatch_counts, fused_checkpoint, reset_dispatch_counts
     from femtotron_amd.model import build_llama_model, init_llama_weights_
     from femtotron_amd.scripts.presets import get_ac_policy
@@ -270,7 +358,8 @@ def main() -> int:
         r["ms_per_step"] = round(r["ms_per_launch"] * r["launches_per_step"] * args.layers / c["layers"], 4)
     dom = max(rows, key=lambda r: r["ms_per_step"])
     roofline = {"bound": "hbm", "kernel": dom["kernel"], "achieved": dom["achieved_gbs"],
-                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["frac"], "traffic": None,
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["frac"],
+                "traffic": measured_traffic(dom["kernel"]),
                 "bytes_per_launch": dom["bytes_per_launch"]}
 
     def use(fused: bool):
