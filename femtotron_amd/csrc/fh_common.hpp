@@ -104,10 +104,23 @@ struct Elem<float> {
 };
 
 // ------------------------------------------------------- wave reductions
+// DPP (data-parallel primitive) lane moves: VALU ops with no LDS round trip.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Sum over the 64 lanes of a wave, returned to every lane: quad swaps, half-row
+// and row mirrors give each 16-lane row its sum, row_bcast15/31 carry rows into
+// lane 63, and readlane broadcasts it.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
+  v += dpp<0xB1>(v);         // quad_perm [1,0,3,2]
+  v += dpp<0x4E>(v);         // quad_perm [2,3,0,1]
+  v += dpp<0x141>(v);        // row_half_mirror
+  v += dpp<0x140>(v);        // row_mirror
+  v += dpp<0x142, 0xa>(v);   // row_bcast:15 into rows 1 and 3
+  v += dpp<0x143, 0xc>(v);   // row_bcast:31 into rows 2 and 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 __device__ __forceinline__ float wave_max(float v) {

@@ -214,7 +214,8 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd(
   for (int c = threadIdx.x; c < cols; c += blockDim.x) dst[c] = lds_acc[c];
 }
 
-// dw[c] = sum_p part[p, c]; block = 64 columns x 16 waves, fixed order.
+// dw[c] = sum_p part[p, c]; block = 64 columns x 16 waves, fixed order.  Each
+// wave keeps 8 independent partial-row loads in flight.
 template <typename T>
 __global__ __launch_bounds__(1024) void k_reduce_cols(const float* __restrict__ part,
                                                       int nparts, int cols,
@@ -224,8 +225,17 @@ __global__ __launch_bounds__(1024) void k_reduce_cols(const float* __restrict__ 
   const int wave = threadIdx.x >> 6;
   const int c = blockIdx.x * 64 + lane;
   float s = 0.f;
-  if (c < cols)
-    for (int p = wave; p < nparts; p += 16) s += part[static_cast<int64_t>(p) * cols + c];
+  if (c < cols) {
+    int p = wave;
+    for (; p + 16 * 7 < nparts; p += 16 * 8) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = part[static_cast<int64_t>(p + 16 * k) * cols + c];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) s += v[k];
+    }
+    for (; p < nparts; p += 16) s += part[static_cast<int64_t>(p) * cols + c];
+  }
   red[wave][lane] = s;
   __syncthreads();
   if (wave == 0 && c < cols) {
