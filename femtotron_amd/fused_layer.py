@@ -56,6 +56,7 @@ def _mm_nt(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     return torch.mm(a, b.t())
 
 
+
 class _Acts:
     """Recomputed activations the backward needs."""
 
@@ -93,19 +94,55 @@ def layer_forward(x2: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, shp: L
     return ops.add(h, m, out=m)
 
 
+_side_streams: dict[int, torch.cuda.Stream] = {}
+
+
+class _WgradStream:
+    """Weight-gradient GEMMs on a side stream (default priority).
+
+    dW = dY^T X feeds nothing else in the layer's backward, so it can run next
+    to the input-gradient chain (dgrad GEMMs, the attention backward, the norm
+    backward) instead of in series with it.  Each GEMM waits for the main
+    stream's work queued so far; its operands are marked as used by the side
+    stream (so the caching allocator does not hand their memory back to the
+    main stream early) and its result as used by the main stream; join() makes
+    the main stream wait for every queued weight-gradient GEMM."""
+
+    def __init__(self, device: torch.device):
+        self.main = torch.cuda.current_stream(device)
+        side = _side_streams.get(device.index)
+        if side is None:
+            side = _side_streams[device.index] = torch.cuda.Stream(device=device)
+        self.side = side
+
+    def mm_tn(self, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+        """a^T @ b on the side stream."""
+        self.side.wait_stream(self.main)
+        with torch.cuda.stream(self.side):
+            out = torch.mm(a.t(), b)
+        a.record_stream(self.side)
+        b.record_stream(self.side)
+        out.record_stream(self.main)
+        return out
+
+    def join(self) -> None:
+        self.main.wait_stream(self.side)
+
+
 def layer_backward(dout2: torch.Tensor, x2: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                    shp: LayerShape, batch: int, seq: int, w: tuple, acts: _Acts):
     wq, wk, wv, wo, wg, wu, wd, w1, w2 = w
     F_ = shp.ffn
+    wg_stream = _WgradStream(dout2.device)
     # MLP: m = p Wd^T
-    dwd = torch.mm(dout2.t(), acts.p)
+    dwd = wg_stream.mm_tn(dout2, acts.p)
     dp = torch.mm(dout2, wd)
     acts.p = None
     dgu = torch.empty_like(acts.gu)
     ops.swiglu_bwd(dp, acts.gu[:, :F_], acts.gu[:, F_:], dgu[:, :F_], dgu[:, F_:])
     del dp
     acts.gu = None
-    dwgu = torch.mm(dgu.t(), acts.z)
+    dwgu = wg_stream.mm_tn(dgu, acts.z)
     dz = torch.mm(dgu, torch.cat((wg, wu), 0))
     del dgu
     acts.z = None
@@ -114,18 +151,18 @@ def layer_backward(dout2: torch.Tensor, x2: torch.Tensor, cos: torch.Tensor, sin
     del dz
     acts.h = None
     # attention output projection
-    dwo = torch.mm(dh.t(), acts.o)
+    dwo = wg_stream.mm_tn(dh, acts.o)
     do = torch.mm(dh, wo)
     dqkv = attention.attn_bwd(do, acts.qkv, acts.o, acts.lse, batch, seq, shp)
     del do
     acts.o = acts.lse = acts.qkv = None
     ops.rope_bwd_(dqkv, shp.n_heads + shp.n_kv_heads, shp.head_dim, seq, cos, sin)
-    wqkv = torch.cat((wq, wk, wv), 0)
-    dwqkv = torch.mm(dqkv.t(), acts.y1)
-    dy1 = torch.mm(dqkv, wqkv)
+    dwqkv = wg_stream.mm_tn(dqkv, acts.y1)
+    dy1 = torch.mm(dqkv, torch.cat((wq, wk, wv), 0))
     del dqkv
     acts.y1 = None
     dx, dw1 = ops.rmsnorm_bwd(dy1, x2, w1, shp.eps1, rstd=acts.rstd1, dres=dh)
+    wg_stream.join()
     hq, hkv = shp.hq, shp.hkv
     dwq, dwk, dwv = dwqkv[:hq], dwqkv[hq:hq + hkv], dwqkv[hq + hkv:]
     dwg, dwu = dwgu[:F_], dwgu[F_:]
