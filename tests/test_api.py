@@ -141,6 +141,33 @@ def test_fused_checkpoint_on_cpu_is_the_stock_checkpoint():
         fused_checkpoint(layer, x, use_reentrant=True, debug=True, position_embeddings=(cos, sin))
 
 
+def test_dispatcher_recognises_layer_mlp_and_norm_only():
+    """The fused path claims HF's decoder layer, MLP and RMSNorm (the modules the
+    full and selective presets wrap) and nothing else; a subclass that overrides
+    forward is not claimed.  On CPU tensors every call still falls back."""
+    from transformers.models.llama import modeling_llama as hf
+    from femtotron_amd.fused_checkpoint import _kind, _plan
+    cfg = llama_config(CFG1, layers=1)
+    layer = hf.LlamaDecoderLayer(cfg, 0)
+
+    class CustomMLP(hf.LlamaMLP):
+        def forward(self, x):
+            return super().forward(x) * 2
+
+    assert _kind(layer) == "layer"
+    assert _kind(layer.mlp) == "mlp"
+    assert _kind(layer.input_layernorm) == "norm"
+    assert _kind(layer.self_attn) is None
+    assert _kind(CustomMLP(cfg)) is None
+    assert "not an unmodified" in _plan(CustomMLP(cfg), (torch.randn(1, 4, 256),), {})
+    assert "HIP" in _plan(layer.mlp, (torch.randn(1, 4, 256),), {})
+    x = torch.randn(1, 4, 256, requires_grad=True)
+    reset_dispatch_counts()
+    y = fused_checkpoint(layer.mlp, x, use_reentrant=False, debug=True)
+    assert dispatch_counts() == {"fused": 0, "fallback": 1}
+    assert torch.equal(y, layer.mlp(x))
+
+
 # --------------------------------------------------------------- C ABI
 def _declared_symbols() -> set[str]:
     text = (ROOT / "include" / "femtohip.h").read_text()
