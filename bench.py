@@ -2,11 +2,16 @@
 """Benchmark: activation-checkpointed fwd+bwd tokens/s of the TinyLlama-1.1B-shaped
 model on one MI355X, through the fused HIP checkpoint path.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload W] [--ac full|selective]
 
 One step = forward (embed, 22 checkpointed decoder layers, final norm, lm_head,
 shifted fp32 cross-entropy) + backward (per-layer recompute + layer backward)
 over one synthetic micro-batch of 8 x 2048 token ids already resident in HBM.
+The default workload is the metric's (TinyLlama, every layer checkpointed);
+--workload llama3-8b-slice / llama2-7b-long run BASELINE configs 4 and 5 (an
+8-layer Llama-3-8B slice at 1 x 8192 tokens, a 4-layer Llama-2-7B slice at
+1 x 32768 tokens) and --ac selective the selective policy (MLP and norms
+checkpointed) instead of whole layers.
 Prints ONE JSON line.  Besides tokens/s it reports:
   * roofline: the fused memory-bound kernel with the largest share of step time,
     its algorithmic bytes per launch / its mean launch time (HIP events on the
@@ -37,6 +42,16 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 TINYLLAMA = dict(hidden=2048, heads=32, kv=4, ffn=5632, vocab=32000, layers=22, theta=10000.0,
                  batch=8, seq=2048)
+WORKLOADS = {
+    "tinyllama": (TINYLLAMA, "TinyLlama-1.1B", "BASELINE config 3"),
+    "llama3-8b-slice": (dict(hidden=4096, heads=32, kv=8, ffn=14336, vocab=128256, layers=8,
+                             theta=500000.0, batch=1, seq=8192), "Llama-3-8B 8-layer slice",
+                        "BASELINE config 4"),
+    "llama2-7b-long": (dict(hidden=4096, heads=32, kv=32, ffn=11008, vocab=32000, layers=4,
+                            theta=10000.0, batch=1, seq=32768), "Llama-2-7B 4-layer slice, long context",
+                       "BASELINE config 5"),
+}
+PRESETS = {"full": "llama_decoder_layer", "selective": "llama_mlp_and_norms"}
 
 
 def log(msg: str) -> None:
@@ -48,8 +63,13 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--layers", type=int, default=TINYLLAMA["layers"],
-                    help="decoder layers (default: the full 22 of TinyLlama-1.1B)")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="tinyllama",
+                    help="model shape (default: TinyLlama-1.1B, the metric's workload)")
+    ap.add_argument("--ac", choices=sorted(PRESETS), default="full",
+                    help="checkpointing policy: every decoder layer (full) or the MLP and norms "
+                         "(selective)")
+    ap.add_argument("--layers", type=int, default=None,
+                    help="decoder layers (default: the workload's, 22 for TinyLlama-1.1B)")
     ap.add_argument("--kernel-iters", type=int, default=20)
     ap.add_argument("--reference-steps", type=int, default=2,
                     help="timed steps of the reference path on the GPU (0 to skip)")
@@ -129,12 +149,12 @@ def event_ms(torch, fn, iters: int) -> float:
     return start.elapsed_time(end) / iters
 
 
-def kernel_table(torch, iters: int):
-    """Fused kernels at the TinyLlama step's shapes.  Each launch reads a
-    different buffer set (working set > 1 GiB) so the 256 MiB MALL cannot serve
-    repeats: the bytes come from HBM as in the step."""
+def kernel_table(torch, c: dict, iters: int, ac: str):
+    """Fused kernels at the step's shapes.  Each launch reads a different buffer
+    set (working set > 1 GiB) so the 256 MiB MALL cannot serve repeats: the bytes
+    come from HBM as in the step.  launches_per_step counts the launches of one
+    step of the model with c["layers"] layers under policy `ac`."""
     from femtotron_amd import ops
-    c = TINYLLAMA
     T, H, F = c["batch"] * c["seq"], c["hidden"], c["ffn"]
     nh, nkv, hd = c["heads"], c["kv"], c["hidden"] // c["heads"]
     Hq, Hkv = nh * hd, nkv * hd
@@ -158,33 +178,42 @@ def kernel_table(torch, iters: int):
                          achieved_gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4)))
 
     L = c["layers"]
+    sel = ac == "selective"
     # rmsnorm_fwd: x -> y   (4TH bytes)
     xs = sets(8, lambda: rnd(T, H))
     ys = sets(8, lambda: torch.empty(T, H, device=dev, dtype=bf))
     rs = torch.empty(T, device=dev, dtype=torch.float32)
     ms = event_ms(torch, lambda i=0: ops.rmsnorm_fwd(xs[i % 8], w, 1e-5, out=ys[i % 8], rstd=rs), iters)
-    add_row("rmsnorm_fwd", "k_rmsnorm_fwd", 2 * L, 4 * T * H, ms)
+    add_row("rmsnorm_fwd", "k_rmsnorm_fwd", 2 * L + 1 if sel else 2 * L, 4 * T * H, ms)
     # add_rmsnorm_fwd: x, a -> h, y   (8TH)
     as_ = sets(8, lambda: rnd(T, H))
     ms = event_ms(torch, lambda i=0: ops.add_rmsnorm_fwd(xs[i % 8], as_[i % 8], w, 1e-5, rstd=rs), iters)
-    add_row("add_rmsnorm_fwd", "k_rmsnorm_fwd (ADD)", 2 * L, 8 * T * H, ms)
-    # rmsnorm_bwd with residual: dy, x, dres -> dx   (8TH)
-    ms = event_ms(torch, lambda i=0: ops.rmsnorm_bwd(ys[i % 8], xs[i % 8], w, 1e-5, rstd=rs,
-                                                       dres=as_[i % 8]), iters)
-    add_row("rmsnorm_bwd", "k_rmsnorm_bwd", 2 * L, 8 * T * H, ms)
+    if not sel:
+        add_row("add_rmsnorm_fwd", "k_rmsnorm_fwd (ADD)", 2 * L, 8 * T * H, ms)
+    if sel:
+        # rmsnorm_bwd without residual, statistic recomputed: dy, x -> dx   (6TH)
+        ms = event_ms(torch, lambda i=0: ops.rmsnorm_bwd(ys[i % 8], xs[i % 8], w, 1e-5), iters)
+        add_row("rmsnorm_bwd", "k_rmsnorm_bwd", 2 * L + 1, 6 * T * H, ms)
+    else:
+        # rmsnorm_bwd with residual: dy, x, dres -> dx   (8TH)
+        ms = event_ms(torch, lambda i=0: ops.rmsnorm_bwd(ys[i % 8], xs[i % 8], w, 1e-5, rstd=rs,
+                                                           dres=as_[i % 8]), iters)
+        add_row("rmsnorm_bwd", "k_rmsnorm_bwd", 2 * L, 8 * T * H, ms)
     del as_
-    # residual add: h + m -> out   (6TH)
-    ms = event_ms(torch, lambda i=0: ops.add(xs[i % 8], ys[i % 8], out=ys[(i + 1) % 8]), iters)
-    add_row("residual_add", "k_add", L, 6 * T * H, ms)
+    if not sel:
+        # residual add: h + m -> out   (6TH)
+        ms = event_ms(torch, lambda i=0: ops.add(xs[i % 8], ys[i % 8], out=ys[(i + 1) % 8]), iters)
+        add_row("residual_add", "k_add", L, 6 * T * H, ms)
     del xs, ys
     # rope on q and k of the qkv buffer   (4T(Hq+Hkv))
     qkvs = sets(6, lambda: rnd(T, Hq + 2 * Hkv))
     cos = torch.cos(torch.arange(c["seq"] * hd, device=dev, dtype=torch.float32)).to(bf).view(1, c["seq"], hd)
     sin = torch.sin(torch.arange(c["seq"] * hd, device=dev, dtype=torch.float32)).to(bf).view(1, c["seq"], hd)
-    ms = event_ms(torch, lambda i=0: ops.rope_fwd_(qkvs[i % 6], nh + nkv, hd, c["seq"], cos, sin), iters)
-    add_row("rope_fwd", "k_rope<fwd>", 2 * L, 4 * T * (Hq + Hkv), ms)
-    ms = event_ms(torch, lambda i=0: ops.rope_bwd_(qkvs[i % 6], nh + nkv, hd, c["seq"], cos, sin), iters)
-    add_row("rope_bwd", "k_rope<bwd>", L, 4 * T * (Hq + Hkv), ms)
+    if not sel:
+        ms = event_ms(torch, lambda i=0: ops.rope_fwd_(qkvs[i % 6], nh + nkv, hd, c["seq"], cos, sin), iters)
+        add_row("rope_fwd", "k_rope<fwd>", 2 * L, 4 * T * (Hq + Hkv), ms)
+        ms = event_ms(torch, lambda i=0: ops.rope_bwd_(qkvs[i % 6], nh + nkv, hd, c["seq"], cos, sin), iters)
+        add_row("rope_bwd", "k_rope<bwd>", L, 4 * T * (Hq + Hkv), ms)
     # SwiGLU: g,u -> p (6TF);  dp,g,u -> dg,du (10TF)
     gus = sets(3, lambda: rnd(T, 2 * F))
     ps = sets(3, lambda: torch.empty(T, F, device=dev, dtype=bf))
@@ -195,6 +224,8 @@ def kernel_table(torch, iters: int):
                                                       dgus[i % 3][:, :F], dgus[i % 3][:, F:]), iters)
     add_row("swiglu_bwd", "k_swiglu_bwd", L, 10 * T * F, ms)
     del gus, ps, dgus
+    if sel:  # attention is outside the checkpointed modules under this policy
+        return rows, []
 
     # attention (MFMA-bound): causal flop count 4*B*nh*S^2*hd/2 forward
     B, S = c["batch"], c["seq"]
@@ -211,11 +242,11 @@ def kernel_table(torch, iters: int):
     # backward: dK/dV kernel 4 products + dQ kernel 3 products (the dQ kernel
     # recomputes S and dP); algorithmic = the 5 products of attention backward
     bwd_flop = 2.5 * fwd_flop
-    mfma = [dict(kernel="attn_fwd", symbol="k_attn_fwd<64>", launches_per_step=2 * L,
+    mfma = [dict(kernel="attn_fwd", symbol=f"k_attn_fwd<{hd}>", launches_per_step=2 * L,
                  flop_per_launch=fwd_flop, ms_per_launch=round(ms_f, 4),
                  achieved_tflops=round(fwd_flop / ms_f / 1e9, 1),
                  frac=round(fwd_flop / ms_f / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)),
-            dict(kernel="attn_bwd", symbol="k_attn_bwd_dkdv<64> + k_attn_bwd_dq<64> + k_attn_delta",
+            dict(kernel="attn_bwd", symbol=f"k_attn_bwd_dq<{hd}> + k_attn_bwd_dkdv<{hd}>",
                  launches_per_step=L, flop_per_launch=bwd_flop, ms_per_launch=round(ms_b, 4),
                  achieved_tflops=round(bwd_flop / ms_b / 1e9, 1),
                  frac=round(bwd_flop / ms_b / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4))]
@@ -334,32 +365,35 @@ def main() -> int:
     from femtotron_amd.training import apply_activation_checkpointing, remove_activation_checkpointing
 
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
-    c = TINYLLAMA
+    c, model_name, cfg_name = WORKLOADS[args.workload]
+    c = dict(c, layers=args.layers or c["layers"])
+    L = c["layers"]
     B, S = c["batch"], c["seq"]
     T = B * S
-    log(f"building TinyLlama-shaped model ({args.layers} layers), bf16, weights N(0, 0.02)")
-    model = build_llama_model(llama_config(c, args.layers))
+    log(f"building {model_name}-shaped model ({L} layers), bf16, weights N(0, 0.02)")
+    model = build_llama_model(llama_config(c, L))
     model = init_llama_weights_(model, device="cuda", dtype=torch.bfloat16, generator_device="cuda")
-    policy = get_ac_policy("llama_decoder_layer")
+    policy = get_ac_policy(PRESETS[args.ac])
     apply_activation_checkpointing(model, policy, checkpoint_fn=fused_checkpoint)
     ids = torch.randint(0, c["vocab"], (B, S), generator=torch.Generator().manual_seed(2000)).cuda()
 
     reset_dispatch_counts()
-    log(f"fused path: {args.warmup} warm-up + {args.steps} timed steps")
+    log(f"fused path ({args.ac} AC): {args.warmup} warm-up + {args.steps} timed steps")
     sec = time_steps(torch, model, ids, args.steps, args.warmup)
     counts = dispatch_counts()
-    assert counts["fallback"] == 0 and counts["fused"] == args.layers * (args.steps + args.warmup), counts
+    calls_per_step = L if args.ac == "full" else 3 * L + 1
+    assert counts["fallback"] == 0 and counts["fused"] == calls_per_step * (args.steps + args.warmup), counts
     tok_s = T / sec
     log(f"fused: {sec * 1e3:.2f} ms/step, {tok_s:.0f} tokens/s")
 
     log("per-kernel HIP-event timings at the step's shapes")
-    rows, mfma = kernel_table(torch, args.kernel_iters)
+    rows, mfma = kernel_table(torch, c, args.kernel_iters, args.ac)
     for r in rows:
-        r["ms_per_step"] = round(r["ms_per_launch"] * r["launches_per_step"] * args.layers / c["layers"], 4)
+        r["ms_per_step"] = round(r["ms_per_launch"] * r["launches_per_step"], 4)
     dom = max(rows, key=lambda r: r["ms_per_step"])
     roofline = {"bound": "hbm", "kernel": dom["kernel"], "achieved": dom["achieved_gbs"],
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["frac"],
-                "traffic": measured_traffic(dom["kernel"]),
+                "traffic": measured_traffic(dom["kernel"]) if args.workload == "tinyllama" else None,
                 "bytes_per_launch": dom["bytes_per_launch"]}
 
     def use(fused: bool):
@@ -389,20 +423,23 @@ def main() -> int:
     torch.cuda.empty_cache()
 
     cpu = None
-    if args.cpu_sample_tokens > 0:
+    if args.cpu_sample_tokens > 0 and args.workload == "tinyllama":
         log(f"cpu baseline: {args.cpu_sample_tokens} tokens on the host")
         cpu = cpu_baseline(torch, args.cpu_sample_tokens)
 
+    metric = METRIC if args.workload == "tinyllama" else f"ckpt'd fwd+bwd tokens/s @1 GPU ({model_name})"
     out = {
-        "metric": METRIC, "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1,
+        "metric": metric, "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (token ids uniform over the vocab, CPU Generator(2000); random-init "
                 "weights N(0, 0.02))",
-        "config": {"workload": "TinyLlama-1.1B-shaped checkpointed fwd+bwd (BASELINE config 3)",
-                   "layers": args.layers, "hidden": c["hidden"], "heads": c["heads"],
+        "config": {"workload": f"{model_name}-shaped checkpointed fwd+bwd ({cfg_name})",
+                   "layers": L, "hidden": c["hidden"], "heads": c["heads"],
                    "kv_heads": c["kv"], "ffn": c["ffn"], "vocab": c["vocab"], "micro_batch": B,
-                   "seq_len": S, "tokens_per_step": T, "activation_checkpointing": "every layer",
+                   "seq_len": S, "tokens_per_step": T,
+                   "activation_checkpointing": "every layer" if args.ac == "full"
+                   else "selective: every LlamaMLP and LlamaRMSNorm",
                    "parallelism": "single GPU (TP=PP=DP=1)"},
         "roofline": roofline,
         "fused_kernels_hbm": rows,

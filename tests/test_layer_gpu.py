@@ -15,7 +15,7 @@ import torch
 from transformers.models.llama import modeling_llama as hf
 
 from oracle import torch_llama as ot
-from tests.helpers import (BF16_ATOL, BF16_RTOL, CFG1, CFG3, CFG4, assert_close, hf_layer_grads,
+from tests.helpers import (BF16_ATOL, BF16_RTOL, CFG1, CFG3, CFG4, CFG5, assert_close, hf_layer_grads,
                            layer_weights, llama_config, load_into_hf_layer, randn, rel_err)
 
 pytestmark = pytest.mark.gpu
@@ -132,12 +132,16 @@ def test_fused_layer_fp32_matches_oracle_1e5():
         assert rel_err(gw[k], ref[2][k]) < 1e-5, f"d{k} rel {rel_err(gw[k], ref[2][k]):.3e}"
 
 
-def test_fused_layer_matches_stock_checkpoint_full_tinyllama_shape():
-    """Full TinyLlama layer (B=8, S=2048): fused vs HF layer + torch checkpoint on GPU."""
-    got = _run_layer(CFG3, 8, 2048, torch.bfloat16, fused=True)
+@pytest.mark.parametrize("name,c", [("tinyllama", CFG3), ("llama3-8b", CFG4), ("llama2-7b-long", CFG5)])
+def test_fused_layer_matches_stock_checkpoint_full_shape(name, c):
+    """One layer at each GPU config's full shape: TinyLlama (B=8, S=2048, GQA 32/4,
+    hd 64), Llama-3-8B (S=8192, GQA 32/8, hd 128, F=14336), Llama-2-7B long
+    context (S=32768, MHA 32/32, hd 128): fused vs HF layer + torch checkpoint
+    on the GPU, tensor-level metric."""
+    got = _run_layer(c, c["batch"], c["seq"], torch.bfloat16, fused=True)
     torch.cuda.synchronize()
-    ref = _run_layer(CFG3, 8, 2048, torch.bfloat16, fused=False)
-    _compare(got, ref, BF16_RTOL, BF16_ATOL, "tinyllama-full")
+    ref = _run_layer(c, c["batch"], c["seq"], torch.bfloat16, fused=False)
+    _compare(got, ref, BF16_RTOL, BF16_ATOL, f"{name}-full")
 
 
 def test_cfg1_model_step_gpu_fp32_vs_cpu_oracle():
