@@ -20,9 +20,19 @@
 // scalar, and P^T feeds the next MFMA straight from registers.  That P operand
 // carries its K index (the key) in the permuted order {4h..4h+3, 8+4h..8+4h+3}
 // (h = i/32) of the accumulator layout; the matching operand is fetched with
-// two ds_read_b64_tr_b16 transpose reads in exactly that order, so tiles stay in
-// natural row-major layout in LDS.
+// two ds_read_b64_tr_b16 transpose reads in exactly that order.
+//
+// LDS tiles are [rows x HD] bf16 without padding, XOR-swizzled in 16-byte
+// chunks: chunk c of row r is stored at chunk position c ^ swz(r).  Operands
+// read a tile in two patterns, (a) ds_read_b128 of one chunk from 16
+// consecutive rows and (b) ds_read_b64_tr_b16 of 4 consecutive chunks from 4
+// consecutive rows (first row a multiple of 4) across 32 lanes; swz() maps
+// both onto the 16 distinct 4-bank groups of one LDS cycle, so neither has
+// bank conflicts.  A read address is a per-lane constant XOR a compile-time
+// constant, plus an immediate offset.
 #include <math.h>
+
+#include <type_traits>
 
 #include "fh_common.hpp"
 
@@ -36,13 +46,17 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+// The forward keeps a stale running maximum until a block's maximum exceeds it
+// by more than this (log2 units): the softmax weights then stay <= 2^8, and
+// the output rescale runs only when the maximum really grows.
+constexpr float kRescaleSlack = 8.f;
 
 __device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 // 2^x on the transcendental unit (v_exp_f32).  Denormal results flush to
-// zero, which is harmless for softmax weights (the row maximum is 2^0).
+// zero, which is harmless for softmax weights.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // max over lanes i and i^32 (v_permlane32_swap exchanges the two row halves).
@@ -56,6 +70,8 @@ __device__ __forceinline__ float xor32_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+__device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
+
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
 #pragma unroll
@@ -65,34 +81,68 @@ __device__ __forceinline__ f32x16 zero16() {
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// 8 consecutive bf16 from global memory.
 __device__ __forceinline__ bf16x8 ld_frag(const uint16_t* p) {
   return as_bf16x8(*reinterpret_cast<const uint4*>(p));
 }
 
-// Operand whose K index runs down the rows of a row-major LDS tile X (stride
-// ld): lane i gets X[row0 + {4h+0..3, 8+4h+0..3}][col0 + i%32], h = i/32.
-__device__ __forceinline__ bf16x8 ld_frag_tr(const uint16_t* X, int ld, int row0, int col0,
-                                             int lane) {
+// ------------------------------------------------------------- LDS tiles
+template <int HD>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (HD == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+  else if constexpr (HD == 64) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  else return (r >> 2) & 3;
+}
+
+// Pattern (a) lane constant: row lane%32 of a 32-row group, chunk lane/32.
+// Step s (K = 16s..16s+15 along the row) of the group at row0 is read at byte
+// row0*2*HD + (A ^ 32s).
+template <int HD>
+__device__ __forceinline__ int lane_off_a(int lane) {
+  const int l32 = lane & 31, hl = lane >> 5;
+  return l32 * (2 * HD) + ((hl ^ swz<HD>(l32)) << 4);
+}
+
+// Pattern (b) lane constant for rows 4*(lane/32) + (lane%16)/4 (+ plus8):
+// the 32-column block dt of the 16-row group at row0 is read at byte
+// row0*2*HD + (B ^ 64dt).
+template <int HD>
+__device__ __forceinline__ int lane_off_b(int lane, int plus8) {
   const int hl = lane >> 5, L = lane & 15, mh = (lane >> 4) & 1;
-  const uint16_t* p0 = X + (row0 + 4 * hl + (L >> 2)) * ld + col0 + 16 * mh + 4 * (L & 3);
-  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0));
-  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0 + 8 * ld));
-  uint4 r;
-  r.x = static_cast<uint16_t>(a[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(a[1])) << 16);
-  r.y = static_cast<uint16_t>(a[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(a[3])) << 16);
-  r.z = static_cast<uint16_t>(b[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(b[1])) << 16);
-  r.w = static_cast<uint16_t>(b[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(b[3])) << 16);
-  return as_bf16x8(r);
+  const int r = 4 * hl + (L >> 2) + plus8;
+  const int cb = 2 * mh + ((L & 3) >> 1);
+  return r * (2 * HD) + ((cb ^ swz<HD>(r)) << 4) + 8 * (L & 1);
+}
+
+// Makes the per-lane read offsets opaque to the optimizer once per loop
+// iteration, so that their XORs with compile-time constants are recomputed
+// (one VALU op per read) instead of each being kept live in its own register.
+__device__ __forceinline__ void refresh_offsets(int& a, int& b0, int& b8) {
+  asm volatile("" : "+v"(a), "+v"(b0), "+v"(b8));
+}
+
+// Operand with K along the rows of a swizzled tile: lane i gets row
+// row0 + i%32, columns 16s + 8*(i/32) .. +7.
+template <int HD>
+__device__ __forceinline__ bf16x8 lds_frag(const char* tile, int a_off, int row0, int s) {
+  return *reinterpret_cast<const bf16x8*>(tile + row0 * (2 * HD) + (a_off ^ (32 * s)));
+}
+
+// Operand with K down the rows of a swizzled tile X: lane i gets
+// X[row0 + {4h+0..3, 8+4h+0..3}][32dt + i%32], h = i/32.
+template <int HD>
+__device__ __forceinline__ bf16x8 lds_frag_tr(const char* tile, int b0, int b8, int row0, int dt) {
+  const char* t = tile + row0 * (2 * HD);
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + (b0 ^ (64 * dt))));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + (b8 ^ (64 * dt))));
+  const uint2 ua = __builtin_bit_cast(uint2, a), ub = __builtin_bit_cast(uint2, b);
+  return as_bf16x8(make_uint4(ua.x, ua.y, ub.x, ub.y));
 }
 
 // Accumulator entries j0..j0+7 rounded to bf16 as an MFMA operand.
 __device__ __forceinline__ bf16x8 pack_frag(const f32x16& acc, int j0) {
-  uint4 r;
-  r.x = f2bf(acc[j0 + 0]) | (static_cast<uint32_t>(f2bf(acc[j0 + 1])) << 16);
-  r.y = f2bf(acc[j0 + 2]) | (static_cast<uint32_t>(f2bf(acc[j0 + 3])) << 16);
-  r.z = f2bf(acc[j0 + 4]) | (static_cast<uint32_t>(f2bf(acc[j0 + 5])) << 16);
-  r.w = f2bf(acc[j0 + 6]) | (static_cast<uint32_t>(f2bf(acc[j0 + 7])) << 16);
-  return as_bf16x8(r);
+  return as_bf16x8(make_uint4(pk_bf16(acc[j0 + 0], acc[j0 + 1]), pk_bf16(acc[j0 + 2], acc[j0 + 3]),
+                              pk_bf16(acc[j0 + 4], acc[j0 + 5]), pk_bf16(acc[j0 + 6], acc[j0 + 7])));
 }
 
 // Row (M index) of accumulator entry j for lane half hl.
@@ -100,42 +150,42 @@ __device__ __forceinline__ int acc_row(int j, int hl) { return 8 * (j >> 2) + 4 
 
 // Per-thread registers holding one ROWS x HD bf16 tile in flight from global
 // memory to LDS (the software pipeline's prefetch stage): load() issues the
-// 16-byte global loads (rows at or beyond `valid` read as zero), store() writes
-// them to an LDS tile of row stride LDST.  Consecutive threads take
-// consecutive 16-byte chunks of a row.
-template <int ROWS, int HD, int LDST, int NT>
+// 16-byte global loads (rows at or beyond `valid` read as zero), store()
+// writes them swizzled into an LDS tile.  Consecutive threads take
+// consecutive 16-byte chunks of a row; every pass covers a multiple of 16
+// rows, so a thread's swizzle is the same in every pass.
+template <int ROWS, int HD, int NT>
 struct TileRegs {
   static constexpr int CPR = HD / 8;
   static constexpr int CHUNKS = ROWS * CPR;
   static constexpr int N = (CHUNKS + NT - 1) / NT;
+  static constexpr int RPP = NT / CPR;  // rows per pass
+  static_assert(NT % CPR == 0 && RPP % 16 == 0, "pass must cover a multiple of 16 rows");
   uint4 r[N];
   __device__ __forceinline__ void load(const uint16_t* src, int64_t ld, int valid, int tid) {
+    const int row = tid / CPR, col = (tid % CPR) * 8;
+    const uint16_t* p = src + static_cast<int64_t>(row) * ld + col;
     if (valid >= ROWS) {  // whole tile in range (the common case): no per-row guard
 #pragma unroll
-      for (int i = 0; i < N; ++i) {
-        const int c = tid + i * NT;
-        const int row = c / CPR, col = (c - row * CPR) * 8;
-        if (CHUNKS % NT == 0 || c < CHUNKS)
-          r[i] = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(row) * ld + col);
-      }
+      for (int i = 0; i < N; ++i)
+        if (CHUNKS % NT == 0 || tid + i * NT < CHUNKS)
+          r[i] = *reinterpret_cast<const uint4*>(p + static_cast<int64_t>(i * RPP) * ld);
       return;
     }
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-      const int c = tid + i * NT;
-      const int row = c / CPR, col = (c - row * CPR) * 8;
       r[i] = make_uint4(0, 0, 0, 0);
-      if ((CHUNKS % NT == 0 || c < CHUNKS) && row < valid)
-        r[i] = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(row) * ld + col);
+      if ((CHUNKS % NT == 0 || tid + i * NT < CHUNKS) && row + i * RPP < valid)
+        r[i] = *reinterpret_cast<const uint4*>(p + static_cast<int64_t>(i * RPP) * ld);
     }
   }
-  __device__ __forceinline__ void store(uint16_t* dst, int tid) const {
+  __device__ __forceinline__ void store(char* tile, int tid) const {
+    const int row = tid / CPR, ch = tid % CPR;
+    char* p = tile + row * (2 * HD) + ((ch ^ swz<HD>(row)) << 4);
 #pragma unroll
-    for (int i = 0; i < N; ++i) {
-      const int c = tid + i * NT;
-      const int row = c / CPR, col = (c - row * CPR) * 8;
-      if (CHUNKS % NT == 0 || c < CHUNKS) *reinterpret_cast<uint4*>(dst + row * LDST + col) = r[i];
-    }
+    for (int i = 0; i < N; ++i)
+      if (CHUNKS % NT == 0 || tid + i * NT < CHUNKS)
+        *reinterpret_cast<uint4*>(p + i * RPP * (2 * HD)) = r[i];
   }
 };
 
@@ -149,156 +199,129 @@ __device__ __forceinline__ void store_rows_T(uint16_t* out_row, const f32x16 (&a
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       uint2 w;
-      w.x = f2bf(acc[dt][4 * g] * mul) | (static_cast<uint32_t>(f2bf(acc[dt][4 * g + 1] * mul)) << 16);
-      w.y = f2bf(acc[dt][4 * g + 2] * mul) | (static_cast<uint32_t>(f2bf(acc[dt][4 * g + 3] * mul)) << 16);
+      w.x = pk_bf16(acc[dt][4 * g] * mul, acc[dt][4 * g + 1] * mul);
+      w.y = pk_bf16(acc[dt][4 * g + 2] * mul, acc[dt][4 * g + 3] * mul);
       *reinterpret_cast<uint2*>(out_row + dt * 32 + 8 * g + 4 * hl) = w;
     }
 }
 
-// Query tiles (of 32) per wave in the forward.  Two tiles would let every K/V
-// fragment read from LDS feed two MFMAs, but the extra registers cost a wave
-// of occupancy and measured slower at head_dim 64 (447 vs 384 us for the
-// TinyLlama attention shape), so one tile for every head_dim.
-template <int HD>
-struct FwdTiles {
-  static constexpr int QT = 1;
-};
-
 // ------------------------------------------------------------ forward (bf16)
-// Block = 4 waves x (32*QT) queries of one (batch, head); loop over 64-key
-// blocks, double-buffered in LDS: the next block's K/V are loaded into
-// registers while the current one is multiplied, then written to the other
-// LDS stage; one barrier per block.
+// Block = 4 waves x 32 queries of one (batch, head); loop over 64-key blocks,
+// double-buffered in LDS: the next block's K/V are loaded into registers while
+// the current one is multiplied, then written to the other LDS stage; one
+// barrier per block.  Heaviest (latest) query blocks are dispatched first.
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_fwd(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_fwd(
     const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
     const uint16_t* __restrict__ v, int64_t ldv, uint16_t* __restrict__ o, int64_t ldo,
     float* __restrict__ lse, int S, int nh, int group, float scale_log2) {
-  constexpr int QT = FwdTiles<HD>::QT;
-  constexpr int BM = 4 * 32 * QT, BN = 64, LDST = HD + 8, NS = HD / 16, ND = HD / 32;
-  __shared__ __align__(16) uint16_t sk[2][BN * LDST];
-  __shared__ __align__(16) uint16_t sv[2][BN * LDST];
+  constexpr int BM = 128, BN = 64, NS = HD / 16, ND = HD / 32, TILE = BN * 2 * HD;
+  __shared__ __align__(16) char sk[2 * TILE];
+  __shared__ __align__(16) char sv[2 * TILE];
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const int bh = blockIdx.y, b = bh / nh, h = bh - b * nh, kvh = h / group;
-  const int q0 = (gridDim.x - 1 - blockIdx.x) * BM;  // heaviest (latest) query blocks first
-  const int qw = q0 + wave * 32 * QT;                 // first query of this wave
+  const int q0 = (gridDim.x - 1 - blockIdx.x) * BM;
+  const int qw = q0 + wave * 32, qi = qw + l32;
   const int64_t tok0 = static_cast<int64_t>(b) * S;
+  int a_off = lane_off_a<HD>(lane);
+  int b0 = lane_off_b<HD>(lane, 0), b8 = lane_off_b<HD>(lane, 8);
 
-  bf16x8 qf[QT][NS];
-#pragma unroll
-  for (int u = 0; u < QT; ++u) {
-    const int qi = qw + 32 * u + l32;
+  bf16x8 qf[NS];
+  {
     const uint16_t* qrow = q + (tok0 + qi) * ldq + static_cast<int64_t>(h) * HD + 8 * hl;
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
-      qf[u][s] = qi < S ? ld_frag(qrow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
+    for (int s = 0; s < NS; ++s) qf[s] = qi < S ? ld_frag(qrow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
   }
-  f32x16 oacc[QT][ND];
-  float m[QT], l[QT];
+  f32x16 oacc[ND];
 #pragma unroll
-  for (int u = 0; u < QT; ++u) {
-    m[u] = -INFINITY;
-    l[u] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < ND; ++dt) oacc[u][dt] = zero16();
-  }
+  for (int dt = 0; dt < ND; ++dt) oacc[dt] = zero16();
+  float m = -INFINITY, l = 0.f;  // running max (log2 units) and sum of weights
 
   const int kend = min(S, q0 + BM);
   const int nkb = (kend + BN - 1) / BN;
   const uint16_t* kb_ptr = k + tok0 * ldk + static_cast<int64_t>(kvh) * HD;
   const uint16_t* vb_ptr = v + tok0 * ldv + static_cast<int64_t>(kvh) * HD;
-  TileRegs<BN, HD, LDST, 256> pk, pv;
+  TileRegs<BN, HD, 256> pk, pv;
   pk.load(kb_ptr, ldk, S, tid);
   pv.load(vb_ptr, ldv, S, tid);
-  pk.store(sk[0], tid);
-  pv.store(sv[0], tid);
+  pk.store(sk, tid);
+  pv.store(sv, tid);
   __syncthreads();
   for (int kb = 0; kb < nkb; ++kb) {
     const int k0 = kb * BN, st = kb & 1;
     const bool more = kb + 1 < nkb;
+    refresh_offsets(a_off, b0, b8);
     if (more) {
       pk.load(kb_ptr + static_cast<int64_t>(k0 + BN) * ldk, ldk, S - k0 - BN, tid);
       pv.load(vb_ptr + static_cast<int64_t>(k0 + BN) * ldv, ldv, S - k0 - BN, tid);
     }
-    if (k0 <= qw + 32 * QT - 1) {  // some key of the block precedes some query of the wave
-      const uint16_t* K = sk[st];
-      const uint16_t* V = sv[st];
-      f32x16 sacc[BN / 32][QT];
+    if (k0 <= qw + 31) {  // some key of the block precedes some query of the wave
+      const char* K = sk + st * TILE;
+      const char* V = sv + st * TILE;
+      f32x16 x[BN / 32];  // raw scores S^T, rows = keys, column = query qi
 #pragma unroll
       for (int t = 0; t < BN / 32; ++t) {
+        x[t] = zero16();
 #pragma unroll
-        for (int u = 0; u < QT; ++u) sacc[t][u] = zero16();
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          const bf16x8 a = ld_frag(K + (32 * t + l32) * LDST + 16 * s + 8 * hl);
-#pragma unroll
-          for (int u = 0; u < QT; ++u) sacc[t][u] = mfma(a, qf[u][s], sacc[t][u]);
-        }
+        for (int s = 0; s < NS; ++s) x[t] = mfma(lds_frag<HD>(K, a_off, 32 * t, s), qf[s], x[t]);
       }
-      const bool need_mask = (k0 + BN - 1 > qw) || (k0 + BN > S);
-#pragma unroll
-      for (int u = 0; u < QT; ++u) {
-        const int qi = qw + 32 * u + l32;
-        float mloc = -INFINITY;
+      float mloc = -INFINITY;
+      if ((k0 + BN - 1 > qw) || (k0 + BN > S)) {  // diagonal or ragged block: mask
 #pragma unroll
         for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
-            float x = sacc[t][u][j] * scale_log2;
-            if (need_mask) {
-              const int key = k0 + 32 * t + acc_row(j, hl);
-              x = ((key > qi) | (key >= S)) ? -INFINITY : x;
-            }
-            sacc[t][u][j] = x;
-            mloc = fmaxf(mloc, x);
+            const int key = k0 + 32 * t + acc_row(j, hl);
+            x[t][j] = ((key > qi) | (key >= S)) ? -INFINITY : x[t][j];
+            mloc = fmaxf(mloc, x[t][j]);
           }
-        mloc = xor32_max(mloc);
-        const float mnew = fmaxf(m[u], mloc);  // finite: key 0 is visible to every query
-        const float alpha = fast_exp2(m[u] - mnew);
-        m[u] = mnew;
-        float lsum = 0.f;
+      } else {
 #pragma unroll
         for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const float p = fast_exp2(sacc[t][u][j] - mnew);
-            sacc[t][u][j] = p;
-            lsum += p;
-          }
-        l[u] = l[u] * alpha + lsum;
+          for (int j = 0; j < 16; ++j) mloc = fmaxf(mloc, x[t][j]);
+      }
+      mloc = xor32_max(mloc) * scale_log2;
+      if (wave_any(mloc > m + kRescaleSlack)) {
+        const float mnew = fmaxf(m, mloc);
+        const float alpha = fast_exp2(m - mnew);
+        m = mnew;
+        l *= alpha;
 #pragma unroll
         for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
-          for (int j = 0; j < 16; ++j) oacc[u][dt][j] *= alpha;
+          for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
       }
+      const float nm = -m;
+      float lsum = 0.f;
+#pragma unroll
+      for (int t = 0; t < BN / 32; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float p = fast_exp2(fmaf(x[t][j], scale_log2, nm));
+          x[t][j] = p;
+          lsum += p;
+        }
+      l += lsum;
 #pragma unroll
       for (int s = 0; s < BN / 16; ++s) {
-        bf16x8 pf[QT];
+        const bf16x8 pf = pack_frag(x[s >> 1], 8 * (s & 1));
 #pragma unroll
-        for (int u = 0; u < QT; ++u) pf[u] = pack_frag(sacc[s >> 1][u], 8 * (s & 1));
-#pragma unroll
-        for (int dt = 0; dt < ND; ++dt) {
-          const bf16x8 a = ld_frag_tr(V, LDST, 16 * s, 32 * dt, lane);
-#pragma unroll
-          for (int u = 0; u < QT; ++u) oacc[u][dt] = mfma(a, pf[u], oacc[u][dt]);
-        }
+        for (int dt = 0; dt < ND; ++dt)
+          oacc[dt] = mfma(lds_frag_tr<HD>(V, b0, b8, 16 * s, dt), pf, oacc[dt]);
       }
     }
     if (more) {
-      pk.store(sk[st ^ 1], tid);
-      pv.store(sv[st ^ 1], tid);
+      pk.store(sk + (st ^ 1) * TILE, tid);
+      pv.store(sv + (st ^ 1) * TILE, tid);
     }
     __syncthreads();
   }
-#pragma unroll
-  for (int u = 0; u < QT; ++u) {
-    const int qi = qw + 32 * u + l32;
-    const float lt = xor32_sum(l[u]);
-    if (qi < S) {
-      store_rows_T<HD>(o + (tok0 + qi) * ldo + static_cast<int64_t>(h) * HD, oacc[u], 1.f / lt, hl);
-      if (lse != nullptr && hl == 0) lse[static_cast<int64_t>(bh) * S + qi] = (m[u] + log2f(lt)) * kLn2;
-    }
+  const float lt = xor32_sum(l);
+  if (qi < S) {
+    store_rows_T<HD>(o + (tok0 + qi) * ldo + static_cast<int64_t>(h) * HD, oacc, 1.f / lt, hl);
+    if (lse != nullptr && hl == 0) lse[static_cast<int64_t>(bh) * S + qi] = (m + log2f(lt)) * kLn2;
   }
 }
 
@@ -335,24 +358,26 @@ __global__ __launch_bounds__(256) void k_attn_delta(const T* __restrict__ o, int
 // holds half of each row; one exchange with lane i^32 completes it) and
 // stores it for the dK/dV kernel, which runs next on the same stream.
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_bwd_dq(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_bwd_dq(
     const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
     const uint16_t* __restrict__ v, int64_t ldv, const uint16_t* __restrict__ o, int64_t ldo,
     const uint16_t* __restrict__ dO, int64_t lddo, const float* __restrict__ lse,
     float* __restrict__ delta, uint16_t* __restrict__ dq, int64_t lddq, int S, int nh, int group,
     float scale_log2, float scale) {
-  constexpr int BM = 128, BN = 64, LDST = HD + 8, NS = HD / 16, ND = HD / 32;
-  __shared__ __align__(16) uint16_t sk[2][BN * LDST];
-  __shared__ __align__(16) uint16_t sv[2][BN * LDST];
+  constexpr int BM = 128, BN = 64, NS = HD / 16, ND = HD / 32, TILE = BN * 2 * HD;
+  __shared__ __align__(16) char sk[2 * TILE];
+  __shared__ __align__(16) char sv[2 * TILE];
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const int bh = blockIdx.y, b = bh / nh, h = bh - b * nh, kvh = h / group;
   const int q0 = (gridDim.x - 1 - blockIdx.x) * BM;
   const int qw = q0 + wave * 32, qi = qw + l32;
   const int64_t tok0 = static_cast<int64_t>(b) * S;
+  int a_off = lane_off_a<HD>(lane);
+  int b0 = lane_off_b<HD>(lane, 0), b8 = lane_off_b<HD>(lane, 8);
 
   bf16x8 qf[NS], gf[NS];
-  float lse2 = 0.f, dl = 0.f;
+  float nlse2 = 0.f, dl = 0.f;
   {
     const int64_t col = static_cast<int64_t>(h) * HD + 8 * hl;
     const uint16_t* qrow = q + (tok0 + qi) * ldq + col;
@@ -377,7 +402,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(
     }
     dl = xor32_sum(part);
     if (qi < S) {
-      lse2 = lse[static_cast<int64_t>(bh) * S + qi] * kLog2e;
+      nlse2 = -lse[static_cast<int64_t>(bh) * S + qi] * kLog2e;
       if (hl == 0) delta[static_cast<int64_t>(bh) * S + qi] = dl;
     }
   }
@@ -389,87 +414,128 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(
   const int nkb = (kend + BN - 1) / BN;
   const uint16_t* kb_ptr = k + tok0 * ldk + static_cast<int64_t>(kvh) * HD;
   const uint16_t* vb_ptr = v + tok0 * ldv + static_cast<int64_t>(kvh) * HD;
-  TileRegs<BN, HD, LDST, 256> pk, pv;
+  TileRegs<BN, HD, 256> pk, pv;
   pk.load(kb_ptr, ldk, S, tid);
   pv.load(vb_ptr, ldv, S, tid);
-  pk.store(sk[0], tid);
-  pv.store(sv[0], tid);
+  pk.store(sk, tid);
+  pv.store(sv, tid);
   __syncthreads();
   for (int kb = 0; kb < nkb; ++kb) {
     const int k0 = kb * BN, st = kb & 1;
     const bool more = kb + 1 < nkb;
+    refresh_offsets(a_off, b0, b8);
     if (more) {
       pk.load(kb_ptr + static_cast<int64_t>(k0 + BN) * ldk, ldk, S - k0 - BN, tid);
       pv.load(vb_ptr + static_cast<int64_t>(k0 + BN) * ldv, ldv, S - k0 - BN, tid);
     }
     if (k0 <= qw + 31) {
-      const uint16_t* K = sk[st];
-      const uint16_t* V = sv[st];
+      const char* K = sk + st * TILE;
+      const char* V = sv + st * TILE;
       const bool need_mask = (k0 + BN - 1 > qw) || (k0 + BN > S);
 #pragma unroll
       for (int t = 0; t < BN / 32; ++t) {
-        f32x16 sacc = zero16(), pacc = zero16();
+        f32x16 x = zero16(), y = zero16();  // S^T, dP^T
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-          sacc = mfma(ld_frag(K + (32 * t + l32) * LDST + 16 * s + 8 * hl), qf[s], sacc);
-          pacc = mfma(ld_frag(V + (32 * t + l32) * LDST + 16 * s + 8 * hl), gf[s], pacc);
+          x = mfma(lds_frag<HD>(K, a_off, 32 * t, s), qf[s], x);
+          y = mfma(lds_frag<HD>(V, a_off, 32 * t, s), gf[s], y);
         }
+        if (need_mask) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          float p = fast_exp2(sacc[j] * scale_log2 - lse2);
-          if (need_mask) {
+          for (int j = 0; j < 16; ++j) {
             const int key = k0 + 32 * t + acc_row(j, hl);
-            p = ((key > qi) | (key >= S)) ? 0.f : p;
+            const float p = fast_exp2(fmaf(x[j], scale_log2, nlse2));
+            x[j] = ((key > qi) | (key >= S)) ? 0.f : p * (y[j] - dl);  // dS^T
           }
-          sacc[j] = p * (pacc[j] - dl);  // dS^T
+        } else {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) x[j] = fast_exp2(fmaf(x[j], scale_log2, nlse2)) * (y[j] - dl);
         }
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
-          const bf16x8 df = pack_frag(sacc, 8 * s2);
+          const bf16x8 df = pack_frag(x, 8 * s2);
 #pragma unroll
           for (int dt = 0; dt < ND; ++dt)
-            dqacc[dt] = mfma(ld_frag_tr(K, LDST, 32 * t + 16 * s2, 32 * dt, lane), df, dqacc[dt]);
+            dqacc[dt] = mfma(lds_frag_tr<HD>(K, b0, b8, 32 * t + 16 * s2, dt), df, dqacc[dt]);
         }
       }
     }
     if (more) {
-      pk.store(sk[st ^ 1], tid);
-      pv.store(sv[st ^ 1], tid);
+      pk.store(sk + (st ^ 1) * TILE, tid);
+      pv.store(sv + (st ^ 1) * TILE, tid);
     }
     __syncthreads();
   }
   if (qi < S) store_rows_T<HD>(dq + (tok0 + qi) * lddq + static_cast<int64_t>(h) * HD, dqacc, scale, hl);
 }
 
-// ---------------------------------------------------- backward: dK, dV (bf16)
-// Block = 8 waves of 32 keys each, for one (batch, kv head).  Causal work per
-// key block grows with the number of later queries, so a block pairs key
-// block j (waves 0-3) with key block nkb-1-j (waves 4-7): every SIMD hosts one
-// wave of each and all blocks carry the same work.  K and V of a wave's keys
-// stay in registers; the loop runs over the group's query heads and BQ-query
-// tiles (double-buffered in LDS, prefetched through registers):
+// Prefetch stage of the dK/dV kernels: the Q and dO tiles, lse and delta of
+// the next (query head, query tile) of the loop, which it walks incrementally
+// (no division in the loop).  q, dO, lse, delta point at the group's first
+// query head; lse/delta rows are [head][S].
+template <int HD, int BQ, int NT>
+struct QTileStream {
+  TileRegs<BQ, HD, NT> pq, pg;
+  float pl = 0.f, pd = 0.f;  // -lse*log2(e) and delta of the tile in flight (threads 0..BQ-1)
+  int hh = 0, qt = 0;        // the tile to fetch next
+  __device__ __forceinline__ void fetch(const uint16_t* q, int64_t ldq, const uint16_t* dO,
+                                        int64_t lddo, const float* lse, const float* delta,
+                                        int S, int qt0, int qt_end, int tid) {
+    const int qs = qt * BQ;
+    const int64_t hcol = static_cast<int64_t>(hh) * HD;
+    pq.load(q + static_cast<int64_t>(qs) * ldq + hcol, ldq, S - qs, tid);
+    pg.load(dO + static_cast<int64_t>(qs) * lddo + hcol, lddo, S - qs, tid);
+    if (tid < BQ) {
+      const int64_t row = static_cast<int64_t>(hh) * S + qs + tid;
+      const bool ok = qs + tid < S;
+      pl = ok ? -lse[row] * kLog2e : 0.f;
+      pd = ok ? delta[row] : 0.f;
+    }
+    if (++qt == qt_end) {
+      qt = qt0;
+      ++hh;
+    }
+  }
+  __device__ __forceinline__ void commit(char* sq, char* sg, float* slse, float* sdl, int tid) const {
+    pq.store(sq, tid);
+    pg.store(sg, tid);
+    if (tid < BQ) {
+      slse[tid] = pl;
+      sdl[tid] = pd;
+    }
+  }
+};
+
+// ------------------------------------------ backward: dK, dV (bf16), fused roles
+// Used for head_dim <= 64.  Block = 8 waves of 32 keys each, for one (batch, kv
+// head).  Causal work per key block grows with the number of later queries, so
+// a block pairs key block j (waves 0-3) with key block nkb-1-j (waves 4-7):
+// every SIMD hosts one wave of each and all blocks carry the same work.  K and
+// V of a wave's keys stay in registers; the loop runs over the group's query
+// heads and 64-query tiles (double-buffered in LDS, prefetched through
+// registers):
 //   S = Q K^T, P = exp(S - lse), dP = dO V^T, dS = P (dP - delta),
 //   dV^T += dO^T P,  dK^T += Q^T dS,  dK = scale * dK.
 // Each kv head's gradient is complete inside one block: no atomics.
 template <int HD>
-struct DkdvTiles {
-  static constexpr int BQ = HD <= 64 ? 64 : 32;
-  static constexpr int NWH = HD <= 64 ? 4 : 2;  // waves per key block (two key blocks per block)
+struct DkdvFusedTiles {
+  static constexpr int BQ = 64;
+  static constexpr int NWH = 4;  // waves per key block (two key blocks per block)
   static constexpr int NT = 2 * NWH * 64;
 };
 
 template <int HD>
-__global__ __launch_bounds__(DkdvTiles<HD>::NT) void k_attn_bwd_dkdv(
+__global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_bwd_dkdv_fused(
     const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
     const uint16_t* __restrict__ v, int64_t ldv, const uint16_t* __restrict__ dO, int64_t lddo,
     const float* __restrict__ lse, const float* __restrict__ delta, uint16_t* __restrict__ dk,
     int64_t lddk, uint16_t* __restrict__ dv, int64_t lddv, int S, int nh, int nkv, int group,
     float scale_log2, float scale) {
-  constexpr int NWH = DkdvTiles<HD>::NWH, NT = DkdvTiles<HD>::NT;
-  constexpr int BKN = NWH * 32, BQ = DkdvTiles<HD>::BQ, LDST = HD + 8, NS = HD / 16, ND = HD / 32;
-  constexpr int NQT = BQ / 32;
-  __shared__ __align__(16) uint16_t sq[2][BQ * LDST];
-  __shared__ __align__(16) uint16_t sg[2][BQ * LDST];
+  constexpr int NWH = DkdvFusedTiles<HD>::NWH, NT = DkdvFusedTiles<HD>::NT;
+  constexpr int BKN = NWH * 32, BQ = DkdvFusedTiles<HD>::BQ, NS = HD / 16, ND = HD / 32;
+  constexpr int NQT = BQ / 32, TILE = BQ * 2 * HD;
+  __shared__ __align__(16) char sq[2 * TILE];
+  __shared__ __align__(16) char sg[2 * TILE];
   __shared__ __align__(16) float slse[2][BQ];
   __shared__ __align__(16) float sdl[2][BQ];
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
@@ -481,6 +547,8 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) void k_attn_bwd_dkdv(
   const bool has_keys = !upper || jhi > jlo;
   const int kw = (upper ? jhi : jlo) * BKN + (wave % NWH) * 32, ki = kw + l32;
   const int64_t tok0 = static_cast<int64_t>(b) * S;
+  int a_off = lane_off_a<HD>(lane);
+  int b0 = lane_off_b<HD>(lane, 0), b8 = lane_off_b<HD>(lane, 8);
 
   bf16x8 kf[NS], vf[NS];
   {
@@ -501,55 +569,39 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) void k_attn_bwd_dkdv(
   }
 
   // iteration space: (query head of the group) x (query tiles from the first key of block jlo)
-  const int qt0 = (jlo * BKN) / BQ;
-  const int nqt = (S + BQ - 1) / BQ - qt0;
-  const int n_it = group * nqt;
-  TileRegs<BQ, HD, LDST, NT> pq, pg;
-  float pl = 0.f, pd = 0.f;  // lse / delta of the tile in flight (threads 0..BQ-1)
-  auto fetch = [&](int it) {
-    const int hh = it / nqt, qt = qt0 + (it - hh * nqt);
-    const int h = kvh * group + hh, qs = qt * BQ;
-    const int64_t col = static_cast<int64_t>(h) * HD;
-    pq.load(q + (tok0 + qs) * ldq + col, ldq, S - qs, tid);
-    pg.load(dO + (tok0 + qs) * lddo + col, lddo, S - qs, tid);
-    if (tid < BQ) {
-      const int64_t row = (static_cast<int64_t>(b) * nh + h) * S + qs + tid;
-      const bool ok = qs + tid < S;
-      pl = ok ? lse[row] * kLog2e : 0.f;
-      pd = ok ? delta[row] : 0.f;
-    }
-  };
-  auto commit = [&](int st) {
-    pq.store(sq[st], tid);
-    pg.store(sg[st], tid);
-    if (tid < BQ) {
-      slse[st][tid] = pl;
-      sdl[st][tid] = pd;
-    }
-  };
+  const int qt0 = (jlo * BKN) / BQ, qt_end = (S + BQ - 1) / BQ;
+  const int n_it = group * (qt_end - qt0);
+  const int64_t h0 = static_cast<int64_t>(kvh) * group;
+  const uint16_t* qg = q + tok0 * ldq + h0 * HD;
+  const uint16_t* gg = dO + tok0 * lddo + h0 * HD;
+  const float* lg = lse + (static_cast<int64_t>(b) * nh + h0) * S;
+  const float* dg = delta + (static_cast<int64_t>(b) * nh + h0) * S;
+  QTileStream<HD, BQ, NT> pre;
+  pre.qt = qt0;
   if (n_it > 0) {
-    fetch(0);
-    commit(0);
+    pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, qt_end, tid);
+    pre.commit(sq, sg, slse[0], sdl[0], tid);
   }
   __syncthreads();
+  int cqt = qt0;  // query tile of the current iteration
   for (int it = 0; it < n_it; ++it) {
     const int st = it & 1;
     const bool more = it + 1 < n_it;
-    if (more) fetch(it + 1);
-    const int q0 = (qt0 + it % nqt) * BQ;
+    refresh_offsets(a_off, b0, b8);
+    if (more) pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, qt_end, tid);
+    const int q0 = cqt * BQ;
     if (has_keys && q0 + BQ - 1 >= kw) {  // some query of the tile reaches this wave's keys
-      const uint16_t* Q = sq[st];
-      const uint16_t* G = sg[st];
+      const char* Q = sq + st * TILE;
+      const char* G = sg + st * TILE;
       const bool need_mask = (q0 < kw + 31) || (q0 + BQ > S) || (kw + 32 > S);
 #pragma unroll
       for (int u = 0; u < NQT; ++u) {
-        f32x16 sacc = zero16(), pacc = zero16();
+        f32x16 x = zero16(), y = zero16();  // S, dP (rows = queries, column = key ki)
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-          sacc = mfma(ld_frag(Q + (32 * u + l32) * LDST + 16 * s + 8 * hl), kf[s], sacc);
-          pacc = mfma(ld_frag(G + (32 * u + l32) * LDST + 16 * s + 8 * hl), vf[s], pacc);
+          x = mfma(lds_frag<HD>(Q, a_off, 32 * u, s), kf[s], x);
+          y = mfma(lds_frag<HD>(G, a_off, 32 * u, s), vf[s], y);
         }
-        // this lane holds rows q = q0 + 32u + acc_row(j, hl) of column key ki
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const float4 L4 = *reinterpret_cast<const float4*>(&slse[st][32 * u + 8 * g + 4 * hl]);
@@ -559,33 +611,198 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) void k_attn_bwd_dkdv(
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int j = 4 * g + e;
-            float p = fast_exp2(sacc[j] * scale_log2 - Lv[e]);
-            if (need_mask) {
-              const int qa = q0 + 32 * u + 8 * g + 4 * hl + e;
-              p = ((ki > qa) | (qa >= S) | (ki >= S)) ? 0.f : p;
-            }
-            sacc[j] = p;                      // P
-            pacc[j] = p * (pacc[j] - Dv[e]);  // dS
+            const float p = fast_exp2(fmaf(x[j], scale_log2, Lv[e]));
+            x[j] = p;                   // P
+            y[j] = p * (y[j] - Dv[e]);  // dS
+          }
+        }
+        if (need_mask) {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int qa = q0 + 32 * u + acc_row(j, hl);
+            const bool dead = (ki > qa) | (qa >= S) | (ki >= S);
+            x[j] = dead ? 0.f : x[j];
+            y[j] = dead ? 0.f : y[j];
           }
         }
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
-          const bf16x8 pf = pack_frag(sacc, 8 * s2);
-          const bf16x8 df = pack_frag(pacc, 8 * s2);
+          const bf16x8 pf = pack_frag(x, 8 * s2);
+          const bf16x8 df = pack_frag(y, 8 * s2);
 #pragma unroll
           for (int dt = 0; dt < ND; ++dt) {
-            dvacc[dt] = mfma(ld_frag_tr(G, LDST, 32 * u + 16 * s2, 32 * dt, lane), pf, dvacc[dt]);
-            dkacc[dt] = mfma(ld_frag_tr(Q, LDST, 32 * u + 16 * s2, 32 * dt, lane), df, dkacc[dt]);
+            dvacc[dt] = mfma(lds_frag_tr<HD>(G, b0, b8, 32 * u + 16 * s2, dt), pf, dvacc[dt]);
+            dkacc[dt] = mfma(lds_frag_tr<HD>(Q, b0, b8, 32 * u + 16 * s2, dt), df, dkacc[dt]);
           }
         }
       }
     }
-    if (more) commit(st ^ 1);
+    if (more) pre.commit(sq + (st ^ 1) * TILE, sg + (st ^ 1) * TILE, slse[st ^ 1], sdl[st ^ 1], tid);
+    if (++cqt == qt_end) cqt = qt0;
     __syncthreads();
   }
   if (has_keys && ki < S) {
     store_rows_T<HD>(dk + (tok0 + ki) * lddk + static_cast<int64_t>(kvh) * HD, dkacc, scale, hl);
     store_rows_T<HD>(dv + (tok0 + ki) * lddv + static_cast<int64_t>(kvh) * HD, dvacc, 1.f, hl);
+  }
+}
+
+// ------------------------------------------ backward: dK, dV (bf16), split roles
+// Used for head_dim 128.  Block = one key block of 32*NKS keys of one (batch,
+// kv head), 2*NKS waves.  Each 32-key sub-tile is shared by two waves with
+// different roles, so that no wave carries both the dK and the dV accumulators
+// (that would need ~300 registers at head_dim 128, i.e. one wave per SIMD):
+//   wave A (waves 0..NKS-1):    holds K;  S = Q K^T, P = exp(S - lse) -> LDS
+//                               (fp32), dV^T += dO^T P
+//   wave B (waves NKS..2NKS-1): holds V;  dP = dO V^T, dS = P (dP - delta) with
+//                               P read from LDS, dK^T += Q^T dS, dK = scale * dK
+// Every query tile runs in two phases separated by a barrier: phase 1 forms S
+// (A) and dP (B), phase 2 the two accumulating products; both roles issue the
+// same number of MFMAs in each phase.  The loop runs over the GQA group's query
+// heads and the BQ-query tiles at or after the block's first key (Q, dO, lse
+// and delta double-buffered in LDS, prefetched through registers), so each kv
+// head's gradient is complete inside one block: no atomics.  Blocks are
+// numbered heaviest (earliest keys, most causal work) first.
+template <int HD>
+struct DkdvTiles {
+  static constexpr int NKS = 2;  // 32-key sub-tiles per block
+  static constexpr int BQ = 32;  // queries per tile
+  static constexpr int NT = 2 * NKS * 64;
+};
+
+template <int HD>
+__global__ __launch_bounds__(DkdvTiles<HD>::NT) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_bwd_dkdv(
+    const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
+    const uint16_t* __restrict__ v, int64_t ldv, const uint16_t* __restrict__ dO, int64_t lddo,
+    const float* __restrict__ lse, const float* __restrict__ delta, uint16_t* __restrict__ dk,
+    int64_t lddk, uint16_t* __restrict__ dv, int64_t lddv, int S, int nh, int nkv, int group,
+    float scale_log2, float scale) {
+  constexpr int NKS = DkdvTiles<HD>::NKS, NT = DkdvTiles<HD>::NT, BQ = DkdvTiles<HD>::BQ;
+  constexpr int BKN = NKS * 32, NS = HD / 16, ND = HD / 32, NQT = BQ / 32, TILE = BQ * 2 * HD;
+  __shared__ __align__(16) char sq[2 * TILE];
+  __shared__ __align__(16) char sg[2 * TILE];
+  __shared__ __align__(16) float slse[2][BQ];
+  __shared__ __align__(16) float sdl[2][BQ];
+  __shared__ __align__(16) float sp[NKS][NQT][16 * 64];  // P of each sub-tile, [j/4][lane][4]
+  const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
+  const bool role_a = wave < NKS;
+  const int sub = role_a ? wave : wave - NKS;
+  const int bk = blockIdx.y, b = bk / nkv, kvh = bk - b * nkv;
+  const int kb0 = blockIdx.x * BKN;
+  const int kw = kb0 + sub * 32, ki = kw + l32;
+  const int64_t tok0 = static_cast<int64_t>(b) * S;
+  int a_off = lane_off_a<HD>(lane);
+  int b0 = lane_off_b<HD>(lane, 0), b8 = lane_off_b<HD>(lane, 8);
+
+  bf16x8 kv[NS];  // K (role A) or V (role B) of this lane's key
+  {
+    const uint16_t* src = role_a ? k + (tok0 + ki) * ldk : v + (tok0 + ki) * ldv;
+    src += static_cast<int64_t>(kvh) * HD + 8 * hl;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) kv[s] = ki < S ? ld_frag(src + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
+  }
+  f32x16 acc[ND];  // dV^T (role A) or dK^T (role B)
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt) acc[dt] = zero16();
+
+  // iteration space: (query head of the group) x (query tiles from the block's first key)
+  const int qt0 = kb0 / BQ, qt_end = (S + BQ - 1) / BQ;
+  const int n_it = group * (qt_end - qt0);
+  const int64_t h0 = static_cast<int64_t>(kvh) * group;
+  const uint16_t* qg = q + tok0 * ldq + h0 * HD;
+  const uint16_t* gg = dO + tok0 * lddo + h0 * HD;
+  const float* lg = lse + (static_cast<int64_t>(b) * nh + h0) * S;
+  const float* dg = delta + (static_cast<int64_t>(b) * nh + h0) * S;
+  QTileStream<HD, BQ, NT> pre;
+  pre.qt = qt0;
+  if (n_it > 0) {
+    pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, qt_end, tid);
+    pre.commit(sq, sg, slse[0], sdl[0], tid);
+  }
+  __syncthreads();
+  int cqt = qt0;  // query tile of the current iteration
+  for (int it = 0; it < n_it; ++it) {
+    const int st = it & 1;
+    const bool more = it + 1 < n_it;
+    refresh_offsets(a_off, b0, b8);
+    if (more) pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, qt_end, tid);
+    const int q0 = cqt * BQ;
+    // some query of the tile reaches this sub-tile's keys (same answer for both roles)
+    const bool active = kw < S && q0 + BQ - 1 >= kw;
+    const bool need_mask = (q0 < kw + 31) || (q0 + BQ > S) || (kw + 32 > S);
+    const char* Q = sq + st * TILE;
+    const char* G = sg + st * TILE;
+    f32x16 x[NQT];  // S then P (role A) / dP then dS (role B), rows = queries, column = key ki
+    // phase 1: S (A) or dP (B)
+    if (active) {
+      const char* X = role_a ? Q : G;
+#pragma unroll
+      for (int u = 0; u < NQT; ++u) {
+        x[u] = zero16();
+#pragma unroll
+        for (int s = 0; s < NS; ++s) x[u] = mfma(lds_frag<HD>(X, a_off, 32 * u, s), kv[s], x[u]);
+      }
+      if (role_a) {
+#pragma unroll
+        for (int u = 0; u < NQT; ++u) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const float4 L4 = *reinterpret_cast<const float4*>(&slse[st][32 * u + 8 * g + 4 * hl]);
+            const float Lv[4] = {L4.x, L4.y, L4.z, L4.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[u][4 * g + e] = fast_exp2(fmaf(x[u][4 * g + e], scale_log2, Lv[e]));
+          }
+          if (need_mask) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+              const int qa = q0 + 32 * u + acc_row(j, hl);
+              x[u][j] = ((ki > qa) | (qa >= S) | (ki >= S)) ? 0.f : x[u][j];
+            }
+          }
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<float4*>(&sp[sub][u][(g * 64 + lane) * 4]) =
+                make_float4(x[u][4 * g], x[u][4 * g + 1], x[u][4 * g + 2], x[u][4 * g + 3]);
+        }
+      }
+    }
+    __syncthreads();
+    // phase 2: dV^T += dO^T P (A) or dS = P (dP - delta), dK^T += Q^T dS (B)
+    if (active) {
+      if (!role_a) {
+#pragma unroll
+        for (int u = 0; u < NQT; ++u)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const float4 D4 = *reinterpret_cast<const float4*>(&sdl[st][32 * u + 8 * g + 4 * hl]);
+            const float4 P4 = *reinterpret_cast<const float4*>(&sp[sub][u][(g * 64 + lane) * 4]);
+            const float Dv[4] = {D4.x, D4.y, D4.z, D4.w};
+            const float Pv[4] = {P4.x, P4.y, P4.z, P4.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[u][4 * g + e] = Pv[e] * (x[u][4 * g + e] - Dv[e]);
+          }
+      }
+      const char* Y = role_a ? G : Q;
+#pragma unroll
+      for (int u = 0; u < NQT; ++u)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const bf16x8 f = pack_frag(x[u], 8 * s2);
+#pragma unroll
+          for (int dt = 0; dt < ND; ++dt)
+            acc[dt] = mfma(lds_frag_tr<HD>(Y, b0, b8, 32 * u + 16 * s2, dt), f, acc[dt]);
+        }
+    }
+    if (more) pre.commit(sq + (st ^ 1) * TILE, sg + (st ^ 1) * TILE, slse[st ^ 1], sdl[st ^ 1], tid);
+    if (++cqt == qt_end) cqt = qt0;
+    __syncthreads();
+  }
+  if (ki < S) {
+    if (role_a)
+      store_rows_T<HD>(dv + (tok0 + ki) * lddv + static_cast<int64_t>(kvh) * HD, acc, 1.f, hl);
+    else
+      store_rows_T<HD>(dk + (tok0 + ki) * lddk + static_cast<int64_t>(kvh) * HD, acc, scale, hl);
   }
 }
 
@@ -757,7 +974,7 @@ extern "C" int fh_attn_fwd(fh_dtype dt, const void* q, int64_t ldq, const void* 
   const int group = static_cast<int>(n_heads / n_kv_heads);
   if (dt == FH_BF16) {
     dispatch_hd(head_dim, [&](auto hdc) {
-      constexpr int BM = 4 * 32 * FwdTiles<hdc()>::QT;
+      constexpr int BM = 128;
       const dim3 grid(static_cast<unsigned>((seq_len + BM - 1) / BM),
                       static_cast<unsigned>(batch * n_heads));
       hipLaunchKernelGGL((k_attn_fwd<hdc()>), grid, dim3(256), 0, stream,
@@ -809,20 +1026,33 @@ extern "C" int fh_attn_bwd(fh_dtype dt, const void* q, int64_t ldq, const void* 
     // dQ first: its prologue writes delta = rowsum(dO*O), which dK/dV reads.
     const dim3 gq(static_cast<unsigned>((seq_len + 127) / 128), static_cast<unsigned>(batch * n_heads));
     dispatch_hd(head_dim, [&](auto hdc) {
-      using DT = DkdvTiles<hdc()>;
-      const int64_t nkb = (seq_len + DT::NWH * 32 - 1) / (DT::NWH * 32);
-      const dim3 gk(static_cast<unsigned>((nkb + 1) / 2), static_cast<unsigned>(batch * n_kv_heads));
-      hipLaunchKernelGGL((k_attn_bwd_dq<hdc()>), gq, dim3(256), 0, stream,
+      constexpr int HD = decltype(hdc)::value;
+      hipLaunchKernelGGL((k_attn_bwd_dq<HD>), gq, dim3(256), 0, stream,
                          static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(k), ldk,
                          static_cast<const uint16_t*>(v), ldv, static_cast<const uint16_t*>(o), ldo,
                          static_cast<const uint16_t*>(dout), lddo, lse, delta,
                          static_cast<uint16_t*>(dq), lddq, S, nh, group, scale * kLog2e, scale);
-      hipLaunchKernelGGL((k_attn_bwd_dkdv<hdc()>), gk, dim3(DT::NT), 0, stream,
-                         static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(k), ldk,
-                         static_cast<const uint16_t*>(v), ldv, static_cast<const uint16_t*>(dout),
-                         lddo, lse, delta, static_cast<uint16_t*>(dk), lddk,
-                         static_cast<uint16_t*>(dv), lddv, S, nh, nkv, group, scale * kLog2e,
-                         scale);
+      const auto kq = static_cast<const uint16_t*>(q);
+      const auto kk = static_cast<const uint16_t*>(k);
+      const auto kvp = static_cast<const uint16_t*>(v);
+      const auto kg = static_cast<const uint16_t*>(dout);
+      const auto kdk = static_cast<uint16_t*>(dk);
+      const auto kdv = static_cast<uint16_t*>(dv);
+      if constexpr (HD <= 64) {
+        using DT = DkdvFusedTiles<HD>;
+        const int64_t nkb = (seq_len + DT::NWH * 32 - 1) / (DT::NWH * 32);
+        const dim3 gk(static_cast<unsigned>((nkb + 1) / 2), static_cast<unsigned>(batch * n_kv_heads));
+        hipLaunchKernelGGL((k_attn_bwd_dkdv_fused<HD>), gk, dim3(DT::NT), 0, stream, kq, ldq, kk,
+                           ldk, kvp, ldv, kg, lddo, lse, delta, kdk, lddk, kdv, lddv, S, nh, nkv,
+                           group, scale * kLog2e, scale);
+      } else {
+        using DT = DkdvTiles<HD>;
+        const int64_t nkb = (seq_len + DT::NKS * 32 - 1) / (DT::NKS * 32);
+        const dim3 gk(static_cast<unsigned>(nkb), static_cast<unsigned>(batch * n_kv_heads));
+        hipLaunchKernelGGL((k_attn_bwd_dkdv<HD>), gk, dim3(DT::NT), 0, stream, kq, ldq, kk, ldk,
+                           kvp, ldv, kg, lddo, lse, delta, kdk, lddk, kdv, lddv, S, nh, nkv, group,
+                           scale * kLog2e, scale);
+      }
       return 0;
     });
   } else {

@@ -30,6 +30,15 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
 
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 
+// Two floats rounded to bf16 and packed (a in the low half) by one
+// v_cvt_pk_bf16_f32; same rounding as f2bf.
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
 // ------------------------------------------------------- element traits
 // Elem<T>::load8 / store8 move 8 consecutive elements between memory and
 // fp32 registers with 128-bit accesses (one dwordx4 for bf16, two for fp32).
@@ -63,10 +72,10 @@ struct Elem<uint16_t> {
   }
   __device__ __forceinline__ static void store8(uint16_t* p, const float v[8]) {
     uint4 q;
-    q.x = f2bf(v[0]) | (static_cast<uint32_t>(f2bf(v[1])) << 16);
-    q.y = f2bf(v[2]) | (static_cast<uint32_t>(f2bf(v[3])) << 16);
-    q.z = f2bf(v[4]) | (static_cast<uint32_t>(f2bf(v[5])) << 16);
-    q.w = f2bf(v[6]) | (static_cast<uint32_t>(f2bf(v[7])) << 16);
+    q.x = pk_bf16(v[0], v[1]);
+    q.y = pk_bf16(v[2], v[3]);
+    q.z = pk_bf16(v[4], v[5]);
+    q.w = pk_bf16(v[6], v[7]);
     *reinterpret_cast<uint4*>(p) = q;
   }
   // Rounds a value to the precision a tensor of this dtype would hold.
