@@ -145,6 +145,26 @@ __device__ __forceinline__ bf16x8 pack_frag(const f32x16& acc, int j0) {
                               pk_bf16(acc[j0 + 4], acc[j0 + 5]), pk_bf16(acc[j0 + 6], acc[j0 + 7])));
 }
 
+// XCD-aware block order.  Workgroup L = blockIdx.x + gridDim.x*blockIdx.y is
+// dispatched to XCD L % 8 (8 XCDs, each with its own L2).  Grids here are
+// (work items along x, heads along y) with causal work varying along x, so the
+// identity mapping gives XCD k only the x == k (mod 8) items of every head: an
+// up to 2.4x imbalance between XCDs at 16 items per head.  This maps XCD k's
+// j-th workgroup to head y = k*(gridDim.y/8) + j % (gridDim.y/8) and rank
+// x = j / (gridDim.y/8): every XCD covers all x of its own contiguous set of
+// heads (balanced work; one head's K/V/Q/dO stay in one L2), ranks in order
+// (rank 0 = dispatched first).  Needs gridDim.y % 8 == 0, else identity.
+struct XcdOrder {
+  int rank, y;
+};
+__device__ __forceinline__ XcdOrder xcd_order() {
+  const int nx = gridDim.x, ny = gridDim.y;
+  if (ny % 8 != 0) return {static_cast<int>(blockIdx.x), static_cast<int>(blockIdx.y)};
+  const int L = blockIdx.x + nx * blockIdx.y;
+  const int xcd = L & 7, j = L >> 3, nyx = ny >> 3;
+  return {j / nyx, xcd * nyx + j % nyx};
+}
+
 // Row (M index) of accumulator entry j for lane half hl.
 __device__ __forceinline__ int acc_row(int j, int hl) { return 8 * (j >> 2) + 4 * hl + (j & 3); }
 
@@ -206,37 +226,55 @@ __device__ __forceinline__ void store_rows_T(uint16_t* out_row, const f32x16 (&a
 }
 
 // ------------------------------------------------------------ forward (bf16)
-// Block = 4 waves x 32 queries of one (batch, head); loop over 64-key blocks,
-// double-buffered in LDS: the next block's K/V are loaded into registers while
-// the current one is multiplied, then written to the other LDS stage; one
-// barrier per block.  Heaviest (latest) query blocks are dispatched first.
+// Block = 4 waves x (32*QT) queries of one (batch, head); loop over 64-key
+// blocks, double-buffered in LDS: the next block's K/V are loaded into
+// registers while the current one is multiplied, then written to the other
+// LDS stage; one barrier per block.  QT query tiles per wave: QT = 2 would
+// let every K/V fragment read from LDS feed two MFMAs, but its registers cost
+// a wave of occupancy and it measured slower at head_dim 64 (342 vs 308 us at
+// the TinyLlama shape), so QT = 1.  Heaviest (latest) query blocks first.
+template <int HD>
+struct FwdTiles {
+  static constexpr int QT = 1;
+};
+
 template <int HD>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_fwd(
     const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
     const uint16_t* __restrict__ v, int64_t ldv, uint16_t* __restrict__ o, int64_t ldo,
     float* __restrict__ lse, int S, int nh, int group, float scale_log2) {
-  constexpr int BM = 128, BN = 64, NS = HD / 16, ND = HD / 32, TILE = BN * 2 * HD;
+  constexpr int QT = FwdTiles<HD>::QT;
+  constexpr int BM = 4 * 32 * QT, BN = 64, NS = HD / 16, ND = HD / 32, TILE = BN * 2 * HD;
   __shared__ __align__(16) char sk[2 * TILE];
   __shared__ __align__(16) char sv[2 * TILE];
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
-  const int bh = blockIdx.y, b = bh / nh, h = bh - b * nh, kvh = h / group;
-  const int q0 = (gridDim.x - 1 - blockIdx.x) * BM;
-  const int qw = q0 + wave * 32, qi = qw + l32;
+  const XcdOrder ord = xcd_order();
+  const int bh = ord.y, b = bh / nh, h = bh - b * nh, kvh = h / group;
+  const int q0 = (gridDim.x - 1 - ord.rank) * BM;  // heaviest (latest) query blocks first
+  const int qw = q0 + wave * 32 * QT;  // first query of this wave
   const int64_t tok0 = static_cast<int64_t>(b) * S;
   int a_off = lane_off_a<HD>(lane);
   int b0 = lane_off_b<HD>(lane, 0), b8 = lane_off_b<HD>(lane, 8);
 
-  bf16x8 qf[NS];
-  {
+  bf16x8 qf[QT][NS];
+#pragma unroll
+  for (int u = 0; u < QT; ++u) {
+    const int qi = qw + 32 * u + l32;
     const uint16_t* qrow = q + (tok0 + qi) * ldq + static_cast<int64_t>(h) * HD + 8 * hl;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) qf[s] = qi < S ? ld_frag(qrow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
+    for (int s = 0; s < NS; ++s)
+      qf[u][s] = qi < S ? ld_frag(qrow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
   }
-  f32x16 oacc[ND];
+  f32x16 oacc[QT][ND];
+  float m[QT], l[QT];  // running max (log2 units) and sum of weights per query tile
 #pragma unroll
-  for (int dt = 0; dt < ND; ++dt) oacc[dt] = zero16();
-  float m = -INFINITY, l = 0.f;  // running max (log2 units) and sum of weights
+  for (int u = 0; u < QT; ++u) {
+    m[u] = -INFINITY;
+    l[u] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) oacc[u][dt] = zero16();
+  }
 
   const int kend = min(S, q0 + BM);
   const int nkb = (kend + BN - 1) / BN;
@@ -256,60 +294,75 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
       pk.load(kb_ptr + static_cast<int64_t>(k0 + BN) * ldk, ldk, S - k0 - BN, tid);
       pv.load(vb_ptr + static_cast<int64_t>(k0 + BN) * ldv, ldv, S - k0 - BN, tid);
     }
-    if (k0 <= qw + 31) {  // some key of the block precedes some query of the wave
+    if (k0 <= qw + 32 * QT - 1) {  // some key of the block precedes some query of the wave
       const char* K = sk + st * TILE;
       const char* V = sv + st * TILE;
-      f32x16 x[BN / 32];  // raw scores S^T, rows = keys, column = query qi
+      f32x16 x[BN / 32][QT];  // raw scores S^T, rows = keys, column = query
 #pragma unroll
       for (int t = 0; t < BN / 32; ++t) {
-        x[t] = zero16();
 #pragma unroll
-        for (int s = 0; s < NS; ++s) x[t] = mfma(lds_frag<HD>(K, a_off, 32 * t, s), qf[s], x[t]);
+        for (int u = 0; u < QT; ++u) x[t][u] = zero16();
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          const bf16x8 a = lds_frag<HD>(K, a_off, 32 * t, s);
+#pragma unroll
+          for (int u = 0; u < QT; ++u) x[t][u] = mfma(a, qf[u][s], x[t][u]);
+        }
       }
-      float mloc = -INFINITY;
-      if ((k0 + BN - 1 > qw) || (k0 + BN > S)) {  // diagonal or ragged block: mask
+      const bool need_mask = (k0 + BN - 1 > qw) || (k0 + BN > S);
+#pragma unroll
+      for (int u = 0; u < QT; ++u) {
+        const int qi = qw + 32 * u + l32;
+        float mloc = -INFINITY;
+        if (need_mask) {  // diagonal or ragged block
+#pragma unroll
+          for (int t = 0; t < BN / 32; ++t)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+              const int key = k0 + 32 * t + acc_row(j, hl);
+              x[t][u][j] = ((key > qi) | (key >= S)) ? -INFINITY : x[t][u][j];
+              mloc = fmaxf(mloc, x[t][u][j]);
+            }
+        } else {
+#pragma unroll
+          for (int t = 0; t < BN / 32; ++t)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) mloc = fmaxf(mloc, x[t][u][j]);
+        }
+        mloc = xor32_max(mloc) * scale_log2;
+        if (wave_any(mloc > m[u] + kRescaleSlack)) {
+          const float mnew = fmaxf(m[u], mloc);
+          const float alpha = fast_exp2(m[u] - mnew);
+          m[u] = mnew;
+          l[u] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) oacc[u][dt][j] *= alpha;
+        }
+        const float nm = -m[u];
+        float lsum = 0.f;
 #pragma unroll
         for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
-            const int key = k0 + 32 * t + acc_row(j, hl);
-            x[t][j] = ((key > qi) | (key >= S)) ? -INFINITY : x[t][j];
-            mloc = fmaxf(mloc, x[t][j]);
+            const float p = fast_exp2(fmaf(x[t][u][j], scale_log2, nm));
+            x[t][u][j] = p;
+            lsum += p;
           }
-      } else {
-#pragma unroll
-        for (int t = 0; t < BN / 32; ++t)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) mloc = fmaxf(mloc, x[t][j]);
+        l[u] += lsum;
       }
-      mloc = xor32_max(mloc) * scale_log2;
-      if (wave_any(mloc > m + kRescaleSlack)) {
-        const float mnew = fmaxf(m, mloc);
-        const float alpha = fast_exp2(m - mnew);
-        m = mnew;
-        l *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
-      }
-      const float nm = -m;
-      float lsum = 0.f;
-#pragma unroll
-      for (int t = 0; t < BN / 32; ++t)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const float p = fast_exp2(fmaf(x[t][j], scale_log2, nm));
-          x[t][j] = p;
-          lsum += p;
-        }
-      l += lsum;
 #pragma unroll
       for (int s = 0; s < BN / 16; ++s) {
-        const bf16x8 pf = pack_frag(x[s >> 1], 8 * (s & 1));
+        bf16x8 pf[QT];
 #pragma unroll
-        for (int dt = 0; dt < ND; ++dt)
-          oacc[dt] = mfma(lds_frag_tr<HD>(V, b0, b8, 16 * s, dt), pf, oacc[dt]);
+        for (int u = 0; u < QT; ++u) pf[u] = pack_frag(x[s >> 1][u], 8 * (s & 1));
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt) {
+          const bf16x8 a = lds_frag_tr<HD>(V, b0, b8, 16 * s, dt);
+#pragma unroll
+          for (int u = 0; u < QT; ++u) oacc[u][dt] = mfma(a, pf[u], oacc[u][dt]);
+        }
       }
     }
     if (more) {
@@ -318,10 +371,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     }
     __syncthreads();
   }
-  const float lt = xor32_sum(l);
-  if (qi < S) {
-    store_rows_T<HD>(o + (tok0 + qi) * ldo + static_cast<int64_t>(h) * HD, oacc, 1.f / lt, hl);
-    if (lse != nullptr && hl == 0) lse[static_cast<int64_t>(bh) * S + qi] = (m + log2f(lt)) * kLn2;
+#pragma unroll
+  for (int u = 0; u < QT; ++u) {
+    const int qi = qw + 32 * u + l32;
+    const float lt = xor32_sum(l[u]);
+    if (qi < S) {
+      store_rows_T<HD>(o + (tok0 + qi) * ldo + static_cast<int64_t>(h) * HD, oacc[u], 1.f / lt, hl);
+      if (lse != nullptr && hl == 0) lse[static_cast<int64_t>(bh) * S + qi] = (m[u] + log2f(lt)) * kLn2;
+    }
   }
 }
 
@@ -369,8 +426,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   __shared__ __align__(16) char sv[2 * TILE];
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
-  const int bh = blockIdx.y, b = bh / nh, h = bh - b * nh, kvh = h / group;
-  const int q0 = (gridDim.x - 1 - blockIdx.x) * BM;
+  const XcdOrder ord = xcd_order();
+  const int bh = ord.y, b = bh / nh, h = bh - b * nh, kvh = h / group;
+  const int q0 = (gridDim.x - 1 - ord.rank) * BM;  // heaviest (latest) query blocks first
   const int qw = q0 + wave * 32, qi = qw + l32;
   const int64_t tok0 = static_cast<int64_t>(b) * S;
   int a_off = lane_off_a<HD>(lane);
@@ -540,9 +598,10 @@ __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves
   __shared__ __align__(16) float sdl[2][BQ];
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
-  const int bk = blockIdx.y, b = bk / nkv, kvh = bk - b * nkv;
+  const XcdOrder ord = xcd_order();
+  const int bk = ord.y, b = bk / nkv, kvh = bk - b * nkv;
   const int nkb = (S + BKN - 1) / BKN;
-  const int jlo = blockIdx.x, jhi = nkb - 1 - blockIdx.x;
+  const int jlo = ord.rank, jhi = nkb - 1 - ord.rank;
   const bool upper = wave >= NWH;
   const bool has_keys = !upper || jhi > jlo;
   const int kw = (upper ? jhi : jlo) * BKN + (wave % NWH) * 32, ki = kw + l32;
@@ -688,8 +747,9 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) __attribute__((amdgpu_waves_per_
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const bool role_a = wave < NKS;
   const int sub = role_a ? wave : wave - NKS;
-  const int bk = blockIdx.y, b = bk / nkv, kvh = bk - b * nkv;
-  const int kb0 = blockIdx.x * BKN;
+  const XcdOrder ord = xcd_order();
+  const int bk = ord.y, b = bk / nkv, kvh = bk - b * nkv;
+  const int kb0 = ord.rank * BKN;  // heaviest (earliest keys) first
   const int kw = kb0 + sub * 32, ki = kw + l32;
   const int64_t tok0 = static_cast<int64_t>(b) * S;
   int a_off = lane_off_a<HD>(lane);
@@ -974,7 +1034,7 @@ extern "C" int fh_attn_fwd(fh_dtype dt, const void* q, int64_t ldq, const void* 
   const int group = static_cast<int>(n_heads / n_kv_heads);
   if (dt == FH_BF16) {
     dispatch_hd(head_dim, [&](auto hdc) {
-      constexpr int BM = 128;
+      constexpr int BM = 4 * 32 * FwdTiles<decltype(hdc)::value>::QT;
       const dim3 grid(static_cast<unsigned>((seq_len + BM - 1) / BM),
                       static_cast<unsigned>(batch * n_heads));
       hipLaunchKernelGGL((k_attn_fwd<hdc()>), grid, dim3(256), 0, stream,
