@@ -75,6 +75,12 @@ def parse_args():
                     help="timed steps of the reference path on the GPU (0 to skip)")
     ap.add_argument("--cpu-sample-tokens", type=int, default=512,
                     help="tokens (one sequence) of the CPU baseline sample (0 to skip)")
+    ap.add_argument("--no-tuned-gemms", action="store_true",
+                    help="use the library's default GEMM heuristics instead of the shipped "
+                         "TunableOp solutions (femtotron_amd/tuned/tunableop_gfx950.csv)")
+    ap.add_argument("--tune-gemms", default=None, metavar="CSV",
+                    help="run TunableOp's search for every projection GEMM of --workload, write "
+                         "the results to CSV and exit")
     ap.add_argument("--profile-kernel", default=None,
                     help="launch only this fused kernel (swiglu_fwd, swiglu_bwd, rmsnorm_fwd, "
                          "add_rmsnorm_fwd, rmsnorm_bwd, rope_fwd, residual_add, attn_fwd, attn_bwd) at "
@@ -355,6 +361,14 @@ def main() -> int:
         return 2
     import torch
 
+    from femtotron_amd import gemm_tuning
+    if args.tune_gemms:
+        gemm_tuning.tune(workloads=(args.workload,), path=args.tune_gemms, log=log)
+        print(json.dumps({"tuned_gemms": args.tune_gemms}), flush=True)
+        return 0
+    tuned = False if args.no_tuned_gemms else gemm_tuning.use_tuned_gemms()
+    log(f"library GEMMs: {'shipped TunableOp solutions' if tuned else 'default heuristics'}")
+
     if args.profile_kernel:
         print(json.dumps(profile_kernel(torch, args.profile_kernel)), flush=True)
         return 0
@@ -444,6 +458,8 @@ def main() -> int:
         "roofline": roofline,
         "fused_kernels_hbm": rows,
         "attention_mfma": mfma,
+        "gemms": ("hipBLASLt/rocBLAS, TunableOp solutions from femtotron_amd/tuned/"
+                  "tunableop_gfx950.csv" if tuned else "hipBLASLt default heuristics"),
         "activation_bytes_per_token": round(act_fused, 1),
         "reference_gpu": ref,
         "cpu_baseline": cpu,
