@@ -39,6 +39,21 @@ __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
+// ------------------------------------------------------ fast division
+// n / d for 32-bit n by a runtime divisor fixed per launch: with
+// M = ceil(2^64 / d), n / d = floor(M * n / 2^64) exactly for every 32-bit n
+// and 1 < d < 2^32 (Lemire, Kaser, Kurz, "Faster Remainder by Direct
+// Computation", 2019).  M is computed on the host; d == 1 is special-cased.
+struct FastDiv {
+  uint64_t m;
+  uint32_t d;
+  FastDiv() = default;
+  __host__ explicit FastDiv(uint32_t div) : m(div > 1 ? ~uint64_t(0) / div + 1 : 0), d(div) {}
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    return d == 1 ? n : static_cast<uint32_t>(__umul64hi(m, n));
+  }
+};
+
 // ------------------------------------------------------- element traits
 // Elem<T>::load8 / store8 move 8 consecutive elements between memory and
 // fp32 registers with 128-bit accesses (one dwordx4 for bf16, two for fp32).
@@ -70,13 +85,16 @@ struct Elem<uint16_t> {
       v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
     }
   }
-  __device__ __forceinline__ static void store8(uint16_t* p, const float v[8]) {
-    uint4 q;
-    q.x = pk_bf16(v[0], v[1]);
-    q.y = pk_bf16(v[2], v[3]);
-    q.z = pk_bf16(v[4], v[5]);
-    q.w = pk_bf16(v[6], v[7]);
+  // 8 floats rounded to bf16 and packed (exact for bf16-representable values).
+  __device__ __forceinline__ static Raw pack(const float v[8]) {
+    return make_uint4(pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3]), pk_bf16(v[4], v[5]),
+                      pk_bf16(v[6], v[7]));
+  }
+  __device__ __forceinline__ static void straw(uint16_t* p, const Raw& q) {
     *reinterpret_cast<uint4*>(p) = q;
+  }
+  __device__ __forceinline__ static void store8(uint16_t* p, const float v[8]) {
+    straw(p, pack(v));
   }
   // Rounds a value to the precision a tensor of this dtype would hold.
   __device__ __forceinline__ static float rnd(float f) { return round_bf(f); }
@@ -103,9 +121,15 @@ struct Elem<float> {
     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
     v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
   }
+  __device__ __forceinline__ static Raw pack(const float v[8]) {
+    return Raw{make_float4(v[0], v[1], v[2], v[3]), make_float4(v[4], v[5], v[6], v[7])};
+  }
+  __device__ __forceinline__ static void straw(float* p, const Raw& q) {
+    *reinterpret_cast<float4*>(p) = q.a;
+    *reinterpret_cast<float4*>(p + 4) = q.b;
+  }
   __device__ __forceinline__ static void store8(float* p, const float v[8]) {
-    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
-    *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    straw(p, pack(v));
   }
   __device__ __forceinline__ static float rnd(float f) { return f; }
   __device__ __forceinline__ static float ld1(const float* p) { return *p; }

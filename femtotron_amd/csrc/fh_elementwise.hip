@@ -9,6 +9,8 @@
 //   LlamaMLP act_fn(gate)*up             models/llama/modeling_llama.py:174-176
 //   SiLUActivation = F.silu              activations.py:93-103
 //   residual adds                        models/llama/modeling_llama.py:317,323
+#include <type_traits>
+
 #include "fh_common.hpp"
 
 namespace fh {
@@ -37,25 +39,62 @@ __device__ __forceinline__ float silu_f(float g) { return g * sigmoid_f(g); }
 constexpr int kRopeHG = FH_ROPE_HEADS_PER_THREAD;
 constexpr int kChunks = FH_EW_CHUNKS;
 
+// Flat chunk index -> (row, first column) of a row-strided [rows, cols]
+// operand.  Index spaces below 2^32 (every layer shape) use the host-computed
+// multiplier; WIDE launches keep 64-bit division.
+template <bool WIDE>
+__device__ __forceinline__ void row_col(int64_t idx, int cpr, const FastDiv& fd, int64_t& r,
+                                        int& c) {
+  if constexpr (WIDE) {
+    r = idx / cpr;
+    c = static_cast<int>(idx - r * cpr) * 8;
+  } else {
+    const uint32_t i = static_cast<uint32_t>(idx), q = fd.div(i);
+    r = q;
+    c = static_cast<int>(i - q * static_cast<uint32_t>(cpr)) * 8;
+  }
+}
+
+inline bool wide(int64_t n) { return n >= (int64_t(1) << 32); }
+
 // One thread = 8 rotation pairs (i, i + d/2) of up to kRopeHG heads of one
 // token: cos/sin for the pairs are loaded once and reused across the heads,
 // and all the heads' loads are issued before the first store.
-template <typename T, bool BWD>
+// Index maps of one launch: token = idx / per_tok, head group = rem / cpp,
+// position = token % seq_len (host-computed multipliers; WIDE launches, whose
+// index space exceeds 32 bits, divide in 64 bits).
+struct RopeDivs {
+  FastDiv per_tok, cpp, seq;
+};
+
+template <typename T, bool BWD, bool WIDE>
 __global__ __launch_bounds__(256) void k_rope(T* __restrict__ qk, int64_t ld, int64_t tokens,
                                               int64_t seq_len, int n_heads, int head_dim,
                                               const T* __restrict__ cosv,
-                                              const T* __restrict__ sinv, int cos_per_token) {
+                                              const T* __restrict__ sinv, int cos_per_token,
+                                              RopeDivs dv) {
   const int cpp = head_dim >> 4;  // 8-wide chunks per half head
   const int ngrp = (n_heads + kRopeHG - 1) / kRopeHG;
   const int64_t per_tok = static_cast<int64_t>(ngrp) * cpp;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= tokens * per_tok) return;
-  const int64_t t = idx / per_tok;
-  const int rem = static_cast<int>(idx - t * per_tok);
-  const int grp = rem / cpp;
-  const int c = (rem - grp * cpp) * 8;
+  int64_t t, crow;
+  int grp, c;
+  if constexpr (WIDE) {
+    t = idx / per_tok;
+    const int rem = static_cast<int>(idx - t * per_tok);
+    grp = rem / cpp;
+    c = (rem - grp * cpp) * 8;
+    crow = cos_per_token ? t : (t % seq_len);
+  } else {
+    const uint32_t i = static_cast<uint32_t>(idx), t32 = dv.per_tok.div(i);
+    const uint32_t rem = i - t32 * static_cast<uint32_t>(per_tok);
+    grp = static_cast<int>(dv.cpp.div(rem));
+    c = static_cast<int>(rem - static_cast<uint32_t>(grp * cpp)) * 8;
+    t = t32;
+    crow = cos_per_token ? t : static_cast<int64_t>(t32 - dv.seq.div(t32) * static_cast<uint32_t>(seq_len));
+  }
   const int half = head_dim >> 1;
-  const int64_t crow = cos_per_token ? t : (t % seq_len);
 
   const T* cb = cosv + crow * head_dim + c;
   const T* sb = sinv + crow * head_dim + c;
@@ -100,11 +139,11 @@ __global__ __launch_bounds__(256) void k_rope(T* __restrict__ qk, int64_t ld, in
 // Streaming kernels: a block covers 256*kChunks consecutive 8-element chunks;
 // thread t takes chunks t, t+256, ... (coalesced per step) and issues all its
 // loads before computing.
-template <typename T>
+template <typename T, bool WIDE>
 __global__ __launch_bounds__(256) void k_swiglu_fwd(const T* __restrict__ g,
                                                     const T* __restrict__ u, int64_t ld_gu,
                                                     T* __restrict__ p, int64_t ld_p,
-                                                    int64_t rows, int cols) {
+                                                    int64_t rows, int cols, FastDiv fd) {
   using Raw = typename Elem<T>::Raw;
   const int cpr = cols >> 3;
   const int64_t total = rows * cpr;
@@ -114,8 +153,9 @@ __global__ __launch_bounds__(256) void k_swiglu_fwd(const T* __restrict__ g,
   for (int k = 0; k < kChunks; ++k) {
     const int64_t idx = first + 256 * k;
     if (idx < total) {
-      const int64_t r = idx / cpr;
-      const int c = static_cast<int>(idx - r * cpr) * 8;
+      int64_t r;
+      int c;
+      row_col<WIDE>(idx, cpr, fd, r, c);
       gr[k] = Elem<T>::ldraw(g + r * ld_gu + c);
       ur[k] = Elem<T>::ldraw(u + r * ld_gu + c);
     }
@@ -124,8 +164,9 @@ __global__ __launch_bounds__(256) void k_swiglu_fwd(const T* __restrict__ g,
   for (int k = 0; k < kChunks; ++k) {
     const int64_t idx = first + 256 * k;
     if (idx >= total) break;
-    const int64_t r = idx / cpr;
-    const int c = static_cast<int>(idx - r * cpr) * 8;
+    int64_t r;
+    int c;
+    row_col<WIDE>(idx, cpr, fd, r, c);
     float gv[8], uv[8], o[8];
     Elem<T>::unpack(gr[k], gv);
     Elem<T>::unpack(ur[k], uv);
@@ -135,12 +176,12 @@ __global__ __launch_bounds__(256) void k_swiglu_fwd(const T* __restrict__ g,
   }
 }
 
-template <typename T>
+template <typename T, bool WIDE>
 __global__ __launch_bounds__(256) void k_swiglu_bwd(const T* __restrict__ dp, int64_t ld_dp,
                                                     const T* __restrict__ g,
                                                     const T* __restrict__ u, int64_t ld_gu,
                                                     T* __restrict__ dg, T* __restrict__ du,
-                                                    int64_t ld_dgu, int64_t rows, int cols) {
+                                                    int64_t ld_dgu, int64_t rows, int cols, FastDiv fd) {
   using Raw = typename Elem<T>::Raw;
   const int cpr = cols >> 3;
   const int64_t total = rows * cpr;
@@ -150,8 +191,9 @@ __global__ __launch_bounds__(256) void k_swiglu_bwd(const T* __restrict__ dp, in
   for (int k = 0; k < kChunks; ++k) {
     const int64_t idx = first + 256 * k;
     if (idx < total) {
-      const int64_t r = idx / cpr;
-      const int c = static_cast<int>(idx - r * cpr) * 8;
+      int64_t r;
+      int c;
+      row_col<WIDE>(idx, cpr, fd, r, c);
       dr[k] = Elem<T>::ldraw(dp + r * ld_dp + c);
       gr[k] = Elem<T>::ldraw(g + r * ld_gu + c);
       ur[k] = Elem<T>::ldraw(u + r * ld_gu + c);
@@ -161,8 +203,9 @@ __global__ __launch_bounds__(256) void k_swiglu_bwd(const T* __restrict__ dp, in
   for (int k = 0; k < kChunks; ++k) {
     const int64_t idx = first + 256 * k;
     if (idx >= total) break;
-    const int64_t r = idx / cpr;
-    const int c = static_cast<int>(idx - r * cpr) * 8;
+    int64_t r;
+    int c;
+    row_col<WIDE>(idx, cpr, fd, r, c);
     float dv[8], gv[8], uv[8], og[8], ou[8];
     Elem<T>::unpack(dr[k], dv);
     Elem<T>::unpack(gr[k], gv);
@@ -231,17 +274,25 @@ int rope_impl(fh_dtype dt, void* qk, int64_t ld, int64_t tokens, int64_t seq_len
   if (tokens == 0 || n_heads == 0) return FH_OK;
   FH_REQUIRE(qk && cosv && sinv, "rope: null pointer");
   FH_REQUIRE(aligned16(qk) && aligned16(cosv) && aligned16(sinv), "rope: pointers must be 16-byte aligned");
-  const int64_t threads = tokens * ((n_heads + kRopeHG - 1) / kRopeHG) * (head_dim / 16);
-  if (dt == FH_BF16)
-    hipLaunchKernelGGL((k_rope<uint16_t, BWD>), dim3(blocks_for(threads)), dim3(256), 0, s,
-                       static_cast<uint16_t*>(qk), ld, tokens, seq_len, static_cast<int>(n_heads),
-                       static_cast<int>(head_dim), static_cast<const uint16_t*>(cosv),
-                       static_cast<const uint16_t*>(sinv), cos_per_token);
-  else
-    hipLaunchKernelGGL((k_rope<float, BWD>), dim3(blocks_for(threads)), dim3(256), 0, s,
-                       static_cast<float*>(qk), ld, tokens, seq_len, static_cast<int>(n_heads),
-                       static_cast<int>(head_dim), static_cast<const float*>(cosv),
-                       static_cast<const float*>(sinv), cos_per_token);
+  const int64_t per_tok = ((n_heads + kRopeHG - 1) / kRopeHG) * (head_dim / 16);
+  const int64_t threads = tokens * per_tok;
+  const bool w64 = wide(threads) || seq_len >= (int64_t(1) << 32);
+  const RopeDivs dv{FastDiv(static_cast<uint32_t>(per_tok)), FastDiv(static_cast<uint32_t>(head_dim / 16)),
+                    FastDiv(static_cast<uint32_t>(w64 ? 1 : seq_len))};
+  auto go = [&](auto tag, auto wide_c) {
+    using T = decltype(tag);
+    hipLaunchKernelGGL((k_rope<T, BWD, decltype(wide_c)::value>), dim3(blocks_for(threads)),
+                       dim3(256), 0, s, static_cast<T*>(qk), ld, tokens, seq_len,
+                       static_cast<int>(n_heads), static_cast<int>(head_dim),
+                       static_cast<const T*>(cosv), static_cast<const T*>(sinv), cos_per_token, dv);
+  };
+  if (dt == FH_BF16) {
+    if (w64) go(uint16_t{}, std::true_type{});
+    else go(uint16_t{}, std::false_type{});
+  } else {
+    if (w64) go(float{}, std::true_type{});
+    else go(float{}, std::false_type{});
+  }
   return check_launch(BWD ? "fh_rope_bwd" : "fh_rope_fwd");
 }
 
@@ -274,14 +325,20 @@ extern "C" int fh_swiglu_fwd(fh_dtype dt, const void* g, const void* u, int64_t 
   FH_REQUIRE(g && u && p, "swiglu_fwd: null pointer");
   FH_REQUIRE(aligned16(g) && aligned16(u) && aligned16(p), "swiglu_fwd: pointers must be 16-byte aligned");
   const int64_t threads = rows * (cols / 8);
-  if (dt == FH_BF16)
-    hipLaunchKernelGGL((k_swiglu_fwd<uint16_t>), dim3(stream_blocks(threads)), dim3(256), 0, stream,
-                       static_cast<const uint16_t*>(g), static_cast<const uint16_t*>(u), ld_gu,
-                       static_cast<uint16_t*>(p), ld_p, rows, static_cast<int>(cols));
-  else
-    hipLaunchKernelGGL((k_swiglu_fwd<float>), dim3(stream_blocks(threads)), dim3(256), 0, stream,
-                       static_cast<const float*>(g), static_cast<const float*>(u), ld_gu,
-                       static_cast<float*>(p), ld_p, rows, static_cast<int>(cols));
+  const FastDiv fd(static_cast<uint32_t>(cols / 8));
+  auto go = [&](auto tag, auto wide_c) {
+    using T = decltype(tag);
+    hipLaunchKernelGGL((k_swiglu_fwd<T, decltype(wide_c)::value>), dim3(stream_blocks(threads)),
+                       dim3(256), 0, stream, static_cast<const T*>(g), static_cast<const T*>(u),
+                       ld_gu, static_cast<T*>(p), ld_p, rows, static_cast<int>(cols), fd);
+  };
+  if (dt == FH_BF16) {
+    if (wide(threads)) go(uint16_t{}, std::true_type{});
+    else go(uint16_t{}, std::false_type{});
+  } else {
+    if (wide(threads)) go(float{}, std::true_type{});
+    else go(float{}, std::false_type{});
+  }
   return check_launch("fh_swiglu_fwd");
 }
 
@@ -298,16 +355,22 @@ extern "C" int fh_swiglu_bwd(fh_dtype dt, const void* dp, int64_t ld_dp, const v
   FH_REQUIRE(aligned16(dp) && aligned16(g) && aligned16(u) && aligned16(dg) && aligned16(du),
              "swiglu_bwd: pointers must be 16-byte aligned");
   const int64_t threads = rows * (cols / 8);
-  if (dt == FH_BF16)
-    hipLaunchKernelGGL((k_swiglu_bwd<uint16_t>), dim3(stream_blocks(threads)), dim3(256), 0, stream,
-                       static_cast<const uint16_t*>(dp), ld_dp, static_cast<const uint16_t*>(g),
-                       static_cast<const uint16_t*>(u), ld_gu, static_cast<uint16_t*>(dg),
-                       static_cast<uint16_t*>(du), ld_dgu, rows, static_cast<int>(cols));
-  else
-    hipLaunchKernelGGL((k_swiglu_bwd<float>), dim3(stream_blocks(threads)), dim3(256), 0, stream,
-                       static_cast<const float*>(dp), ld_dp, static_cast<const float*>(g),
-                       static_cast<const float*>(u), ld_gu, static_cast<float*>(dg),
-                       static_cast<float*>(du), ld_dgu, rows, static_cast<int>(cols));
+  const FastDiv fd(static_cast<uint32_t>(cols / 8));
+  auto go = [&](auto tag, auto wide_c) {
+    using T = decltype(tag);
+    hipLaunchKernelGGL((k_swiglu_bwd<T, decltype(wide_c)::value>), dim3(stream_blocks(threads)),
+                       dim3(256), 0, stream, static_cast<const T*>(dp), ld_dp,
+                       static_cast<const T*>(g), static_cast<const T*>(u), ld_gu,
+                       static_cast<T*>(dg), static_cast<T*>(du), ld_dgu, rows,
+                       static_cast<int>(cols), fd);
+  };
+  if (dt == FH_BF16) {
+    if (wide(threads)) go(uint16_t{}, std::true_type{});
+    else go(uint16_t{}, std::false_type{});
+  } else {
+    if (wide(threads)) go(float{}, std::true_type{});
+    else go(float{}, std::false_type{});
+  }
   return check_launch("fh_swiglu_bwd");
 }
 

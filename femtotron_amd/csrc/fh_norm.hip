@@ -3,20 +3,21 @@
 // Reference arithmetic: LlamaRMSNorm.forward, transformers 5.15.0
 // models/llama/modeling_llama.py:62-67, and the residual adds at :317/:323.
 //
-// Layout: one wave64 per row.  Lane l owns the 8-element chunks starting at
-// columns (i*64 + l)*8, i < NV, so each load instruction of a wave covers one
-// contiguous 1 KiB (bf16) span of the row; the row stays in registers between
-// the reduction and the normalisation, so x is read from HBM exactly once.
+// Layout: lane l of a wave owns the 8-element chunks starting at columns
+// (i*64 + l)*8 of its share of a row, so each load instruction of a wave
+// covers one contiguous 1 KiB (bf16) span; rows stay in registers, packed as
+// loaded, between the reduction and the normalisation, so every input is read
+// from HBM exactly once.  The weight row is loaded once per wave, together
+// with the first data, so its latency is never on a row's critical path.
 #include "fh_common.hpp"
 
 namespace fh {
 namespace {
 
-constexpr int kRowsPerBlock = 4;  // 4 waves = 256 threads
+constexpr int kWavesPerBlock = 4;  // 256 threads
 
-// Rows per wave kept in flight (FH_NORM_FWD_ROWS).  One row per wave, i.e.
-// more waves, measured faster than two rows per wave at T=16384, H=2048
-// (4.76 vs 4.39 TB/s).
+// Forward: one wave per R consecutive rows (all loads of the R rows issued
+// before the first reduction).
 #ifndef FH_NORM_FWD_ROWS
 #define FH_NORM_FWD_ROWS 1
 #endif
@@ -25,17 +26,18 @@ struct FwdRows {
   static constexpr int R = NV <= 4 ? FH_NORM_FWD_ROWS : 1;
 };
 
-template <typename T, int NV, bool ADD>
+template <typename T, int NV, bool ADD, int R>
 __global__ __launch_bounds__(256) void k_rmsnorm_fwd(
     const T* __restrict__ x, const T* __restrict__ a, const T* __restrict__ w,
     T* __restrict__ h, T* __restrict__ y, float* __restrict__ rstd,
     int64_t rows, int cols, float eps) {
-  constexpr int R = FwdRows<NV>::R;
+  using Raw = typename Elem<T>::Raw;
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6)) * R;
+  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6)) * R;
   if (row0 >= rows) return;  // uniform per wave
 
-  float v[R][NV][8];
+  Raw xr[R][NV], wr[NV];
+  [[maybe_unused]] Raw ar[R][NV];
 #pragma unroll
   for (int k = 0; k < R; ++k) {
     const int64_t base = (row0 + k) * cols;
@@ -44,19 +46,15 @@ __global__ __launch_bounds__(256) void k_rmsnorm_fwd(
     for (int i = 0; i < NV; ++i) {
       const int c = (i * kWave + lane) * 8;
       if (ok && c < cols) {
-        Elem<T>::load8(x + base + c, v[k][i]);
-        if constexpr (ADD) {
-          float b[8];
-          Elem<T>::load8(a + base + c, b);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) v[k][i][j] = Elem<T>::rnd(v[k][i][j] + b[j]);
-          Elem<T>::store8(h + base + c, v[k][i]);
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[k][i][j] = 0.f;
+        xr[k][i] = Elem<T>::ldraw(x + base + c);
+        if constexpr (ADD) ar[k][i] = Elem<T>::ldraw(a + base + c);
       }
     }
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = (i * kWave + lane) * 8;
+    if (c < cols) wr[i] = Elem<T>::ldraw(w + c);
   }
 #pragma unroll
   for (int k = 0; k < R; ++k) {
@@ -64,19 +62,34 @@ __global__ __launch_bounds__(256) void k_rmsnorm_fwd(
     const int64_t base = (row0 + k) * cols;
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < NV; ++i)
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * kWave + lane) * 8;
+      if (c < cols) {
+        float v[8];
+        Elem<T>::unpack(xr[k][i], v);
+        if constexpr (ADD) {  // h = to_dtype(x + a), kept packed for the normalisation
+          float b[8];
+          Elem<T>::unpack(ar[k][i], b);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) ss = fmaf(v[k][i][j], v[k][i][j], ss);
+          for (int j = 0; j < 8; ++j) v[j] = Elem<T>::rnd(v[j] + b[j]);
+          xr[k][i] = Elem<T>::pack(v);
+          Elem<T>::straw(h + base + c, xr[k][i]);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = fmaf(v[j], v[j], ss);
+      }
+    }
     ss = wave_sum(ss);
     const float r = rsqrtf(ss / static_cast<float>(cols) + eps);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int c = (i * kWave + lane) * 8;
       if (c < cols) {
-        float wv[8], o[8];
-        Elem<T>::load8(w + c, wv);
+        float v[8], wv[8], o[8];
+        Elem<T>::unpack(xr[k][i], v);
+        Elem<T>::unpack(wr[i], wv);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = Elem<T>::rnd(wv[j] * Elem<T>::rnd(v[k][i][j] * r));
+        for (int j = 0; j < 8; ++j) o[j] = Elem<T>::rnd(wv[j] * Elem<T>::rnd(v[j] * r));
         Elem<T>::store8(y + base + c, o);
       }
     }
@@ -84,125 +97,144 @@ __global__ __launch_bounds__(256) void k_rmsnorm_fwd(
   }
 }
 
-// Backward.  Each wave walks row pairs (row0, row0 + S), (row0 + 2S, ...) with
-// S = 4*gridDim.x, issuing all loads of a pair (x, dy and the residual
-// gradient, kept packed until used) before the first reduction, and keeps its
-// share of the weight gradient in registers; the 4 waves of a block are then
-// summed in a fixed order through LDS into one fp32 partial row per block
-// (deterministic), which k_reduce_cols folds into dw.
-template <typename T, int NV, bool RES, bool HAVE_RSTD>
+// Backward.  WPR waves share a row (WPR = 2 above 2048 columns), each holding
+// NVW chunks of 8 per lane, so every width keeps the register footprint of a
+// 2048-column row.  A block's 4 waves take 4/WPR rows per step; the step loop
+// is uniform across the block (its barriers combine the WPR per-wave partial
+// sums of a row in a fixed order, through a parity-double-buffered LDS slot).
+// Per row:
+//   r   = rstd (given) or rsqrt(mean(x^2) + eps)
+//   dn  = to_dtype(dy * w)          (the gradient at the bf16 normalised value)
+//   dot = mean(dn * x * r)
+//   dx  = r * (dn - x * r * dot) [+ dres]
+//   dw += dy * to_dtype(x * r)      (per-wave registers)
+// The weight-gradient partials of the block's waves are summed in a fixed
+// order through LDS into one fp32 row per block (deterministic), which
+// k_reduce_parts / k_reduce_stage fold into dw.
+template <typename T, int NVW, int WPR, bool RES, bool HAVE_RSTD>
 __global__ __launch_bounds__(256) void k_rmsnorm_bwd(
     const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ w,
     const float* __restrict__ rstd, const T* __restrict__ dres,
     T* __restrict__ dx, float* __restrict__ part, int64_t rows, int cols,
     float eps) {
   using Raw = typename Elem<T>::Raw;
-  constexpr int R = NV <= 4 ? 2 : 1;
-  extern __shared__ float lds_acc[];
+  constexpr int RPB = kWavesPerBlock / WPR;  // rows per block step
+  extern __shared__ float lds_acc[];          // cols floats
+  __shared__ float red[2][2][kWavesPerBlock];  // [step parity][ss | dot][wave]
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
+  const int rsub = wave / WPR, slice = wave % WPR;
+  auto col = [&](int i) { return ((slice * NVW + i) * kWave + lane) * 8; };
 
-  float acc[NV][8];
+  Raw wr[NVW];
 #pragma unroll
-  for (int i = 0; i < NV; ++i)
+  for (int i = 0; i < NVW; ++i)
+    if (col(i) < cols) wr[i] = Elem<T>::ldraw(w + col(i));
+  float acc[NVW][8];
+#pragma unroll
+  for (int i = 0; i < NVW; ++i)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = 0.f;
 
   const float inv_cols = 1.f / static_cast<float>(cols);
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kRowsPerBlock;
-  for (int64_t row0 = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + wave; row0 < rows;
-       row0 += R * stride) {
-    Raw xr[R][NV], gr[R][NV], rr[R][NV];
+  int par = 0;
+  for (int64_t step0 = static_cast<int64_t>(blockIdx.x) * RPB; step0 < rows;
+       step0 += static_cast<int64_t>(gridDim.x) * RPB, par ^= 1) {
+    const int64_t row = step0 + rsub;
+    const bool valid = row < rows;  // uniform per wave
+    const int64_t base = row * cols;
+    Raw xr[NVW], gr[NVW];
+    [[maybe_unused]] Raw rr[NVW];
 #pragma unroll
-    for (int k = 0; k < R; ++k) {
-      const int64_t row = row0 + k * stride;
-      const int64_t base = row * cols;
+    for (int i = 0; i < NVW; ++i) {
+      const int c = col(i);
+      if (valid && c < cols) {
+        xr[i] = Elem<T>::ldraw(x + base + c);
+        gr[i] = Elem<T>::ldraw(dy + base + c);
+        if constexpr (RES) rr[i] = Elem<T>::ldraw(dres + base + c);
+      }
+    }
+    float r;
+    if constexpr (HAVE_RSTD) {
+      r = valid ? rstd[row] : 0.f;
+    } else {
+      float ss = 0.f;
 #pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int c = (i * kWave + lane) * 8;
-        if (row < rows && c < cols) {
-          xr[k][i] = Elem<T>::ldraw(x + base + c);
-          gr[k][i] = Elem<T>::ldraw(dy + base + c);
-          if constexpr (RES) rr[k][i] = Elem<T>::ldraw(dres + base + c);
+      for (int i = 0; i < NVW; ++i) {
+        if (valid && col(i) < cols) {
+          float xv[8];
+          Elem<T>::unpack(xr[i], xv);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) ss = fmaf(xv[j], xv[j], ss);
+        }
+      }
+      ss = wave_sum(ss);
+      if constexpr (WPR > 1) {
+        if (lane == 0) red[par][0][wave] = ss;
+        __syncthreads();
+        ss = 0.f;
+#pragma unroll
+        for (int s = 0; s < WPR; ++s) ss += red[par][0][rsub * WPR + s];
+      }
+      r = rsqrtf(ss * inv_cols + eps);
+    }
+    float dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < NVW; ++i) {
+      if (valid && col(i) < cols) {
+        float wv[8], xv[8], gv[8];
+        Elem<T>::unpack(wr[i], wv);
+        Elem<T>::unpack(xr[i], xv);
+        Elem<T>::unpack(gr[i], gv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float n = xv[j] * r;
+          dot = fmaf(Elem<T>::rnd(gv[j] * wv[j]), n, dot);
+          acc[i][j] = fmaf(gv[j], Elem<T>::rnd(n), acc[i][j]);
         }
       }
     }
+    dot = wave_sum(dot);
+    if constexpr (WPR > 1) {
+      if (lane == 0) red[par][1][wave] = dot;
+      __syncthreads();
+      dot = 0.f;
 #pragma unroll
-    for (int k = 0; k < R; ++k) {
-      const int64_t row = row0 + k * stride;
-      if (row >= rows) break;  // uniform per wave
-      const int64_t base = row * cols;
-      float r;
-      if constexpr (HAVE_RSTD) {
-        r = rstd[row];
-      } else {
-        float ss = 0.f;
+      for (int s = 0; s < WPR; ++s) dot += red[par][1][rsub * WPR + s];
+    }
+    dot *= inv_cols;
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-          if ((i * kWave + lane) * 8 < cols) {
-            float xv[8];
-            Elem<T>::unpack(xr[k][i], xv);
+    for (int i = 0; i < NVW; ++i) {
+      const int c = col(i);
+      if (valid && c < cols) {
+        float wv[8], xv[8], gv[8], o[8];
+        Elem<T>::unpack(wr[i], wv);
+        Elem<T>::unpack(xr[i], xv);
+        Elem<T>::unpack(gr[i], gv);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) ss = fmaf(xv[j], xv[j], ss);
-          }
+        for (int j = 0; j < 8; ++j) o[j] = r * (Elem<T>::rnd(gv[j] * wv[j]) - xv[j] * r * dot);
+        if constexpr (RES) {
+          float rv[8];
+          Elem<T>::unpack(rr[i], rv);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) o[j] += rv[j];
         }
-        r = rsqrtf(wave_sum(ss) * inv_cols + eps);
-      }
-      // dn = to_dtype(dy*w) is the gradient arriving at the bf16 normalised
-      // value; dot = mean(dn * n) over the row.
-      float dot = 0.f;
-      float dn[NV][8];
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int c = (i * kWave + lane) * 8;
-        if (c < cols) {
-          float wv[8], xv[8], gv[8];
-          Elem<T>::load8(w + c, wv);
-          Elem<T>::unpack(xr[k][i], xv);
-          Elem<T>::unpack(gr[k][i], gv);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float n = xv[j] * r;
-            dn[i][j] = Elem<T>::rnd(gv[j] * wv[j]);
-            acc[i][j] = fmaf(gv[j], Elem<T>::rnd(n), acc[i][j]);
-            dot = fmaf(dn[i][j], n, dot);
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) dn[i][j] = 0.f;
-        }
-      }
-      dot = wave_sum(dot) * inv_cols;
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int c = (i * kWave + lane) * 8;
-        if (c < cols) {
-          float xv[8], o[8];
-          Elem<T>::unpack(xr[k][i], xv);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) o[j] = r * (dn[i][j] - xv[j] * r * dot);
-          if constexpr (RES) {
-            float rv[8];
-            Elem<T>::unpack(rr[k][i], rv);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) o[j] += rv[j];
-          }
-          Elem<T>::store8(dx + base + c, o);
-        }
+        Elem<T>::store8(dx + base + c, o);
       }
     }
   }
 
-  // Fixed-order combination of the 4 per-wave partials.
-  for (int wv = 0; wv < kRowsPerBlock; ++wv) {
-    if (wave == wv) {
+  // Fixed-order combination of the per-wave partials (waves with the same
+  // slice cover the same columns; row groups rsub = 0, 1, ... in order).
+  for (int s = 0; s < RPB; ++s) {
+    if (rsub == s) {
 #pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int c = (i * kWave + lane) * 8;
+      for (int i = 0; i < NVW; ++i) {
+        const int c = col(i);
         if (c < cols) {
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            if (wv == 0) lds_acc[c + j] = acc[i][j];
+            if (s == 0) lds_acc[c + j] = acc[i][j];
             else lds_acc[c + j] += acc[i][j];
           }
         }
@@ -214,72 +246,100 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd(
   for (int c = threadIdx.x; c < cols; c += blockDim.x) dst[c] = lds_acc[c];
 }
 
-// dw[c] = sum_p part[p, c]; block = 64 columns x 16 waves, fixed order.  Each
-// wave keeps 8 independent partial-row loads in flight.
-template <typename T>
-__global__ __launch_bounds__(1024) void k_reduce_cols(const float* __restrict__ part,
-                                                      int nparts, int cols,
-                                                      T* __restrict__ out) {
-  __shared__ float red[16][65];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int c = blockIdx.x * 64 + lane;
+// dw[c] = sum_p part[p, c], deterministic, in two stages.  Stage 1: block
+// (cx, g) sums partial rows p = g, g + G, g + 2G, ... (each of its 4 waves
+// takes every 4th of them, all loads in flight at once) for 64 columns and
+// combines its waves in a fixed order into stage[g][c].  Stage 2 sums the G
+// stage rows of a column in order.  The partial rows are few (<= 512) and
+// wide, so one stage would leave the reduction latency-bound on a handful of
+// CUs.
+constexpr int kReduceGroups = 16;
+
+__global__ __launch_bounds__(256) void k_reduce_parts(const float* __restrict__ part, int nparts,
+                                                      int cols, float* __restrict__ stage) {
+  __shared__ float red[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + lane, g = blockIdx.y;
   float s = 0.f;
   if (c < cols) {
-    int p = wave;
-    for (; p + 16 * 7 < nparts; p += 16 * 8) {
-      float v[8];
+    constexpr int U = 8;  // loads in flight per lane
+    int p = g + kReduceGroups * wave;
+    for (; p + kReduceGroups * 4 * (U - 1) < nparts; p += kReduceGroups * 4 * U) {
+      float v[U];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = part[static_cast<int64_t>(p + 16 * k) * cols + c];
+      for (int k = 0; k < U; ++k) v[k] = part[static_cast<int64_t>(p + kReduceGroups * 4 * k) * cols + c];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) s += v[k];
+      for (int k = 0; k < U; ++k) s += v[k];
     }
-    for (; p < nparts; p += 16) s += part[static_cast<int64_t>(p) * cols + c];
+    for (; p < nparts; p += kReduceGroups * 4) s += part[static_cast<int64_t>(p) * cols + c];
   }
   red[wave][lane] = s;
   __syncthreads();
-  if (wave == 0 && c < cols) {
-    float t = 0.f;
-    for (int k = 0; k < 16; ++k) t += red[k][lane];
-    Elem<T>::st1(out + c, t);
-  }
+  if (wave == 0 && c < cols)
+    stage[static_cast<int64_t>(g) * cols + c] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
 }
 
-// Backward grid cap: fewer blocks mean fewer fp32 dw partial rows for
-// k_reduce_cols; 512 blocks measured best at T=16384, H=2048 (4.05 TB/s for
-// both kernels together vs 3.43 at 1024 and 3.74 at 256).
+template <typename T>
+__global__ __launch_bounds__(256) void k_fill_zero(T* __restrict__ out, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) Elem<T>::st1(out + i, 0.f);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_reduce_stage(const float* __restrict__ stage, int cols,
+                                                      T* __restrict__ out) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= cols) return;
+  float t = 0.f;
+#pragma unroll
+  for (int g = 0; g < kReduceGroups; ++g) t += stage[static_cast<int64_t>(g) * cols + c];
+  Elem<T>::st1(out + c, t);
+}
+
+// Backward grid cap: fewer blocks mean fewer fp32 dw partial rows to reduce;
+// 512 measured best at T=16384, H=2048 (256 and 1024 both slower).
 #ifndef FH_NORM_BWD_BLOCKS
 #define FH_NORM_BWD_BLOCKS 512
 #endif
 constexpr int kMaxBwdBlocks = FH_NORM_BWD_BLOCKS;
 
-int bwd_blocks(int64_t rows) {
-  const int64_t need = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-  return static_cast<int>(need < kMaxBwdBlocks ? need : kMaxBwdBlocks);
-}
-
 template <typename T, int NV>
 void launch_fwd(const void* x, const void* a, const void* w, void* h, void* y, float* rstd,
                 int64_t rows, int cols, float eps, hipStream_t s) {
-  const int64_t per_block = static_cast<int64_t>(kRowsPerBlock) * FwdRows<NV>::R;
+  constexpr int R = FwdRows<NV>::R;
+  const int64_t per_block = static_cast<int64_t>(kWavesPerBlock) * R;
   const dim3 grid(static_cast<unsigned>((rows + per_block - 1) / per_block));
   if (a != nullptr) {
-    hipLaunchKernelGGL((k_rmsnorm_fwd<T, NV, true>), grid, dim3(256), 0, s,
+    hipLaunchKernelGGL((k_rmsnorm_fwd<T, NV, true, R>), grid, dim3(256), 0, s,
                        static_cast<const T*>(x), static_cast<const T*>(a),
                        static_cast<const T*>(w), static_cast<T*>(h), static_cast<T*>(y), rstd,
                        rows, cols, eps);
   } else {
-    hipLaunchKernelGGL((k_rmsnorm_fwd<T, NV, false>), grid, dim3(256), 0, s,
+    hipLaunchKernelGGL((k_rmsnorm_fwd<T, NV, false, R>), grid, dim3(256), 0, s,
                        static_cast<const T*>(x), nullptr, static_cast<const T*>(w), nullptr,
                        static_cast<T*>(y), rstd, rows, cols, eps);
   }
+}
+
+// Backward row split: WPR waves per row and NVW chunks of 8 per lane.
+template <int NV>
+struct BwdSplit {
+  static constexpr int WPR = NV > 4 ? 2 : 1;
+  static constexpr int NVW = NV / WPR;
+};
+
+int bwd_blocks(int64_t rows, int wpr) {
+  const int64_t rpb = kWavesPerBlock / wpr;
+  const int64_t need = (rows + rpb - 1) / rpb;
+  return static_cast<int>(need < kMaxBwdBlocks ? need : kMaxBwdBlocks);
 }
 
 template <typename T, int NV, bool RES, bool HR>
 void launch_bwd_k(const void* dy, const void* x, const void* w, const float* rstd,
                   const void* dres, void* dx, float* part, int64_t rows, int cols, float eps,
                   int blocks, hipStream_t s) {
-  hipLaunchKernelGGL((k_rmsnorm_bwd<T, NV, RES, HR>), dim3(blocks), dim3(256),
+  using SP = BwdSplit<NV>;
+  hipLaunchKernelGGL((k_rmsnorm_bwd<T, SP::NVW, SP::WPR, RES, HR>), dim3(blocks), dim3(256),
                      static_cast<size_t>(cols) * sizeof(float), s, static_cast<const T*>(dy),
                      static_cast<const T*>(x), static_cast<const T*>(w), rstd,
                      static_cast<const T*>(dres), static_cast<T*>(dx), part, rows, cols, eps);
@@ -289,14 +349,17 @@ template <typename T, int NV>
 void launch_bwd(const void* dy, const void* x, const void* w, const float* rstd,
                 const void* dres, void* dx, void* dw, float* part, int64_t rows, int cols,
                 float eps, hipStream_t s) {
-  const int blocks = bwd_blocks(rows);
+  const int blocks = bwd_blocks(rows, BwdSplit<NV>::WPR);
   const bool res = dres != nullptr, hr = rstd != nullptr;
   if (res && hr) launch_bwd_k<T, NV, true, true>(dy, x, w, rstd, dres, dx, part, rows, cols, eps, blocks, s);
   else if (res) launch_bwd_k<T, NV, true, false>(dy, x, w, rstd, dres, dx, part, rows, cols, eps, blocks, s);
   else if (hr) launch_bwd_k<T, NV, false, true>(dy, x, w, rstd, dres, dx, part, rows, cols, eps, blocks, s);
   else launch_bwd_k<T, NV, false, false>(dy, x, w, rstd, dres, dx, part, rows, cols, eps, blocks, s);
-  hipLaunchKernelGGL((k_reduce_cols<T>), dim3((cols + 63) / 64), dim3(1024), 0, s, part, blocks,
-                     cols, static_cast<T*>(dw));
+  float* stage = part + static_cast<int64_t>(blocks) * cols;
+  hipLaunchKernelGGL(k_reduce_parts, dim3((cols + 63) / 64, kReduceGroups), dim3(256), 0, s, part,
+                     blocks, cols, stage);
+  hipLaunchKernelGGL((k_reduce_stage<T>), dim3((cols + 255) / 256), dim3(256), 0, s, stage, cols,
+                     static_cast<T*>(dw));
 }
 
 // Chunks of 8 per lane: cols <= 512*NV.
@@ -357,7 +420,10 @@ extern "C" int fh_add_rmsnorm_fwd(fh_dtype dt, const void* x, const void* a, con
 
 extern "C" size_t fh_rmsnorm_bwd_workspace_size(int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0) return 0;
-  return static_cast<size_t>(bwd_blocks(rows)) * static_cast<size_t>(cols) * sizeof(float);
+  // one fp32 partial row per backward block (rows wider than 2048 take 2 waves
+  // each), then the reduction's stage rows
+  const int64_t nrows = bwd_blocks(rows, cols > 2048 ? 2 : 1) + kReduceGroups;
+  return static_cast<size_t>(nrows) * static_cast<size_t>(cols) * sizeof(float);
 }
 
 extern "C" int fh_rmsnorm_bwd(fh_dtype dt, const void* dy, const void* x, const void* w,
@@ -372,11 +438,11 @@ extern "C" int fh_rmsnorm_bwd(fh_dtype dt, const void* dy, const void* x, const 
     // zero partials; a kernel rather than hipMemsetAsync so the call stays
     // safe inside a captured graph).
     if (dt == FH_BF16)
-      hipLaunchKernelGGL((k_reduce_cols<uint16_t>), dim3((c + 63) / 64), dim3(1024), 0, stream,
-                         nullptr, 0, c, static_cast<uint16_t*>(dw));
+      hipLaunchKernelGGL((k_fill_zero<uint16_t>), dim3((c + 255) / 256), dim3(256), 0, stream,
+                         static_cast<uint16_t*>(dw), c);
     else
-      hipLaunchKernelGGL((k_reduce_cols<float>), dim3((c + 63) / 64), dim3(1024), 0, stream,
-                         nullptr, 0, c, static_cast<float*>(dw));
+      hipLaunchKernelGGL((k_fill_zero<float>), dim3((c + 255) / 256), dim3(256), 0, stream,
+                         static_cast<float*>(dw), c);
     return check_launch("fh_rmsnorm_bwd");
   }
   FH_REQUIRE(dy && x && dx && workspace, "rmsnorm_bwd: null pointer");
