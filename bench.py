@@ -373,7 +373,7 @@ def main() -> int:
         print(json.dumps(profile_kernel(torch, args.profile_kernel)), flush=True)
         return 0
 
-    from femtotron_amd import dispatch_counts, fused_checkpoint, reset_dispatch_counts
+    from femtotron_amd import dispatch_counts, fused_checkpoint, pack_layer_weights, reset_dispatch_counts
     from femtotron_amd.model import build_llama_model, init_llama_weights_
     from femtotron_amd.scripts.presets import get_ac_policy
     from femtotron_amd.training import apply_activation_checkpointing, remove_activation_checkpointing
@@ -387,6 +387,7 @@ def main() -> int:
     log(f"building {model_name}-shaped model ({L} layers), bf16, weights N(0, 0.02)")
     model = build_llama_model(llama_config(c, L))
     model = init_llama_weights_(model, device="cuda", dtype=torch.bfloat16, generator_device="cuda")
+    packed_groups = pack_layer_weights(model)  # q/k/v and gate/up as row views of one buffer
     policy = get_ac_policy(PRESETS[args.ac])
     apply_activation_checkpointing(model, policy, checkpoint_fn=fused_checkpoint)
     ids = torch.randint(0, c["vocab"], (B, S), generator=torch.Generator().manual_seed(2000)).cuda()
@@ -460,6 +461,7 @@ def main() -> int:
         "attention_mfma": mfma,
         "gemms": ("hipBLASLt/rocBLAS, TunableOp solutions from femtotron_amd/tuned/"
                   "tunableop_gfx950.csv" if tuned else "hipBLASLt default heuristics"),
+        "weights": f"q/k/v and gate/up packed contiguously ({packed_groups} groups)",
         "activation_bytes_per_token": round(act_fused, 1),
         "reference_gpu": ref,
         "cpu_baseline": cpu,

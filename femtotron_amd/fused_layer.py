@@ -29,6 +29,7 @@ from dataclasses import dataclass
 import torch
 
 from . import attention, ops
+from .weight_packing import packed
 
 
 @dataclass(frozen=True)
@@ -56,6 +57,13 @@ def _mm_nt(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     return torch.mm(a, b.t())
 
 
+def _cat_rows(*ws: torch.Tensor) -> torch.Tensor:
+    """[W1; W2; ...]: a view when the weights are packed contiguously
+    (femtotron_amd.weight_packing), else a concatenated copy."""
+    view = packed(*ws)
+    return view if view is not None else torch.cat(ws, 0)
+
+
 
 class _Acts:
     """Recomputed activations the backward needs."""
@@ -74,7 +82,7 @@ def layer_forward(x2: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, shp: L
     rstd1 = torch.empty(T, dtype=torch.float32, device=dev) if keep else None
     y1 = ops.rmsnorm_fwd(x2, w1, shp.eps1, rstd=rstd1)
 
-    wqkv = torch.cat((wq, wk, wv), 0)
+    wqkv = _cat_rows(wq, wk, wv)
     qkv = _mm_nt(y1, wqkv)
     ops.rope_fwd_(qkv, shp.n_heads + shp.n_kv_heads, shp.head_dim, seq, cos, sin)
     o, lse = attention.attn_fwd(qkv, batch, seq, shp, need_lse=keep)
@@ -82,7 +90,7 @@ def layer_forward(x2: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, shp: L
     rstd2 = torch.empty(T, dtype=torch.float32, device=dev) if keep else None
     h, z = ops.add_rmsnorm_fwd(x2, a, w2, shp.eps2, rstd=rstd2)
     del a
-    gu = _mm_nt(z, torch.cat((wg, wu), 0))
+    gu = _mm_nt(z, _cat_rows(wg, wu))
     F_ = shp.ffn
     p = ops.swiglu_fwd(gu[:, :F_], gu[:, F_:])
     if keep:
@@ -143,7 +151,7 @@ def layer_backward(dout2: torch.Tensor, x2: torch.Tensor, cos: torch.Tensor, sin
     del dp
     acts.gu = None
     dwgu = wg_stream.mm_tn(dgu, acts.z)
-    dz = torch.mm(dgu, torch.cat((wg, wu), 0))
+    dz = torch.mm(dgu, _cat_rows(wg, wu))
     del dgu
     acts.z = None
     # post-attention norm + residual: dh = dout + RMSNorm2^T(dz)
@@ -158,7 +166,7 @@ def layer_backward(dout2: torch.Tensor, x2: torch.Tensor, cos: torch.Tensor, sin
     acts.o = acts.lse = acts.qkv = None
     ops.rope_bwd_(dqkv, shp.n_heads + shp.n_kv_heads, shp.head_dim, seq, cos, sin)
     dwqkv = wg_stream.mm_tn(dqkv, acts.y1)
-    dy1 = torch.mm(dqkv, torch.cat((wq, wk, wv), 0))
+    dy1 = torch.mm(dqkv, _cat_rows(wq, wk, wv))
     del dqkv
     acts.y1 = None
     dx, dw1 = ops.rmsnorm_bwd(dy1, x2, w1, shp.eps1, rstd=acts.rstd1, dres=dh)

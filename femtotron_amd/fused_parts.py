@@ -22,7 +22,7 @@ from __future__ import annotations
 import torch
 
 from . import ops
-from .fused_layer import _mm_nt, _WgradStream
+from .fused_layer import _cat_rows, _mm_nt, _WgradStream
 
 
 def mlp_forward(z2: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor, wd: torch.Tensor, *,
@@ -30,7 +30,7 @@ def mlp_forward(z2: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor, wd: torch.
     """z2 [T, H] -> m [T, H]; keep=True stops after the SwiGLU product and
     returns (gu, p) for the backward."""
     F_ = wg.shape[0]
-    gu = _mm_nt(z2, torch.cat((wg, wu), 0))
+    gu = _mm_nt(z2, _cat_rows(wg, wu))
     p = ops.swiglu_fwd(gu[:, :F_], gu[:, F_:])
     if keep:
         return gu, p
@@ -49,7 +49,7 @@ def mlp_backward(dm2: torch.Tensor, z2: torch.Tensor, wg: torch.Tensor, wu: torc
     ops.swiglu_bwd(dp, gu[:, :F_], gu[:, F_:], dgu[:, :F_], dgu[:, F_:])
     del dp, gu
     dwgu = wg_stream.mm_tn(dgu, z2)
-    dz = torch.mm(dgu, torch.cat((wg, wu), 0))
+    dz = torch.mm(dgu, _cat_rows(wg, wu))
     wg_stream.join()
     return dz, dwgu[:F_], dwgu[F_:], dwd
 
