@@ -84,7 +84,7 @@ def parse_args():
     ap.add_argument("--profile-kernel", default=None,
                     help="launch only this fused kernel (swiglu_fwd, swiglu_bwd, rmsnorm_fwd, "
                          "add_rmsnorm_fwd, rmsnorm_bwd, rope_fwd, residual_add, attn_fwd, attn_bwd) at "
-                         "the step's shape, after a 1 GiB device copy that calibrates HBM byte "
+                         "--workload's step shape, after a 1 GiB device copy that calibrates HBM byte "
                          "counters, for rocprofv3 --pmc runs; prints one JSON line and exits")
     return ap.parse_args()
 
@@ -259,13 +259,13 @@ def kernel_table(torch, c: dict, iters: int, ac: str):
     return rows, mfma
 
 
-def profile_kernel(torch, name: str, launches: int = 10) -> dict:
+def profile_kernel(torch, name: str, c: dict, launches: int = 10) -> dict:
     """A 1 GiB device-to-device copy (known traffic: 1 GiB read + 1 GiB written),
-    then `launches` launches of one fused kernel at the TinyLlama step's shape,
-    each on a fresh buffer set.  Under rocprofv3 --pmc FETCH_SIZE (or WRITE_SIZE)
-    the copy's reading calibrates the counter's units."""
+    then `launches` launches of one fused kernel at the step's shape of workload
+    `c`, each on a fresh buffer set (attention: on one buffer set).  Under
+    rocprofv3 --pmc FETCH_SIZE (or WRITE_SIZE) the copy's reading calibrates the
+    counter's units."""
     from femtotron_amd import ops
-    c = TINYLLAMA
     T, H, F = c["batch"] * c["seq"], c["hidden"], c["ffn"]
     nh, nkv, hd = c["heads"], c["kv"], c["hidden"] // c["heads"]
     Hq, Hkv = nh * hd, nkv * hd
@@ -370,7 +370,8 @@ def main() -> int:
     log(f"library GEMMs: {'shipped TunableOp solutions' if tuned else 'default heuristics'}")
 
     if args.profile_kernel:
-        print(json.dumps(profile_kernel(torch, args.profile_kernel)), flush=True)
+        print(json.dumps(profile_kernel(torch, args.profile_kernel, WORKLOADS[args.workload][0])),
+              flush=True)
         return 0
 
     from femtotron_amd import dispatch_counts, fused_checkpoint, pack_layer_weights, reset_dispatch_counts
