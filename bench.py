@@ -75,6 +75,9 @@ def parse_args():
                     help="timed steps of the reference path on the GPU (0 to skip)")
     ap.add_argument("--cpu-sample-tokens", type=int, default=512,
                     help="tokens (one sequence) of the CPU baseline sample (0 to skip)")
+    ap.add_argument("--stock-loss-head", action="store_true",
+                    help="fused path with the reference's loss head (materialised fp32 logits) "
+                         "instead of the fused lm_head + chunked cross-entropy")
     ap.add_argument("--no-tuned-gemms", action="store_true",
                     help="use the library's default GEMM heuristics instead of the shipped "
                          "TunableOp solutions (femtotron_amd/tuned/tunableop_gfx950.csv)")
@@ -100,13 +103,13 @@ def llama_config(c: dict, layers: int):
     return cfg
 
 
-def time_steps(torch, model, ids, steps: int, warmup: int) -> float:
+def time_steps(torch, model, ids, steps: int, warmup: int, materialize_logits: bool = True) -> float:
     params = [p for p in model.parameters() if p.requires_grad]
 
     def step():
         for p in params:
             p.grad = None
-        model(ids, labels=ids)["loss"].backward()
+        model(ids, labels=ids, materialize_logits=materialize_logits)["loss"].backward()
 
     for _ in range(warmup):
         step()
@@ -118,15 +121,15 @@ def time_steps(torch, model, ids, steps: int, warmup: int) -> float:
     return (time.perf_counter() - t0) / steps
 
 
-def activation_bytes_per_token(torch, model, ids) -> float:
+def activation_bytes_per_token(torch, model, ids, materialize_logits: bool = True) -> float:
     """(max_memory_allocated during one fwd+bwd - memory_allocated before the
     forward) / tokens, with the gradients of a previous step already allocated
     (femtotron/test/integration/test_zero_ac.py:125-139 measures the same way)."""
-    model(ids, labels=ids)["loss"].backward()  # grads exist afterwards
+    model(ids, labels=ids, materialize_logits=materialize_logits)["loss"].backward()  # grads exist
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
     base = torch.cuda.memory_allocated()
-    model(ids, labels=ids)["loss"].backward()
+    model(ids, labels=ids, materialize_logits=materialize_logits)["loss"].backward()
     torch.cuda.synchronize()
     return (torch.cuda.max_memory_allocated() - base) / ids.numel()
 
@@ -395,7 +398,8 @@ def main() -> int:
 
     reset_dispatch_counts()
     log(f"fused path ({args.ac} AC): {args.warmup} warm-up + {args.steps} timed steps")
-    sec = time_steps(torch, model, ids, args.steps, args.warmup)
+    fused_head = not args.stock_loss_head
+    sec = time_steps(torch, model, ids, args.steps, args.warmup, materialize_logits=not fused_head)
     counts = dispatch_counts()
     calls_per_step = L if args.ac == "full" else 3 * L + 1
     assert counts["fallback"] == 0 and counts["fused"] == calls_per_step * (args.steps + args.warmup), counts
@@ -431,7 +435,7 @@ def main() -> int:
     # Activation memory, measured back to back for both paths in the same
     # allocator state (each after one step of its own to allocate gradients).
     use(True)
-    act_fused = activation_bytes_per_token(torch, model, ids)
+    act_fused = activation_bytes_per_token(torch, model, ids, materialize_logits=not fused_head)
     if ref is not None:
         use(False)
         ref["activation_bytes_per_token"] = round(activation_bytes_per_token(torch, model, ids), 1)
@@ -463,6 +467,8 @@ def main() -> int:
         "gemms": ("hipBLASLt/rocBLAS, TunableOp solutions from femtotron_amd/tuned/"
                   "tunableop_gfx950.csv" if tuned else "hipBLASLt default heuristics"),
         "weights": f"q/k/v and gate/up packed contiguously ({packed_groups} groups)",
+        "loss_head": ("fused lm_head + chunked cross-entropy (materialize_logits=False)" if fused_head
+                      else "reference: materialised logits, fp32 cross-entropy"),
         "activation_bytes_per_token": round(act_fused, 1),
         "reference_gpu": ref,
         "cpu_baseline": cpu,

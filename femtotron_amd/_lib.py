@@ -42,6 +42,7 @@ SIGNATURES: dict[str, tuple] = {
     "fh_attn_bwd": (c_int, [c_int, _V, _I64, _V, _I64, _V, _I64, _V, _I64, _V, _I64,
                             POINTER(c_float), _V, _I64, _V, _I64, _V, _I64, _V,
                             _I64, _I64, _I64, _I64, _I64, _F, _V]),
+    "fh_ce_fwd_bwd": (c_int, [c_int, _V, _I64, _V, _I64, _I64, _I64, _V, POINTER(c_float), _V]),
 }
 
 _lock = threading.Lock()

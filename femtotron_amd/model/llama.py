@@ -3,8 +3,9 @@
 ``LlamaForTraining`` mirrors femtotron/model/llama.py:20-123: backbone
 ``self.model = LlamaPartialModel``, ``self.lm_head`` (bias-free Linear, tied to
 the embedding when ``tie_word_embeddings``), ``use_cache = False``, and
-``forward(input_ids, labels=None) -> {"logits", "loss"}`` with the shifted
-next-token cross-entropy computed on fp32 logits, ignore_index -100 (:72-111).
+``forward(input_ids, labels=None, materialize_logits=True) -> {"logits", "loss"}``
+with the shifted next-token cross-entropy computed on fp32 logits, ignore_index
+-100 (:72-111); ``materialize_logits=False`` selects the fused loss head.
 
 ``build_llama_model`` mirrors llama.py:161-194 (construction on the meta
 device).  At TP = 1 the reference's ``parallelize_model`` only swaps the
@@ -26,6 +27,7 @@ import torch.nn.functional as F
 from torch import nn
 from transformers import LlamaConfig
 
+from .. import fused_loss
 from .llama_partial_model import LlamaPartialModel
 
 
@@ -43,8 +45,18 @@ class LlamaForTraining(nn.Module):
     def tie_weights(self):
         self.lm_head.weight = self.model.embed_tokens.weight
 
-    def forward(self, input_ids: torch.Tensor, labels: torch.Tensor | None = None) -> dict:
+    def forward(self, input_ids: torch.Tensor, labels: torch.Tensor | None = None,
+                materialize_logits: bool = True) -> dict:
+        """materialize_logits=False (the flag of femtotron/model/base.py:15) asks
+        for the loss only: with labels, on a HIP device, it is computed by the
+        fused lm_head + chunked cross-entropy (femtotron_amd/fused_loss.py) and
+        "logits" is None; otherwise the logits are materialised as the
+        reference does."""
         hidden = self.model(input_ids)
+        if (labels is not None and not materialize_logits and isinstance(self.lm_head, nn.Linear)
+                and self.lm_head.bias is None and fused_loss.supported(hidden, self.lm_head.weight)):
+            return {"logits": None,
+                    "loss": fused_loss.fused_causal_lm_loss(hidden, self.lm_head.weight, labels)}
         logits = self.lm_head(hidden)
         out: dict = {"logits": logits}
         if labels is not None:

@@ -245,3 +245,24 @@ def attn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
               _rowmajor(dout, "dout"), _fptr(lse), _ptr(dq), _rowmajor(dq, "dq"), _ptr(dk),
               _rowmajor(dk, "dk"), _ptr(dv), _rowmajor(dv, "dv"), _ptr(ws), batch, seq_len,
               n_heads, n_kv_heads, head_dim, float(scale), _stream(q))
+
+
+# ------------------------------------------------------------- loss head
+def ce_fwd_bwd_(logits: torch.Tensor, labels: torch.Tensor, inv_count: torch.Tensor,
+                ignore_index: int = -100) -> torch.Tensor:
+    """Cross-entropy of the rows of `logits` [rows, V] against `labels` (int64
+    [rows]); overwrites `logits` with the gradient (softmax - onehot) * inv_count
+    (0 for ignored rows) and returns the fp32 per-row losses.  `inv_count` is a
+    device fp32 scalar, 1 / (number of non-ignored labels of the whole batch)."""
+    _require_gpu(logits, labels, inv_count)
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("ce_fwd_bwd_: logits must be a row-major 2-D tensor")
+    if labels.dtype != torch.int64 or not labels.is_contiguous() or labels.numel() != logits.size(0):
+        raise ValueError("ce_fwd_bwd_: labels must be contiguous int64 with one entry per row")
+    if inv_count.dtype != torch.float32 or inv_count.numel() != 1:
+        raise ValueError("ce_fwd_bwd_: inv_count must be a one-element fp32 tensor")
+    loss_rows = torch.empty(logits.size(0), dtype=torch.float32, device=logits.device)
+    _lib.call("fh_ce_fwd_bwd", _dtype_code(logits), _ptr(logits), logits.stride(0), _ptr(labels),
+              logits.size(0), logits.size(1), int(ignore_index), _ptr(inv_count), _fptr(loss_rows),
+              _stream(logits))
+    return loss_rows

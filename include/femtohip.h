@@ -171,6 +171,27 @@ int fh_attn_bwd(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t 
                 void* workspace, int64_t batch, int64_t seq_len, int64_t n_heads,
                 int64_t n_kv_heads, int64_t head_dim, float scale, hipStream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Causal-LM cross-entropy, forward and gradient in one pass, in place.
+ * Replaces, for one chunk of rows of the logits, the loss head of
+ * femtotron/model/llama.py:104-111 and femtotron/model/base.py:24-31:
+ *   F.cross_entropy(logits.float().view(-1, V), labels.view(-1), ignore_index=-100)
+ * (mean over the rows whose label is not ignore_index) and its autograd
+ * gradient (softmax(x) - onehot(label)) / n_valid, rounded to the logits dtype
+ * as the backward of .float() does.  The next-token shift is the caller's
+ * (labels[b, s] = input label at s+1, ignore_index at each sequence's end).
+ *
+ * logits: [rows, vocab] row stride ld (FH_BF16 or FH_F32), overwritten with the
+ *         gradient; labels: int64 [rows] device; inv_count: device fp32 scalar
+ *         1/n_valid; loss_rows: fp32 [rows] = logsumexp(x_r) - x_r[label_r]
+ *         (0 for ignored rows; NaN, with a NaN gradient row, for a label
+ *         outside [0, vocab)).  The loss is sum(loss_rows) * inv_count.
+ * fp32 log-sum-exp; deterministic (fixed-order reductions).
+ */
+int fh_ce_fwd_bwd(fh_dtype dt, void* logits, int64_t ld, const int64_t* labels, int64_t rows,
+                  int64_t vocab, int64_t ignore_index, const float* inv_count, float* loss_rows,
+                  hipStream_t stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif
