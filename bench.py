@@ -84,9 +84,12 @@ def parse_args():
     ap.add_argument("--tune-gemms", default=None, metavar="CSV",
                     help="run TunableOp's search for every projection GEMM of --workload, write "
                          "the results to CSV and exit")
+    ap.add_argument("--no-optimizer", action="store_true",
+                    help="skip the fused-AdamW timing (reported beside the fwd+bwd metric)")
     ap.add_argument("--profile-kernel", default=None,
                     help="launch only this fused kernel (swiglu_fwd, swiglu_bwd, rmsnorm_fwd, "
-                         "add_rmsnorm_fwd, rmsnorm_bwd, rope_fwd, residual_add, attn_fwd, attn_bwd) at "
+                         "add_rmsnorm_fwd, rmsnorm_bwd, rope_fwd, residual_add, attn_fwd, attn_bwd; "
+                         "adamw: one optimizer step over the workload's parameter shapes) at "
                          "--workload's step shape, after a 1 GiB device copy that calibrates HBM byte "
                          "counters, for rocprofv3 --pmc runs; prints one JSON line and exits")
     return ap.parse_args()
@@ -320,6 +323,19 @@ def profile_kernel(torch, name: str, c: dict, launches: int = 10) -> dict:
             fn = lambda i: ops.attn_bwd(q, k, v, o, do, lse, dqkv[:, :Hq], dqkv[:, Hq:Hq + Hkv],
                                         dqkv[:, Hq + Hkv:], c["batch"], c["seq"], nh, nkv, hd, hd ** -0.5)
         nbytes = None
+    elif name == "adamw":
+        from femtotron_amd.optim import FusedAdamW
+        V, L = c["vocab"], c["layers"]
+        shapes = [(V, H)] + [(Hq, H), (Hkv, H), (Hkv, H), (H, Hq), (F, H), (F, H), (H, F), (H,), (H,)] * L
+        shapes += [(H,), (V, H)]
+        params = [rnd(*s) for s in shapes]
+        for p in params:
+            p.grad = rnd(*p.shape)
+        opt = FusedAdamW([{"params": [p for p in params if p.dim() > 1], "weight_decay": 0.01},
+                          {"params": [p for p in params if p.dim() == 1], "weight_decay": 0.0}],
+                         lr=3e-4, max_grad_norm=1.0)
+        fn = lambda i: opt.step()
+        nbytes = 30 * sum(p.numel() for p in params)  # per step: k_grad_sq 2 B, k_adamw 28 B per param
     else:
         raise SystemExit(f"unknown kernel {name!r}")
     torch.cuda.synchronize()
@@ -328,6 +344,59 @@ def profile_kernel(torch, name: str, c: dict, launches: int = 10) -> dict:
     torch.cuda.synchronize()
     return {"profile_kernel": name, "launches": n, "algorithmic_bytes_per_launch": nbytes,
             "calibration_copy_bytes": 1 << 30, "shape": {"tokens": T, "hidden": H, "ffn": F}}
+
+
+def optimizer_timing(torch, model, iters: int) -> dict:
+    """The mixed-precision AdamW step over the model's parameters with random
+    bf16 gradients: the fused path (FusedAdamW, one fh_adamw_step call) against
+    the reference's sequence on the same GPU (master.grad = grad.float();
+    ClipGradNorm; torch.optim.AdamW(foreach) on the fp32 masters;
+    param.copy_(master)).  Algorithmic bytes per bf16 parameter: 2 (gradient,
+    norm pass) + 2 + 3 x 4 read (gradient, master, moments) + 3 x 4 + 2 written
+    = 30."""
+    from femtotron_amd.optim import FusedAdamW, get_param_groups
+    params = list(model.parameters())
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    for p in params:
+        p.grad = torch.randn(p.shape, device=p.device, dtype=p.dtype, generator=gen)
+    n = sum(p.numel() for p in params)
+    kw = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-8)
+    opt = FusedAdamW(get_param_groups(model, 0.01), max_grad_norm=1.0, **kw)
+    ms = event_ms(torch, lambda i=0: opt.step(), iters)
+    del opt
+    torch.cuda.empty_cache()
+    masters = {id(p): p.detach().float().clone().requires_grad_(True) for p in params}
+    groups = [{"params": [masters[id(p)] for p in g["params"]], "weight_decay": g["weight_decay"]}
+              for g in get_param_groups(model, 0.01)]
+    ref = torch.optim.AdamW(groups, foreach=True, **kw)
+
+    def ref_step(i=0):
+        for p in params:
+            masters[id(p)].grad = p.grad.float()
+        grads = [m.grad for m in masters.values()]
+        total = torch.zeros((), device="cuda")
+        for g in grads:
+            total += g.float().pow(2).sum()
+        coef = (1.0 / (total.sqrt() + 1e-6)).clamp(max=1.0)
+        for g in grads:
+            g.mul_(coef)
+        ref.step()
+        with torch.no_grad():
+            for p in params:
+                p.copy_(masters[id(p)])
+
+    ms_ref = event_ms(torch, ref_step, max(3, iters // 4))
+    del ref, masters, groups
+    for p in params:
+        p.grad = None
+    torch.cuda.empty_cache()
+    gbs = 30 * n / (ms * 1e-3) / 1e9
+    return {"kernels": "k_grad_sq + k_clip_coef + k_adamw (one fh_adamw_step call)", "params": n,
+            "bytes_per_step": 30 * n, "ms_per_step": round(ms, 4), "achieved_gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "reference_ms_per_step": round(ms_ref, 3),
+            "speedup_vs_reference": round(ms_ref / ms, 2),
+            "reference": "master.grad = grad.float(); ClipGradNorm(1.0); torch.optim.AdamW(foreach) "
+                         "on fp32 masters; param.copy_(master)"}
 
 
 def cpu_baseline(torch, n_tokens: int) -> dict:
@@ -439,6 +508,12 @@ def main() -> int:
     if ref is not None:
         use(False)
         ref["activation_bytes_per_token"] = round(activation_bytes_per_token(torch, model, ids), 1)
+    optimizer = None
+    if not args.no_optimizer:
+        log("mixed-precision AdamW step: fused vs the reference's sequence")
+        optimizer = optimizer_timing(torch, model, args.kernel_iters)
+        log(f"optimizer: fused {optimizer['ms_per_step']:.2f} ms, reference "
+            f"{optimizer['reference_ms_per_step']:.2f} ms")
     del model
     torch.cuda.empty_cache()
 
@@ -471,6 +546,7 @@ def main() -> int:
                       else "reference: materialised logits, fp32 cross-entropy"),
         "activation_bytes_per_token": round(act_fused, 1),
         "reference_gpu": ref,
+        "optimizer_step": optimizer,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

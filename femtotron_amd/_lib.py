@@ -23,6 +23,12 @@ _V = c_void_p
 _I64 = c_int64
 _F = c_float
 
+
+class FhAdamHyper(ctypes.Structure):
+    """FhAdamHyper of include/femtohip.h (passed by value to fh_adamw_step)."""
+    _fields_ = [("one_minus_beta1", c_float), ("beta2", c_float), ("one_minus_beta2", c_float),
+                ("eps", c_float), ("step_size", c_float), ("bias_correction2_sqrt", c_float)]
+
 # name -> (restype, argtypes); mirrors include/femtohip.h exactly.
 SIGNATURES: dict[str, tuple] = {
     "fh_abi_version": (c_int, []),
@@ -43,6 +49,8 @@ SIGNATURES: dict[str, tuple] = {
                             POINTER(c_float), _V, _I64, _V, _I64, _V, _I64, _V,
                             _I64, _I64, _I64, _I64, _I64, _F, _V]),
     "fh_ce_fwd_bwd": (c_int, [c_int, _V, _I64, _V, _I64, _I64, _I64, _V, POINTER(c_float), _V]),
+    "fh_adamw_workspace_size": (c_size_t, [_I64]),
+    "fh_adamw_step": (c_int, [c_int, _V, _V, c_int, _I64, FhAdamHyper, _F, _V, _V]),
 }
 
 _lock = threading.Lock()

@@ -192,6 +192,47 @@ int fh_ce_fwd_bwd(fh_dtype dt, void* logits, int64_t ld, const int64_t* labels, 
                   int64_t vocab, int64_t ignore_index, const float* inv_count, float* loss_rows,
                   hipStream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Mixed-precision AdamW step with global gradient-norm clipping.
+ * Replaces femtotron/training/mixed_precision_manager.py:318-331 (step():
+ * master.grad = param.grad.float(); ClipGradNorm of grad_transform.py:13-63;
+ * torch.optim.AdamW on the fp32 masters, femtotron/scripts/train.py:264-276; param.copy_(master),
+ * param_group.py:82-87) for every tensor of one device in two passes over the
+ * gradients.  table: device array of n_tensors FhAdamTensor; chunk_start:
+ * device int64 [n_tensors + 1], chunk_start[i] = sum over j < i of
+ * ceil(numel_j / 2048), chunk_start[n] = total_chunks.  All pointers 16-byte
+ * aligned; param/grad in dt (FH_BF16 or FH_F32), the rest fp32.
+ * hyper: per-step scalars (step_size = lr / (1 - beta1^step),
+ * bias_correction2_sqrt = sqrt(1 - beta2^step)); per-tensor decay = 1 - lr * wd.
+ * max_grad_norm <= 0 disables clipping.  workspace: fh_adamw_workspace_size
+ * bytes; after the call it holds, at float index total_chunks, the clipping
+ * coefficient and then the gradient norm (before clipping).
+ */
+typedef struct {
+  void* param;            /* model-dtype parameter (receives the cast master) */
+  const void* grad;       /* model-dtype gradient */
+  float* master;          /* fp32 master weights */
+  float* exp_avg;         /* fp32 first moment */
+  float* exp_avg_sq;      /* fp32 second moment */
+  int64_t numel;
+  float decay;            /* 1 - lr * weight_decay of this tensor's group */
+  float reserved;
+} FhAdamTensor;
+
+typedef struct {
+  float one_minus_beta1;
+  float beta2;
+  float one_minus_beta2;
+  float eps;
+  float step_size;
+  float bias_correction2_sqrt;
+} FhAdamHyper;
+
+size_t fh_adamw_workspace_size(int64_t total_chunks);
+int fh_adamw_step(fh_dtype dt, const FhAdamTensor* table, const int64_t* chunk_start,
+                  int n_tensors, int64_t total_chunks, FhAdamHyper hyper, float max_grad_norm,
+                  void* workspace, hipStream_t stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif
