@@ -84,11 +84,14 @@ def parse_args():
     ap.add_argument("--tune-gemms", default=None, metavar="CSV",
                     help="run TunableOp's search for every projection GEMM of --workload, write "
                          "the results to CSV and exit")
+    ap.add_argument("--stock-boundary", action="store_true",
+                    help="keep the reference's nn.Embedding and final LlamaRMSNorm (no fuse_boundary_ops)")
     ap.add_argument("--no-optimizer", action="store_true",
                     help="skip the fused-AdamW timing (reported beside the fwd+bwd metric)")
     ap.add_argument("--profile-kernel", default=None,
                     help="launch only this fused kernel (swiglu_fwd, swiglu_bwd, rmsnorm_fwd, "
                          "add_rmsnorm_fwd, rmsnorm_bwd, rope_fwd, residual_add, attn_fwd, attn_bwd; "
+                         "embedding_fwd, embedding_bwd; "
                          "adamw: one optimizer step over the workload's parameter shapes) at "
                          "--workload's step shape, after a 1 GiB device copy that calibrates HBM byte "
                          "counters, for rocprofv3 --pmc runs; prints one JSON line and exits")
@@ -161,7 +164,7 @@ def event_ms(torch, fn, iters: int) -> float:
     return start.elapsed_time(end) / iters
 
 
-def kernel_table(torch, c: dict, iters: int, ac: str):
+def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True):
     """Fused kernels at the step's shapes.  Each launch reads a different buffer
     set (working set > 1 GiB) so the 256 MiB MALL cannot serve repeats: the bytes
     come from HBM as in the step.  launches_per_step counts the launches of one
@@ -196,7 +199,8 @@ def kernel_table(torch, c: dict, iters: int, ac: str):
     ys = sets(8, lambda: torch.empty(T, H, device=dev, dtype=bf))
     rs = torch.empty(T, device=dev, dtype=torch.float32)
     ms = event_ms(torch, lambda i=0: ops.rmsnorm_fwd(xs[i % 8], w, 1e-5, out=ys[i % 8], rstd=rs), iters)
-    add_row("rmsnorm_fwd", "k_rmsnorm_fwd", 2 * L + 1 if sel else 2 * L, 4 * T * H, ms)
+    # + the final norm: checkpointed under the selective policy, FusedRMSNorm otherwise
+    add_row("rmsnorm_fwd", "k_rmsnorm_fwd", 2 * L + (1 if sel or boundary else 0), 4 * T * H, ms)
     # add_rmsnorm_fwd: x, a -> h, y   (8TH)
     as_ = sets(8, lambda: rnd(T, H))
     ms = event_ms(torch, lambda i=0: ops.add_rmsnorm_fwd(xs[i % 8], as_[i % 8], w, 1e-5, rstd=rs), iters)
@@ -211,6 +215,10 @@ def kernel_table(torch, c: dict, iters: int, ac: str):
         ms = event_ms(torch, lambda i=0: ops.rmsnorm_bwd(ys[i % 8], xs[i % 8], w, 1e-5, rstd=rs,
                                                            dres=as_[i % 8]), iters)
         add_row("rmsnorm_bwd", "k_rmsnorm_bwd", 2 * L, 8 * T * H, ms)
+        if boundary:
+            # the final norm's backward: no residual, statistic recomputed: dy, x -> dx   (6TH)
+            ms = event_ms(torch, lambda i=0: ops.rmsnorm_bwd(ys[i % 8], xs[i % 8], w, 1e-5), iters)
+            add_row("final_rmsnorm_bwd", "k_rmsnorm_bwd", 1, 6 * T * H, ms)
     del as_
     if not sel:
         # residual add: h + m -> out   (6TH)
@@ -236,6 +244,20 @@ def kernel_table(torch, c: dict, iters: int, ac: str):
                                                       dgus[i % 3][:, :F], dgus[i % 3][:, F:]), iters)
     add_row("swiglu_bwd", "k_swiglu_bwd", L, 10 * T * F, ms)
     del gus, ps, dgus
+    if boundary:
+        # embedding: gather (T rows read and written + int64 ids); backward:
+        # dy read, every vocabulary row written, ids read (the radix sort's
+        # 4-byte keys/values are not counted)
+        V = c["vocab"]
+        emb = rnd(V, H)
+        ids = torch.randint(0, V, (T,), device=dev, generator=g)
+        ms = event_ms(torch, lambda i=0: ops.embedding_fwd(ids, emb), iters)
+        add_row("embedding_fwd", "k_embed_fwd", 1, 4 * T * H + 8 * T, ms)
+        dys = sets(3, lambda: rnd(T, H))
+        ms = event_ms(torch, lambda i=0: ops.embedding_bwd(dys[i % 3], ids, V), iters)
+        add_row("embedding_bwd", "k_embed_keys + 3 x k_radix_* + k_embed_bounds + k_embed_rows", 1,
+                2 * T * H + 2 * V * H + 8 * T, ms)
+        del emb, dys
     if sel:  # attention is outside the checkpointed modules under this policy
         return rows, []
 
@@ -323,6 +345,17 @@ def profile_kernel(torch, name: str, c: dict, launches: int = 10) -> dict:
             fn = lambda i: ops.attn_bwd(q, k, v, o, do, lse, dqkv[:, :Hq], dqkv[:, Hq:Hq + Hkv],
                                         dqkv[:, Hq + Hkv:], c["batch"], c["seq"], nh, nkv, hd, hd ** -0.5)
         nbytes = None
+    elif name in ("embedding_fwd", "embedding_bwd"):
+        V = c["vocab"]
+        emb = rnd(V, H)
+        ids = torch.randint(0, V, (T,), device=dev, generator=g)
+        if name == "embedding_fwd":
+            fn = lambda i: ops.embedding_fwd(ids, emb)
+            nbytes = 4 * T * H + 8 * T
+        else:
+            dys = [rnd(T, H) for _ in range(n)]
+            fn = lambda i: ops.embedding_bwd(dys[i], ids, V)
+            nbytes = 2 * T * H + 2 * V * H + 8 * T
     elif name == "adamw":
         from femtotron_amd.optim import FusedAdamW
         V, L = c["vocab"], c["layers"]
@@ -446,7 +479,9 @@ def main() -> int:
               flush=True)
         return 0
 
-    from femtotron_amd import dispatch_counts, fused_checkpoint, pack_layer_weights, reset_dispatch_counts
+    from femtotron_amd import (dispatch_counts, fuse_boundary_ops, fused_checkpoint, pack_layer_weights,
+                               reset_dispatch_counts)
+    from femtotron_amd.boundary_ops import unfuse_boundary_ops
     from femtotron_amd.model import build_llama_model, init_llama_weights_
     from femtotron_amd.scripts.presets import get_ac_policy
     from femtotron_amd.training import apply_activation_checkpointing, remove_activation_checkpointing
@@ -461,6 +496,7 @@ def main() -> int:
     model = build_llama_model(llama_config(c, L))
     model = init_llama_weights_(model, device="cuda", dtype=torch.bfloat16, generator_device="cuda")
     packed_groups = pack_layer_weights(model)  # q/k/v and gate/up as row views of one buffer
+    boundary = fuse_boundary_ops(model) if not args.stock_boundary else 0  # embedding, final norm
     policy = get_ac_policy(PRESETS[args.ac])
     apply_activation_checkpointing(model, policy, checkpoint_fn=fused_checkpoint)
     ids = torch.randint(0, c["vocab"], (B, S), generator=torch.Generator().manual_seed(2000)).cuda()
@@ -470,13 +506,14 @@ def main() -> int:
     fused_head = not args.stock_loss_head
     sec = time_steps(torch, model, ids, args.steps, args.warmup, materialize_logits=not fused_head)
     counts = dispatch_counts()
-    calls_per_step = L if args.ac == "full" else 3 * L + 1
+    # selective: 2 norms + 1 MLP per layer, + the final norm unless fuse_boundary_ops took it
+    calls_per_step = L if args.ac == "full" else 3 * L + (0 if boundary else 1)
     assert counts["fallback"] == 0 and counts["fused"] == calls_per_step * (args.steps + args.warmup), counts
     tok_s = T / sec
     log(f"fused: {sec * 1e3:.2f} ms/step, {tok_s:.0f} tokens/s")
 
     log("per-kernel HIP-event timings at the step's shapes")
-    rows, mfma = kernel_table(torch, c, args.kernel_iters, args.ac)
+    rows, mfma = kernel_table(torch, c, args.kernel_iters, args.ac, boundary=bool(boundary))
     for r in rows:
         r["ms_per_step"] = round(r["ms_per_launch"] * r["launches_per_step"], 4)
     dom = max(rows, key=lambda r: r["ms_per_step"])
@@ -487,6 +524,8 @@ def main() -> int:
 
     def use(fused: bool):
         remove_activation_checkpointing(model)
+        if boundary:
+            (fuse_boundary_ops if fused else unfuse_boundary_ops)(model)
         if fused:
             apply_activation_checkpointing(model, policy, checkpoint_fn=fused_checkpoint)
         else:
@@ -542,6 +581,8 @@ def main() -> int:
         "gemms": ("hipBLASLt/rocBLAS, TunableOp solutions from femtotron_amd/tuned/"
                   "tunableop_gfx950.csv" if tuned else "hipBLASLt default heuristics"),
         "weights": f"q/k/v and gate/up packed contiguously ({packed_groups} groups)",
+        "boundary_ops": ("fused embedding (deterministic scatter-add backward) and final RMSNorm"
+                         if boundary else "reference nn.Embedding and LlamaRMSNorm"),
         "loss_head": ("fused lm_head + chunked cross-entropy (materialize_logits=False)" if fused_head
                       else "reference: materialised logits, fp32 cross-entropy"),
         "activation_bytes_per_token": round(act_fused, 1),

@@ -266,3 +266,47 @@ def ce_fwd_bwd_(logits: torch.Tensor, labels: torch.Tensor, inv_count: torch.Ten
               logits.size(0), logits.size(1), int(ignore_index), _ptr(inv_count), _fptr(loss_rows),
               _stream(logits))
     return loss_rows
+
+
+# ------------------------------------------------------------- embedding
+def _embedding_args(weight: torch.Tensor, ids: torch.Tensor) -> tuple[int, int]:
+    if weight.dim() != 2 or not weight.is_contiguous():
+        raise ValueError("embedding: weight must be a contiguous [vocab, hidden] tensor")
+    if ids.dtype != torch.int64 or not ids.is_contiguous():
+        raise ValueError("embedding: ids must be contiguous int64")
+    vocab, hidden = weight.shape
+    if hidden % 8 != 0:
+        raise ValueError(f"embedding: hidden must be a multiple of 8, got {hidden}")
+    return vocab, hidden
+
+
+def embedding_fwd(ids: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """weight[ids] with zero rows for ids outside [0, vocab): [*ids.shape, hidden]."""
+    _require_gpu(ids, weight)
+    vocab, hidden = _embedding_args(weight, ids)
+    out = torch.empty(*ids.shape, hidden, dtype=weight.dtype, device=weight.device)
+    _lib.call("fh_embedding_fwd", _dtype_code(weight), _ptr(weight), _ptr(ids), _ptr(out),
+              ids.numel(), vocab, hidden, _stream(weight))
+    return out
+
+
+def embedding_bwd(dy: torch.Tensor, ids: torch.Tensor, vocab: int,
+                  padding_idx: int | None = None) -> torch.Tensor:
+    """Weight gradient of the lookup: [vocab, hidden], row v = sum of the dy rows
+    of the tokens with id v (fp32, token order), zero for unused ids; tokens with
+    an id outside [0, vocab) or equal to padding_idx contribute nothing."""
+    _require_gpu(dy, ids)
+    hidden = dy.size(-1)
+    if not dy.is_contiguous() or dy.numel() != ids.numel() * hidden:
+        raise ValueError("embedding_bwd: dy must be contiguous [*ids.shape, hidden]")
+    if ids.dtype != torch.int64 or not ids.is_contiguous():
+        raise ValueError("embedding_bwd: ids must be contiguous int64")
+    if hidden % 8 != 0:
+        raise ValueError(f"embedding_bwd: hidden must be a multiple of 8, got {hidden}")
+    dw = torch.empty(vocab, hidden, dtype=dy.dtype, device=dy.device)
+    n = ids.numel()
+    ws = torch.empty(_lib.lib().fh_embedding_bwd_workspace_size(n, vocab), dtype=torch.uint8,
+                     device=dy.device)
+    _lib.call("fh_embedding_bwd", _dtype_code(dy), _ptr(dy), _ptr(ids), _ptr(dw), n, vocab, hidden,
+              -1 if padding_idx is None else int(padding_idx), _ptr(ws), _stream(dy))
+    return dw

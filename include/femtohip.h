@@ -233,6 +233,34 @@ int fh_adamw_step(fh_dtype dt, const FhAdamTensor* table, const int64_t* chunk_s
                   int n_tensors, int64_t total_chunks, FhAdamHyper hyper, float max_grad_norm,
                   void* workspace, hipStream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Token embedding of the first pipeline stage
+ * (femtotron/model/llama_partial_model.py:181-184): nn.Embedding, replaced at
+ * TP = 1 by VocabParallelEmbedding (femtotron/parallel/tensor_parallel/
+ * embedding.py:57-79: ids outside [0, vocab) give zero rows).
+ *
+ * fh_embedding_fwd: out[t, :] = weight[ids[t], :] for 0 <= ids[t] < vocab,
+ * zeros otherwise.  weight [vocab, hidden], out [n_tokens, hidden] (contiguous,
+ * FH_BF16 or FH_F32, 16-byte aligned, hidden % 8 == 0); ids int64 on the device.
+ */
+int fh_embedding_fwd(fh_dtype dt, const void* weight, const int64_t* ids, void* out,
+                     int64_t n_tokens, int64_t vocab, int64_t hidden, hipStream_t stream);
+
+/* Bytes of workspace fh_embedding_bwd needs. */
+size_t fh_embedding_bwd_workspace_size(int64_t n_tokens, int64_t vocab);
+
+/* Backward of the lookup (F.embedding's weight gradient, the reference's
+ * scatter-add): dweight[v, :] = sum over tokens t with ids[t] == v of
+ * dy[t, :], accumulated in fp32 in ascending t and rounded once; every row of
+ * dweight [vocab, hidden] is written (zeros for ids no token uses).  Tokens
+ * whose id is outside [0, vocab) or equals padding_idx (nn.Embedding's; pass
+ * -1 for none) contribute nothing.  Deterministic: a stable radix sort of the
+ * ids, no floating-point atomics; n_tokens, vocab < 2^31.
+ */
+int fh_embedding_bwd(fh_dtype dt, const void* dy, const int64_t* ids, void* dweight,
+                     int64_t n_tokens, int64_t vocab, int64_t hidden, int64_t padding_idx,
+                     void* workspace, hipStream_t stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif
