@@ -280,7 +280,8 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True):
                  flop_per_launch=fwd_flop, ms_per_launch=round(ms_f, 4),
                  achieved_tflops=round(fwd_flop / ms_f / 1e9, 1),
                  frac=round(fwd_flop / ms_f / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)),
-            dict(kernel="attn_bwd", symbol=f"k_attn_bwd_dq<{hd}> + k_attn_bwd_dkdv<{hd}>",
+            dict(kernel="attn_bwd", symbol=f"k_attn_bwd_dq<{hd}> + k_attn_bwd_dkdv"
+                                           f"{'_fused' if hd <= 64 else ''}<{hd}>",
                  launches_per_step=L, flop_per_launch=bwd_flop, ms_per_launch=round(ms_b, 4),
                  achieved_tflops=round(bwd_flop / ms_b / 1e9, 1),
                  frac=round(bwd_flop / ms_b / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4))]

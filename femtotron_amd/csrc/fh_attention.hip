@@ -298,6 +298,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
       const char* K = sk + st * TILE;
       const char* V = sv + st * TILE;
       f32x16 x[BN / 32][QT];  // raw scores S^T, rows = keys, column = query
+      __builtin_amdgcn_iglp_opt(0);  // LDS reads interleaved with MFMAs (head_dim 128: -3%)
 #pragma unroll
       for (int t = 0; t < BN / 32; ++t) {
 #pragma unroll
@@ -656,6 +657,9 @@ __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves
 #pragma unroll
       for (int u = 0; u < NQT; ++u) {
         f32x16 x = zero16(), y = zero16();  // S, dP (rows = queries, column = key ki)
+        // Scheduling strategy 0 interleaves this tile's LDS fragment reads with
+        // its MFMAs (measured 749 -> 709 us for the TinyLlama backward).
+        __builtin_amdgcn_iglp_opt(0);
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
           x = mfma(lds_frag<HD>(Q, a_off, 32 * u, s), kf[s], x);
