@@ -50,6 +50,8 @@ SIGNATURES: dict[str, tuple] = {
                             _I64, _I64, _I64, _I64, _I64, _F, _V]),
     "fh_ce_fwd_bwd": (c_int, [c_int, _V, _I64, _V, _I64, _I64, _I64, _V, POINTER(c_float), _V]),
     "fh_adamw_workspace_size": (c_size_t, [_I64]),
+    "fh_gemm_tn_workspace_size": (c_size_t, [_I64, _I64, _I64]),
+    "fh_gemm_tn": (c_int, [c_int, _V, _I64, _V, _I64, _V, _I64, _I64, _I64, _I64, _V, _V]),
     "fh_embedding_fwd": (c_int, [c_int, _V, _V, _V, _I64, _I64, _I64, _V]),
     "fh_embedding_bwd_workspace_size": (c_size_t, [_I64, _I64]),
     "fh_embedding_bwd": (c_int, [c_int, _V, _V, _V, _I64, _I64, _I64, _I64, _V, _V]),

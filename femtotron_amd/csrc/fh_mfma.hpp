@@ -1,0 +1,138 @@
+// MFMA tile helpers shared by the attention and GEMM kernels (gfx950, wave64).
+//
+// v_mfma_f32_32x32x16_bf16: lane i of an operand holds row/col i%32 and the
+// K-slice 8*(i/32)..+7; lane i of the fp32 accumulator holds column i%32 and
+// rows 8*(j/4) + 4*(i/32) + j%4, j = 0..15.
+//
+// LDS tiles are [rows x HD] bf16 without padding, XOR-swizzled in 16-byte
+// chunks: chunk c of row r is stored at chunk position c ^ swz(r).  Operands
+// read a tile in two patterns, (a) ds_read_b128 of one chunk from 16
+// consecutive rows and (b) ds_read_b64_tr_b16 of 4 consecutive chunks from 4
+// consecutive rows (first row a multiple of 4) across 32 lanes; swz() maps
+// both onto the 16 distinct 4-bank groups of one LDS cycle, so neither has
+// bank conflicts.  A read address is a per-lane constant XOR a compile-time
+// constant, plus an immediate offset.
+#pragma once
+
+#include "fh_common.hpp"
+
+namespace fh {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+__device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) z[j] = 0.f;
+  return z;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// ------------------------------------------------------------- LDS tiles
+template <int HD>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (HD == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+  else if constexpr (HD == 64) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  else return (r >> 2) & 3;
+}
+
+// Pattern (a) lane constant: row lane%32 of a 32-row group, chunk lane/32.
+// Step s (K = 16s..16s+15 along the row) of the group at row0 is read at byte
+// row0*2*HD + (A ^ 32s).
+template <int HD>
+__device__ __forceinline__ int lane_off_a(int lane) {
+  const int l32 = lane & 31, hl = lane >> 5;
+  return l32 * (2 * HD) + ((hl ^ swz<HD>(l32)) << 4);
+}
+
+// Pattern (b) lane constant for rows 4*(lane/32) + (lane%16)/4 (+ plus8):
+// the 32-column block dt of the 16-row group at row0 is read at byte
+// row0*2*HD + (B ^ 64dt).
+template <int HD>
+__device__ __forceinline__ int lane_off_b(int lane, int plus8) {
+  const int hl = lane >> 5, L = lane & 15, mh = (lane >> 4) & 1;
+  const int r = 4 * hl + (L >> 2) + plus8;
+  const int cb = 2 * mh + ((L & 3) >> 1);
+  return r * (2 * HD) + ((cb ^ swz<HD>(r)) << 4) + 8 * (L & 1);
+}
+
+// Makes the per-lane read offsets opaque to the optimizer once per loop
+// iteration, so that their XORs with compile-time constants are recomputed
+// (one VALU op per read) instead of each being kept live in its own register.
+__device__ __forceinline__ void refresh_offsets(int& a, int& b0, int& b8) {
+  asm volatile("" : "+v"(a), "+v"(b0), "+v"(b8));
+}
+
+// Operand with K along the rows of a swizzled tile: lane i gets row
+// row0 + i%32, columns 16s + 8*(i/32) .. +7.
+template <int HD>
+__device__ __forceinline__ bf16x8 lds_frag(const char* tile, int a_off, int row0, int s) {
+  return *reinterpret_cast<const bf16x8*>(tile + row0 * (2 * HD) + (a_off ^ (32 * s)));
+}
+
+// Operand with K down the rows of a swizzled tile X: lane i gets
+// X[row0 + {4h+0..3, 8+4h+0..3}][32dt + i%32], h = i/32.
+template <int HD>
+__device__ __forceinline__ bf16x8 lds_frag_tr(const char* tile, int b0, int b8, int row0, int dt) {
+  const char* t = tile + row0 * (2 * HD);
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + (b0 ^ (64 * dt))));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + (b8 ^ (64 * dt))));
+  const uint2 ua = __builtin_bit_cast(uint2, a), ub = __builtin_bit_cast(uint2, b);
+  return as_bf16x8(make_uint4(ua.x, ua.y, ub.x, ub.y));
+}
+
+// Row (M index) of accumulator entry j for lane half hl.
+__device__ __forceinline__ int acc_row(int j, int hl) { return 8 * (j >> 2) + 4 * hl + (j & 3); }
+
+// Per-thread registers holding one ROWS x HD bf16 tile in flight from global
+// memory to LDS (the software pipeline's prefetch stage): load() issues the
+// 16-byte global loads (rows at or beyond `valid` read as zero), store()
+// writes them swizzled into an LDS tile.  Consecutive threads take
+// consecutive 16-byte chunks of a row; every pass covers a multiple of 16
+// rows, so a thread's swizzle is the same in every pass.
+template <int ROWS, int HD, int NT>
+struct TileRegs {
+  static constexpr int CPR = HD / 8;
+  static constexpr int CHUNKS = ROWS * CPR;
+  static constexpr int N = (CHUNKS + NT - 1) / NT;
+  static constexpr int RPP = NT / CPR;  // rows per pass
+  static_assert(NT % CPR == 0 && RPP % 16 == 0, "pass must cover a multiple of 16 rows");
+  uint4 r[N];
+  __device__ __forceinline__ void load(const uint16_t* src, int64_t ld, int valid, int tid) {
+    const int row = tid / CPR, col = (tid % CPR) * 8;
+    const uint16_t* p = src + static_cast<int64_t>(row) * ld + col;
+    if (valid >= ROWS) {  // whole tile in range (the common case): no per-row guard
+#pragma unroll
+      for (int i = 0; i < N; ++i)
+        if (CHUNKS % NT == 0 || tid + i * NT < CHUNKS)
+          r[i] = *reinterpret_cast<const uint4*>(p + static_cast<int64_t>(i * RPP) * ld);
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      r[i] = make_uint4(0, 0, 0, 0);
+      if ((CHUNKS % NT == 0 || tid + i * NT < CHUNKS) && row + i * RPP < valid)
+        r[i] = *reinterpret_cast<const uint4*>(p + static_cast<int64_t>(i * RPP) * ld);
+    }
+  }
+  __device__ __forceinline__ void store(char* tile, int tid) const {
+    const int row = tid / CPR, ch = tid % CPR;
+    char* p = tile + row * (2 * HD) + ((ch ^ swz<HD>(row)) << 4);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (CHUNKS % NT == 0 || tid + i * NT < CHUNKS)
+        *reinterpret_cast<uint4*>(p + i * RPP * (2 * HD)) = r[i];
+  }
+};
+
+}  // namespace
+}  // namespace fh

@@ -310,3 +310,33 @@ def embedding_bwd(dy: torch.Tensor, ids: torch.Tensor, vocab: int,
     _lib.call("fh_embedding_bwd", _dtype_code(dy), _ptr(dy), _ptr(ids), _ptr(dw), n, vocab, hidden,
               -1 if padding_idx is None else int(padding_idx), _ptr(ws), _stream(dy))
     return dw
+
+
+# ------------------------------------------------------------- GEMM
+def gemm_tn_supported(a: torch.Tensor, b: torch.Tensor) -> bool:
+    """Whether gemm_tn takes a [k, m] and b [k, n]: bf16 on one HIP device, last
+    dims contiguous, m and n multiples of 256, k a multiple of 64, aligned."""
+    if not (a.is_cuda and b.is_cuda and a.device == b.device and a.dtype == b.dtype == torch.bfloat16):
+        return False
+    if a.dim() != 2 or b.dim() != 2 or a.size(0) != b.size(0) or a.stride(1) != 1 or b.stride(1) != 1:
+        return False
+    k, m = a.shape
+    n = b.size(1)
+    return (m % 256 == 0 and n % 256 == 0 and k % 64 == 0 and k > 0 and a.stride(0) % 8 == 0
+            and b.stride(0) % 8 == 0 and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0)
+
+
+def gemm_tn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """a^T @ b for a [k, m], b [k, n] (bf16, token-major): [m, n], fp32 accumulation."""
+    _require_gpu(a, b)
+    if not gemm_tn_supported(a, b):
+        raise ValueError(f"gemm_tn: unsupported operands {tuple(a.shape)} {a.stride()} x "
+                         f"{tuple(b.shape)} {b.stride()} ({a.dtype})")
+    k, m = a.shape
+    n = b.size(1)
+    c = torch.empty(m, n, dtype=a.dtype, device=a.device)
+    nbytes = _lib.lib().fh_gemm_tn_workspace_size(m, n, k)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device) if nbytes else None
+    _lib.call("fh_gemm_tn", _dtype_code(a), _ptr(a), a.stride(0), _ptr(b), b.stride(0), _ptr(c), n,
+              m, n, k, _ptr(ws), _stream(a))
+    return c

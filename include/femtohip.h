@@ -261,6 +261,21 @@ int fh_embedding_bwd(fh_dtype dt, const void* dy, const int64_t* ids, void* dwei
                      int64_t n_tokens, int64_t vocab, int64_t hidden, int64_t padding_idx,
                      void* workspace, hipStream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Weight-gradient GEMM of the projections: C[m, n] = sum_t A[t, m] * B[t, n]
+ * (C = A^T B), the grad_weight = grad_output^T @ input of every F.linear in the
+ * layer backward (femtotron/parallel/tensor_parallel/linear.py:72, 206; HF
+ * nn.Linear at one rank).  A [k, m] (row stride lda), B [k, n] (ldb), C [m, n]
+ * (ldc), all bf16, row-major, 16-byte aligned; m, n multiples of 256, k a
+ * multiple of 64.  fp32 accumulation, C rounded to bf16 once.  When the
+ * output has few 256 x 256 tiles the k range is split into slices whose fp32
+ * partial sums go to `workspace` (fh_gemm_tn_workspace_size bytes, 0 = none
+ * needed) and are added in slice order: deterministic.
+ */
+size_t fh_gemm_tn_workspace_size(int64_t m, int64_t n, int64_t k);
+int fh_gemm_tn(fh_dtype dt, const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
+               int64_t ldc, int64_t m, int64_t n, int64_t k, void* workspace, hipStream_t stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif
