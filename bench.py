@@ -16,7 +16,8 @@ Prints ONE JSON line.  Besides tokens/s it reports:
   * roofline: the fused memory-bound kernel with the largest share of step time,
     its algorithmic bytes per launch / its mean launch time (HIP events on the
     launch stream) against the 8 TB/s HBM peak, and every other fused kernel;
-  * attention kernels against the 2.5 PFLOP/s dense bf16 MFMA peak;
+  * attention kernels and the hand-written weight-gradient GEMM against the 2.5 PFLOP/s dense
+    bf16 MFMA peak;
   * peak activation bytes per token of the fused path and of the reference path
     (Hugging Face layers under torch.utils.checkpoint, debug=True) on the same GPU;
   * cpu_baseline: the reference-equivalent path (oracle/torch_llama.py under
@@ -91,7 +92,7 @@ def parse_args():
     ap.add_argument("--profile-kernel", default=None,
                     help="launch only this fused kernel (swiglu_fwd, swiglu_bwd, rmsnorm_fwd, "
                          "add_rmsnorm_fwd, rmsnorm_bwd, rope_fwd, residual_add, attn_fwd, attn_bwd; "
-                         "embedding_fwd, embedding_bwd; "
+                         "embedding_fwd, embedding_bwd; gemm_tn_qkv, gemm_tn_o (weight-gradient GEMM); "
                          "adamw: one optimizer step over the workload's parameter shapes) at "
                          "--workload's step shape, after a 1 GiB device copy that calibrates HBM byte "
                          "counters, for rocprofv3 --pmc runs; prints one JSON line and exits")
@@ -285,6 +286,20 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True):
                  launches_per_step=L, flop_per_launch=bwd_flop, ms_per_launch=round(ms_b, 4),
                  achieved_tflops=round(bwd_flop / ms_b / 1e9, 1),
                  frac=round(bwd_flop / ms_b / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4))]
+    # the hand-written weight-gradient GEMM, at the projections the layer routes to it
+    from femtotron_amd.fused_layer import GEMM_TN_MAX_TILES
+    for name, n_out, k_in in (("wgrad_qkv", Hq + 2 * Hkv, H), ("wgrad_o", H, Hq)):
+        dy = rnd(T, n_out)
+        xin = rnd(T, k_in)
+        if not ops.gemm_tn_supported(dy, xin) or (n_out // 256) * (k_in // 256) > GEMM_TN_MAX_TILES:
+            continue
+        ms = event_ms(torch, lambda i=0: ops.gemm_tn(dy, xin), iters)
+        flop = 2 * T * n_out * k_in
+        mfma.append(dict(kernel=name, symbol="k_gemm_tn (+ k_gemm_tn_reduce)", launches_per_step=L,
+                         flop_per_launch=flop, ms_per_launch=round(ms, 4),
+                         achieved_tflops=round(flop / ms / 1e9, 1),
+                         frac=round(flop / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)))
+        del dy, xin
     return rows, mfma
 
 
@@ -357,6 +372,12 @@ def profile_kernel(torch, name: str, c: dict, launches: int = 10) -> dict:
             dys = [rnd(T, H) for _ in range(n)]
             fn = lambda i: ops.embedding_bwd(dys[i], ids, V)
             nbytes = 2 * T * H + 2 * V * H + 8 * T
+    elif name in ("gemm_tn_qkv", "gemm_tn_o"):
+        n_out, k_in = (Hq + 2 * Hkv, H) if name == "gemm_tn_qkv" else (H, Hq)
+        dys = [rnd(T, n_out) for _ in range(2)]
+        xs = [rnd(T, k_in) for _ in range(2)]
+        fn = lambda i: ops.gemm_tn(dys[i % 2], xs[i % 2])
+        nbytes = None  # MFMA-bound: 2*T*n_out*k_in FLOP per launch
     elif name == "adamw":
         from femtotron_amd.optim import FusedAdamW
         V, L = c["vocab"], c["layers"]
@@ -578,7 +599,7 @@ def main() -> int:
                    "parallelism": "single GPU (TP=PP=DP=1)"},
         "roofline": roofline,
         "fused_kernels_hbm": rows,
-        "attention_mfma": mfma,
+        "mfma_kernels": mfma,
         "gemms": ("hipBLASLt/rocBLAS, TunableOp solutions from femtotron_amd/tuned/"
                   "tunableop_gfx950.csv" if tuned else "hipBLASLt default heuristics"),
         "weights": f"q/k/v and gate/up packed contiguously ({packed_groups} groups)",
