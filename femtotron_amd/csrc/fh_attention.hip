@@ -415,59 +415,136 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 }
 
 // Prefetch stage of the dK/dV kernels: the Q and dO tiles, lse and delta of
-// the next (query head, query tile) of the loop, which it walks incrementally
-// (no division in the loop).  q, dO, lse, delta point at the group's first
-// query head; lse/delta rows are [head][S].
+// one (query tile, query head) item of the loop.  Items run from the last
+// query tile down to the key block's first (qt0), and over the group's query
+// heads within a tile: all blocks of one kv head start at the same tile and
+// move down together, so a tile loaded by one block is found in L2 by the
+// others.  q, dO, lse, delta point at the group's first query head;
+// lse/delta rows are [head][S].  fetch() is branch-free: every thread issues
+// the same loads, rows past S and tiles past the last item are clamped in
+// bounds (so it may run past the end), and every check and all arithmetic on
+// the loaded values wait for commit().  Arithmetic on a loaded value inside
+// fetch() would make the wave wait at once for all of this fetch's loads,
+// tile included, and a branch around a load would make the compiler wait for
+// every load in flight before the next commit().
 template <int HD, int BQ, int NT>
 struct QTileStream {
   TileRegs<BQ, HD, NT> pq, pg;
-  float pl = 0.f, pd = 0.f;  // -lse*log2(e) and delta of the tile in flight (threads 0..BQ-1)
-  int hh = 0, qt = 0;        // the tile to fetch next
+  float pl = 0.f, pd = 0.f;  // lse and delta of query row tid % BQ of the tile in flight
+  int valid = 0;             // rows of the tile in flight inside the sequence (>= 1)
+  int qt = 0, hh = 0;        // the item to fetch next
+  __device__ __forceinline__ void start(int qt_end) {
+    qt = qt_end - 1;
+    hh = 0;
+  }
   __device__ __forceinline__ void fetch(const uint16_t* q, int64_t ldq, const uint16_t* dO,
                                         int64_t lddo, const float* lse, const float* delta,
-                                        int S, int qt0, int qt_end, int tid) {
-    const int qs = qt * BQ;
+                                        int S, int qt0, int group, int tid) {
+    const int qs = max(qt, qt0) * BQ;
     const int64_t hcol = static_cast<int64_t>(hh) * HD;
-    pq.load(q + static_cast<int64_t>(qs) * ldq + hcol, ldq, S - qs, tid);
-    pg.load(dO + static_cast<int64_t>(qs) * lddo + hcol, lddo, S - qs, tid);
-    if (tid < BQ) {
-      const int64_t row = static_cast<int64_t>(hh) * S + qs + tid;
-      const bool ok = qs + tid < S;
-      pl = ok ? -lse[row] * kLog2e : 0.f;
-      pd = ok ? delta[row] : 0.f;
-    }
-    if (++qt == qt_end) {
-      qt = qt0;
-      ++hh;
+    valid = S - qs;
+    pq.load_clamped(q + static_cast<int64_t>(qs) * ldq + hcol, ldq, valid, tid);
+    pg.load_clamped(dO + static_cast<int64_t>(qs) * lddo + hcol, lddo, valid, tid);
+    const int64_t row = static_cast<int64_t>(hh) * S + min(qs + tid % BQ, S - 1);
+    pl = lse[row];
+    pd = delta[row];
+    advance(group);
+  }
+  // Steps to the next item without loading it.
+  __device__ __forceinline__ void advance(int group) {
+    if (++hh == group) {
+      hh = 0;
+      --qt;
     }
   }
   __device__ __forceinline__ void commit(char* sq, char* sg, float* slse, float* sdl, int tid) const {
-    pq.store(sq, tid);
-    pg.store(sg, tid);
+    pq.store_valid(sq, valid, tid);
+    pg.store_valid(sg, valid, tid);
     if (tid < BQ) {
-      slse[tid] = pl;
-      sdl[tid] = pd;
+      const bool ok = tid < valid;
+      slse[tid] = ok ? -pl * kLog2e : 0.f;  // exp2 argument offset: -lse * log2(e)
+      sdl[tid] = ok ? pd : 0.f;
     }
   }
 };
 
 // ------------------------------------------ backward: dK, dV (bf16), fused roles
-// Used for head_dim <= 64.  Block = 8 waves of 32 keys each, for one (batch, kv
-// head).  Causal work per key block grows with the number of later queries, so
-// a block pairs key block j (waves 0-3) with key block nkb-1-j (waves 4-7):
-// every SIMD hosts one wave of each and all blocks carry the same work.  K and
-// V of a wave's keys stay in registers; the loop runs over the group's query
-// heads and 64-query tiles (double-buffered in LDS, prefetched through
+// Used for head_dim <= 64.  Block = 8 waves for one (batch, kv head) and two
+// key blocks of 128 keys, j and nkb-1-j, taken one after the other (causal
+// work per key block grows with the number of later queries, so every block
+// carries the same work).  Within a key block, wave w holds K and V of keys
+// 32*(w%4)..+31 in registers, and each 64-query tile is split between the two
+// halves of the block: waves 0-3 take its queries 0-31, waves 4-7 queries
+// 32-63.  So all 8 waves (two per SIMD) are busy in every iteration, and every
+// block runs the same number of iterations.  The loop runs over the group's
+// query heads and 64-query tiles (double-buffered in LDS, prefetched through
 // registers):
 //   S = Q K^T, P = exp(S - lse), dP = dO V^T, dS = P (dP - delta),
 //   dV^T += dO^T P,  dK^T += Q^T dS,  dK = scale * dK.
-// Each kv head's gradient is complete inside one block: no atomics.
+// At the end of a key block the halves' partial dK and dV are exchanged
+// through LDS and summed in a fixed order (half 0 + half 1): half 0 stores dK,
+// half 1 stores dV.  Each kv head's gradient is complete inside one block: no
+// atomics.
 template <int HD>
 struct DkdvFusedTiles {
   static constexpr int BQ = 64;
-  static constexpr int NWH = 4;  // waves per key block (two key blocks per block)
+  static constexpr int NWH = 4;  // waves per query half (32 keys each)
   static constexpr int NT = 2 * NWH * 64;
 };
+
+// One wave's share of a query tile in the dK/dV kernel: the 32 queries at
+// row hrow of the LDS tiles Q and dO (first query qh) against the wave's 32
+// keys (first key kw, this lane's key ki), accumulated into dK^T and dV^T.
+template <int HD>
+__device__ __forceinline__ void dkdv_tile(const char* Q, const char* G, const float* sl, const float* sd,
+                                          const bf16x8 (&kf)[HD / 16], const bf16x8 (&vf)[HD / 16],
+                                          f32x16 (&dkacc)[HD / 32], f32x16 (&dvacc)[HD / 32], int a_off,
+                                          int b0, int b8, int hrow, int qh, int kw, int ki, int S,
+                                          float scale_log2, int hl) {
+  constexpr int NS = HD / 16, ND = HD / 32;
+  const bool need_mask = (qh < kw + 31) || (qh + 32 > S) || (kw + 32 > S);
+  f32x16 x = zero16(), y = zero16();  // S, dP (rows = queries, column = key ki)
+  // Scheduling strategy 0 interleaves the LDS fragment reads with the MFMAs.
+  __builtin_amdgcn_iglp_opt(0);
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    x = mfma(lds_frag<HD>(Q, a_off, hrow, s), kf[s], x);
+    y = mfma(lds_frag<HD>(G, a_off, hrow, s), vf[s], y);
+  }
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const float4 L4 = *reinterpret_cast<const float4*>(&sl[hrow + 8 * g + 4 * hl]);
+    const float4 D4 = *reinterpret_cast<const float4*>(&sd[hrow + 8 * g + 4 * hl]);
+    const float Lv[4] = {L4.x, L4.y, L4.z, L4.w};
+    const float Dv[4] = {D4.x, D4.y, D4.z, D4.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int j = 4 * g + e;
+      const float p = fast_exp2(fmaf(x[j], scale_log2, Lv[e]));
+      x[j] = p;                   // P
+      y[j] = p * (y[j] - Dv[e]);  // dS
+    }
+  }
+  if (need_mask) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int qa = qh + acc_row(j, hl);
+      const bool dead = (ki > qa) | (qa >= S) | (ki >= S);
+      x[j] = dead ? 0.f : x[j];
+      y[j] = dead ? 0.f : y[j];
+    }
+  }
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) {
+    const bf16x8 pf = pack_frag(x, 8 * s2);
+    const bf16x8 df = pack_frag(y, 8 * s2);
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) {
+      dvacc[dt] = mfma(lds_frag_tr<HD>(G, b0, b8, hrow + 16 * s2, dt), pf, dvacc[dt]);
+      dkacc[dt] = mfma(lds_frag_tr<HD>(Q, b0, b8, hrow + 16 * s2, dt), df, dkacc[dt]);
+    }
+  }
+}
 
 template <int HD>
 __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_bwd_dkdv_fused(
@@ -478,121 +555,121 @@ __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves
     float scale_log2, float scale) {
   constexpr int NWH = DkdvFusedTiles<HD>::NWH, NT = DkdvFusedTiles<HD>::NT;
   constexpr int BKN = NWH * 32, BQ = DkdvFusedTiles<HD>::BQ, NS = HD / 16, ND = HD / 32;
-  constexpr int NQT = BQ / 32, TILE = BQ * 2 * HD;
+  constexpr int TILE = BQ * 2 * HD;
+  static_assert(BQ == 64 && BKN % BQ == 0, "two 32-query halves per tile; key blocks align with tiles");
   __shared__ __align__(16) char sq[2 * TILE];
   __shared__ __align__(16) char sg[2 * TILE];
   __shared__ __align__(16) float slse[2][BQ];
   __shared__ __align__(16) float sdl[2][BQ];
+  __shared__ __align__(16) float xchg[2][NWH][ND * 16][64];  // [0]: dV of half 0, [1]: dK of half 1
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
+  const int half = wave / NWH, wq = wave % NWH;
   const XcdOrder ord = xcd_order();
   const int bk = ord.y, b = bk / nkv, kvh = bk - b * nkv;
   const int nkb = (S + BKN - 1) / BKN;
   const int jlo = ord.rank, jhi = nkb - 1 - ord.rank;
-  const bool upper = wave >= NWH;
-  const bool has_keys = !upper || jhi > jlo;
-  const int kw = (upper ? jhi : jlo) * BKN + (wave % NWH) * 32, ki = kw + l32;
   const int64_t tok0 = static_cast<int64_t>(b) * S;
   int a_off = lane_off_a<HD>(lane);
   int b0 = lane_off_b<HD>(lane, 0), b8 = lane_off_b<HD>(lane, 8);
-
-  bf16x8 kf[NS], vf[NS];
-  {
-    const bool ok = has_keys && ki < S;
-    const uint16_t* krow = k + (tok0 + ki) * ldk + static_cast<int64_t>(kvh) * HD + 8 * hl;
-    const uint16_t* vrow = v + (tok0 + ki) * ldv + static_cast<int64_t>(kvh) * HD + 8 * hl;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      kf[s] = ok ? ld_frag(krow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
-      vf[s] = ok ? ld_frag(vrow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
-    }
-  }
-  f32x16 dkacc[ND], dvacc[ND];
-#pragma unroll
-  for (int dt = 0; dt < ND; ++dt) {
-    dkacc[dt] = zero16();
-    dvacc[dt] = zero16();
-  }
-
-  // iteration space: (query head of the group) x (query tiles from the first key of block jlo)
-  const int qt0 = (jlo * BKN) / BQ, qt_end = (S + BQ - 1) / BQ;
-  const int n_it = group * (qt_end - qt0);
   const int64_t h0 = static_cast<int64_t>(kvh) * group;
   const uint16_t* qg = q + tok0 * ldq + h0 * HD;
   const uint16_t* gg = dO + tok0 * lddo + h0 * HD;
   const float* lg = lse + (static_cast<int64_t>(b) * nh + h0) * S;
   const float* dg = delta + (static_cast<int64_t>(b) * nh + h0) * S;
-  QTileStream<HD, BQ, NT> pre;
-  pre.qt = qt0;
-  if (n_it > 0) {
-    pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, qt_end, tid);
-    pre.commit(sq, sg, slse[0], sdl[0], tid);
-  }
-  __syncthreads();
-  int cqt = qt0;  // query tile of the current iteration
-  for (int it = 0; it < n_it; ++it) {
-    const int st = it & 1;
-    const bool more = it + 1 < n_it;
-    refresh_offsets(a_off, b0, b8);
-    if (more) pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, qt_end, tid);
-    const int q0 = cqt * BQ;
-    if (has_keys && q0 + BQ - 1 >= kw) {  // some query of the tile reaches this wave's keys
-      const char* Q = sq + st * TILE;
-      const char* G = sg + st * TILE;
-      const bool need_mask = (q0 < kw + 31) || (q0 + BQ > S) || (kw + 32 > S);
+  const int qt_end = (S + BQ - 1) / BQ;
+  const int hrow = 32 * half;  // this wave's first query row within a tile
+
+  for (int ph = 0; ph < 2; ++ph) {
+    if (ph == 1 && jhi <= jlo) break;  // block-uniform: the middle key block of an odd count
+    const int jb = ph == 0 ? jlo : jhi;
+    const int kw = jb * BKN + wq * 32, ki = kw + l32;
+    bf16x8 kf[NS], vf[NS];
+    {
+      const bool ok = ki < S;
+      const uint16_t* krow = k + (tok0 + ki) * ldk + static_cast<int64_t>(kvh) * HD + 8 * hl;
+      const uint16_t* vrow = v + (tok0 + ki) * ldv + static_cast<int64_t>(kvh) * HD + 8 * hl;
 #pragma unroll
-      for (int u = 0; u < NQT; ++u) {
-        f32x16 x = zero16(), y = zero16();  // S, dP (rows = queries, column = key ki)
-        // Scheduling strategy 0 interleaves this tile's LDS fragment reads with
-        // its MFMAs (measured 749 -> 709 us for the TinyLlama backward).
-        __builtin_amdgcn_iglp_opt(0);
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          x = mfma(lds_frag<HD>(Q, a_off, 32 * u, s), kf[s], x);
-          y = mfma(lds_frag<HD>(G, a_off, 32 * u, s), vf[s], y);
-        }
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const float4 L4 = *reinterpret_cast<const float4*>(&slse[st][32 * u + 8 * g + 4 * hl]);
-          const float4 D4 = *reinterpret_cast<const float4*>(&sdl[st][32 * u + 8 * g + 4 * hl]);
-          const float Lv[4] = {L4.x, L4.y, L4.z, L4.w};
-          const float Dv[4] = {D4.x, D4.y, D4.z, D4.w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int j = 4 * g + e;
-            const float p = fast_exp2(fmaf(x[j], scale_log2, Lv[e]));
-            x[j] = p;                   // P
-            y[j] = p * (y[j] - Dv[e]);  // dS
-          }
-        }
-        if (need_mask) {
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int qa = q0 + 32 * u + acc_row(j, hl);
-            const bool dead = (ki > qa) | (qa >= S) | (ki >= S);
-            x[j] = dead ? 0.f : x[j];
-            y[j] = dead ? 0.f : y[j];
-          }
-        }
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          const bf16x8 pf = pack_frag(x, 8 * s2);
-          const bf16x8 df = pack_frag(y, 8 * s2);
-#pragma unroll
-          for (int dt = 0; dt < ND; ++dt) {
-            dvacc[dt] = mfma(lds_frag_tr<HD>(G, b0, b8, 32 * u + 16 * s2, dt), pf, dvacc[dt]);
-            dkacc[dt] = mfma(lds_frag_tr<HD>(Q, b0, b8, 32 * u + 16 * s2, dt), df, dkacc[dt]);
-          }
-        }
+      for (int s = 0; s < NS; ++s) {
+        kf[s] = ok ? ld_frag(krow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
+        vf[s] = ok ? ld_frag(vrow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
       }
     }
-    if (more) pre.commit(sq + (st ^ 1) * TILE, sg + (st ^ 1) * TILE, slse[st ^ 1], sdl[st ^ 1], tid);
-    if (++cqt == qt_end) cqt = qt0;
+    f32x16 dkacc[ND], dvacc[ND];
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) {
+      dkacc[dt] = zero16();
+      dvacc[dt] = zero16();
+    }
+
+    // Iteration space: (query tiles from the key block's first key, last tile
+    // first) x (query heads of the group), n_it >= 1 items.  Two register
+    // stages take every other item: the tile of iteration it + 2 is loaded
+    // while iteration it computes and written to LDS at the end of iteration
+    // it + 1, so its global loads have two iterations to arrive.
+    const int qt0 = (jb * BKN) / BQ;
+    const int n_it = group * (qt_end - qt0);
+    QTileStream<HD, BQ, NT> pa, pb;  // items 0, 2, 4, ... and 1, 3, 5, ...
+    pa.start(qt_end);
+    pb.start(qt_end);
+    pb.advance(group);
+    pa.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, tid);
+    pa.advance(group);
+    pb.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, tid);
+    pb.advance(group);
+    pa.commit(sq, sg, slse[0], sdl[0], tid);
     __syncthreads();
+    int cqt = qt_end - 1, chh = 0;  // query tile and head of the current item
+    // One iteration: PF (free registers) fetches item IT + 2, PC (holding item
+    // IT + 1) is written to the other LDS stage once the tile is done.  The
+    // loop runs whole pairs and fetches unconditionally (items past the end
+    // are clamped reads, never used), so every path has one fetch's loads in
+    // flight at each commit.
+#define FH_DKDV_ITER(IT, PF, PC)                                                                  \
+  {                                                                                               \
+    const int st = (IT) & 1;                                                                      \
+    refresh_offsets(a_off, b0, b8);                                                               \
+    PF.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, tid);                                      \
+    PF.advance(group);                                                                            \
+    const int qh = cqt * BQ + hrow; /* first query of this wave's half */                         \
+    if ((IT) < n_it && qh + 31 >= kw) /* some query of the half reaches this wave's keys */      \
+      dkdv_tile<HD>(sq + st * TILE, sg + st * TILE, slse[st], sdl[st], kf, vf, dkacc, dvacc,     \
+                    a_off, b0, b8, hrow, qh, kw, ki, S, scale_log2, hl);                          \
+    if ((IT) + 1 < n_it)                                                                          \
+      PC.commit(sq + (st ^ 1) * TILE, sg + (st ^ 1) * TILE, slse[st ^ 1], sdl[st ^ 1], tid);      \
+    if (++chh == group) {                                                                         \
+      chh = 0;                                                                                    \
+      --cqt;                                                                                      \
+    }                                                                                             \
+    __syncthreads();                                                                              \
   }
-  if (has_keys && ki < S) {
-    store_rows_T<HD>(dk + (tok0 + ki) * lddk + static_cast<int64_t>(kvh) * HD, dkacc, scale, hl);
-    store_rows_T<HD>(dv + (tok0 + ki) * lddv + static_cast<int64_t>(kvh) * HD, dvacc, 1.f, hl);
+    for (int it = 0; it < n_it; it += 2) {
+      FH_DKDV_ITER(it, pa, pb)
+      FH_DKDV_ITER(it + 1, pb, pa)
+    }
+#undef FH_DKDV_ITER
+
+    // Sum the halves: half 0 hands over its dV, half 1 its dK.
+    float(*mine)[64] = xchg[half][wq];
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) mine[dt * 16 + j][lane] = half == 0 ? dvacc[dt][j] : dkacc[dt][j];
+    __syncthreads();
+    const float(*other)[64] = xchg[half ^ 1][wq];
+    if (half == 0) {
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) dkacc[dt][j] = dkacc[dt][j] + other[dt * 16 + j][lane];
+      if (ki < S) store_rows_T<HD>(dk + (tok0 + ki) * lddk + static_cast<int64_t>(kvh) * HD, dkacc, scale, hl);
+    } else {
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) dvacc[dt][j] = other[dt * 16 + j][lane] + dvacc[dt][j];
+      if (ki < S) store_rows_T<HD>(dv + (tok0 + ki) * lddv + static_cast<int64_t>(kvh) * HD, dvacc, 1.f, hl);
+    }
   }
 }
 
@@ -656,7 +733,7 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) __attribute__((amdgpu_waves_per_
 #pragma unroll
   for (int dt = 0; dt < ND; ++dt) acc[dt] = zero16();
 
-  // iteration space: (query head of the group) x (query tiles from the block's first key)
+  // iteration space: (query tiles from the block's first key, last first) x (query heads of the group)
   const int qt0 = kb0 / BQ, qt_end = (S + BQ - 1) / BQ;
   const int n_it = group * (qt_end - qt0);
   const int64_t h0 = static_cast<int64_t>(kvh) * group;
@@ -665,18 +742,18 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) __attribute__((amdgpu_waves_per_
   const float* lg = lse + (static_cast<int64_t>(b) * nh + h0) * S;
   const float* dg = delta + (static_cast<int64_t>(b) * nh + h0) * S;
   QTileStream<HD, BQ, NT> pre;
-  pre.qt = qt0;
+  pre.start(qt_end);
   if (n_it > 0) {
-    pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, qt_end, tid);
+    pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, tid);
     pre.commit(sq, sg, slse[0], sdl[0], tid);
   }
   __syncthreads();
-  int cqt = qt0;  // query tile of the current iteration
+  int cqt = qt_end - 1, chh = 0;  // query tile and head of the current item
   for (int it = 0; it < n_it; ++it) {
     const int st = it & 1;
     const bool more = it + 1 < n_it;
     refresh_offsets(a_off, b0, b8);
-    if (more) pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, qt_end, tid);
+    pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, tid);  // past the end: clamped, unused
     const int q0 = cqt * BQ;
     // some query of the tile reaches this sub-tile's keys (same answer for both roles)
     const bool active = kw < S && q0 + BQ - 1 >= kw;
@@ -745,7 +822,10 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) __attribute__((amdgpu_waves_per_
         }
     }
     if (more) pre.commit(sq + (st ^ 1) * TILE, sg + (st ^ 1) * TILE, slse[st ^ 1], sdl[st ^ 1], tid);
-    if (++cqt == qt_end) cqt = qt0;
+    if (++chh == group) {
+      chh = 0;
+      --cqt;
+    }
     __syncthreads();
   }
   if (ki < S) {

@@ -132,6 +132,29 @@ struct TileRegs {
       if (CHUNKS % NT == 0 || tid + i * NT < CHUNKS)
         *reinterpret_cast<uint4*>(p + i * RPP * (2 * HD)) = r[i];
   }
+  // Branch-free pair for software pipelines: every thread issues the same N
+  // loads whatever `valid` is (1 <= valid; rows at or beyond it re-read row
+  // valid - 1, threads past the tile re-read a chunk of it), so every path
+  // has the same loads in flight and the compiler waits for exactly one
+  // stage's loads before a store_valid().  store_valid() writes zeros for
+  // the rows at or beyond valid.
+  __device__ __forceinline__ void load_clamped(const uint16_t* src, int64_t ld, int valid, int tid) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int c = CHUNKS % NT == 0 ? tid + i * NT : (tid + i * NT) % CHUNKS;
+      const int row = min(c / CPR, valid - 1);
+      r[i] = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(row) * ld + (c % CPR) * 8);
+    }
+  }
+  __device__ __forceinline__ void store_valid(char* tile, int valid, int tid) const {
+    const int row = tid / CPR, ch = tid % CPR;
+    char* p = tile + row * (2 * HD) + ((ch ^ swz<HD>(row)) << 4);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (CHUNKS % NT == 0 || tid + i * NT < CHUNKS)
+        *reinterpret_cast<uint4*>(p + i * RPP * (2 * HD)) =
+            row + i * RPP < valid ? r[i] : make_uint4(0, 0, 0, 0);
+  }
 };
 
 }  // namespace

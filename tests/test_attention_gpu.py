@@ -74,6 +74,7 @@ def _tensor_err(a, b):
     (1, 300, 8, 8, 128),    # MHA, hd 128, ragged
     (1, 130, 32, 8, 128),   # Llama-3 grouping
     (3, 65, 2, 2, 64),      # S just past one key block
+    (1, 300, 4, 2, 64),     # odd count of 128-key blocks: the middle block is paired with itself
     (1, 1, 4, 2, 64),       # single token: output is v
 ])
 def test_attention_bf16_matches_closed_form(B, S, nh, nkv, hd):
