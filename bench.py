@@ -87,6 +87,9 @@ def parse_args():
                          "the results to CSV and exit")
     ap.add_argument("--stock-boundary", action="store_true",
                     help="keep the reference's nn.Embedding and final LlamaRMSNorm (no fuse_boundary_ops)")
+    ap.add_argument("--stock-attention", action="store_true",
+                    help="under --ac selective keep HF's LlamaAttention outside the checkpoints "
+                         "(no fuse_attention)")
     ap.add_argument("--no-optimizer", action="store_true",
                     help="skip the fused-AdamW timing (reported beside the fwd+bwd metric)")
     ap.add_argument("--profile-kernel", default=None,
@@ -165,7 +168,8 @@ def event_ms(torch, fn, iters: int) -> float:
     return start.elapsed_time(end) / iters
 
 
-def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True):
+def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True,
+                 fused_attention: bool = False):
     """Fused kernels at the step's shapes.  Each launch reads a different buffer
     set (working set > 1 GiB) so the 256 MiB MALL cannot serve repeats: the bytes
     come from HBM as in the step.  launches_per_step counts the launches of one
@@ -195,6 +199,11 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True):
 
     L = c["layers"]
     sel = ac == "selective"
+    # attention's kernels run in the step: inside the fused layer (full AC,
+    # forward twice: forward and recompute) or in fused_attention's modules
+    # outside the checkpoints (selective AC, forward once)
+    attn = not sel or fused_attention
+    n_fwd = L if sel else 2 * L
     # rmsnorm_fwd: x -> y   (4TH bytes)
     xs = sets(8, lambda: rnd(T, H))
     ys = sets(8, lambda: torch.empty(T, H, device=dev, dtype=bf))
@@ -230,9 +239,9 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True):
     qkvs = sets(6, lambda: rnd(T, Hq + 2 * Hkv))
     cos = torch.cos(torch.arange(c["seq"] * hd, device=dev, dtype=torch.float32)).to(bf).view(1, c["seq"], hd)
     sin = torch.sin(torch.arange(c["seq"] * hd, device=dev, dtype=torch.float32)).to(bf).view(1, c["seq"], hd)
-    if not sel:
+    if attn:
         ms = event_ms(torch, lambda i=0: ops.rope_fwd_(qkvs[i % 6], nh + nkv, hd, c["seq"], cos, sin), iters)
-        add_row("rope_fwd", "k_rope<fwd>", 2 * L, 4 * T * (Hq + Hkv), ms)
+        add_row("rope_fwd", "k_rope<fwd>", n_fwd, 4 * T * (Hq + Hkv), ms)
         ms = event_ms(torch, lambda i=0: ops.rope_bwd_(qkvs[i % 6], nh + nkv, hd, c["seq"], cos, sin), iters)
         add_row("rope_bwd", "k_rope<bwd>", L, 4 * T * (Hq + Hkv), ms)
     # SwiGLU: g,u -> p (6TF);  dp,g,u -> dg,du (10TF)
@@ -259,7 +268,7 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True):
         add_row("embedding_bwd", "k_embed_keys + 3 x k_radix_* + k_embed_bounds + k_embed_rows", 1,
                 2 * T * H + 2 * V * H + 8 * T, ms)
         del emb, dys
-    if sel:  # attention is outside the checkpointed modules under this policy
+    if not attn:  # HF's attention outside the checkpointed modules (selective, --stock-attention)
         return rows, []
 
     # attention (MFMA-bound): causal flop count 4*B*nh*S^2*hd/2 forward
@@ -277,7 +286,7 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True):
     # backward: dK/dV kernel 4 products + dQ kernel 3 products (the dQ kernel
     # recomputes S and dP); algorithmic = the 5 products of attention backward
     bwd_flop = 2.5 * fwd_flop
-    mfma = [dict(kernel="attn_fwd", symbol=f"k_attn_fwd<{hd}>", launches_per_step=2 * L,
+    mfma = [dict(kernel="attn_fwd", symbol=f"k_attn_fwd<{hd}>", launches_per_step=n_fwd,
                  flop_per_launch=fwd_flop, ms_per_launch=round(ms_f, 4),
                  achieved_tflops=round(fwd_flop / ms_f / 1e9, 1),
                  frac=round(fwd_flop / ms_f / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)),
@@ -501,9 +510,11 @@ def main() -> int:
               flush=True)
         return 0
 
-    from femtotron_amd import (dispatch_counts, fuse_boundary_ops, fused_checkpoint, pack_layer_weights,
-                               reset_dispatch_counts)
+    from femtotron_amd import (dispatch_counts, fuse_attention, fuse_boundary_ops, fused_checkpoint,
+                               pack_layer_weights, reset_dispatch_counts)
     from femtotron_amd.boundary_ops import unfuse_boundary_ops
+    from femtotron_amd.fused_attention import (attention_dispatch_counts, reset_attention_dispatch_counts,
+                                               unfuse_attention)
     from femtotron_amd.model import build_llama_model, init_llama_weights_
     from femtotron_amd.scripts.presets import get_ac_policy
     from femtotron_amd.training import apply_activation_checkpointing, remove_activation_checkpointing
@@ -519,11 +530,14 @@ def main() -> int:
     model = init_llama_weights_(model, device="cuda", dtype=torch.bfloat16, generator_device="cuda")
     packed_groups = pack_layer_weights(model)  # q/k/v and gate/up as row views of one buffer
     boundary = fuse_boundary_ops(model) if not args.stock_boundary else 0  # embedding, final norm
+    # selective AC leaves attention outside the checkpoints: run it on the kernels too
+    attn_fused = fuse_attention(model) if args.ac == "selective" and not args.stock_attention else 0
     policy = get_ac_policy(PRESETS[args.ac])
     apply_activation_checkpointing(model, policy, checkpoint_fn=fused_checkpoint)
     ids = torch.randint(0, c["vocab"], (B, S), generator=torch.Generator().manual_seed(2000)).cuda()
 
     reset_dispatch_counts()
+    reset_attention_dispatch_counts()
     log(f"fused path ({args.ac} AC): {args.warmup} warm-up + {args.steps} timed steps")
     fused_head = not args.stock_loss_head
     sec = time_steps(torch, model, ids, args.steps, args.warmup, materialize_logits=not fused_head)
@@ -531,11 +545,15 @@ def main() -> int:
     # selective: 2 norms + 1 MLP per layer, + the final norm unless fuse_boundary_ops took it
     calls_per_step = L if args.ac == "full" else 3 * L + (0 if boundary else 1)
     assert counts["fallback"] == 0 and counts["fused"] == calls_per_step * (args.steps + args.warmup), counts
+    if attn_fused:
+        acounts = attention_dispatch_counts()
+        assert acounts == {"fused": L * (args.steps + args.warmup), "fallback": 0}, acounts
     tok_s = T / sec
     log(f"fused: {sec * 1e3:.2f} ms/step, {tok_s:.0f} tokens/s")
 
     log("per-kernel HIP-event timings at the step's shapes")
-    rows, mfma = kernel_table(torch, c, args.kernel_iters, args.ac, boundary=bool(boundary))
+    rows, mfma = kernel_table(torch, c, args.kernel_iters, args.ac, boundary=bool(boundary),
+                              fused_attention=bool(attn_fused))
     for r in rows:
         r["ms_per_step"] = round(r["ms_per_launch"] * r["launches_per_step"], 4)
     dom = max(rows, key=lambda r: r["ms_per_step"])
@@ -548,6 +566,8 @@ def main() -> int:
         remove_activation_checkpointing(model)
         if boundary:
             (fuse_boundary_ops if fused else unfuse_boundary_ops)(model)
+        if attn_fused:
+            (fuse_attention if fused else unfuse_attention)(model)
         if fused:
             apply_activation_checkpointing(model, policy, checkpoint_fn=fused_checkpoint)
         else:
@@ -595,7 +615,9 @@ def main() -> int:
                    "kv_heads": c["kv"], "ffn": c["ffn"], "vocab": c["vocab"], "micro_batch": B,
                    "seq_len": S, "tokens_per_step": T,
                    "activation_checkpointing": "every layer" if args.ac == "full"
-                   else "selective: every LlamaMLP and LlamaRMSNorm",
+                   else "selective: every LlamaMLP and LlamaRMSNorm; attention outside the "
+                        + ("checkpoints on the fused kernels (fuse_attention)" if attn_fused
+                           else "checkpoints as HF's LlamaAttention"),
                    "parallelism": "single GPU (TP=PP=DP=1)"},
         "roofline": roofline,
         "fused_kernels_hbm": rows,

@@ -10,7 +10,8 @@ device then run on the hand-written gfx950 kernels of ``libfemtohip.so``.
 from .fused_checkpoint import (dispatch_counts, fused_checkpoint, last_fallback_reason,
                                reset_dispatch_counts)
 from .boundary_ops import fuse_boundary_ops
+from .fused_attention import fuse_attention
 from .weight_packing import pack_layer_weights
 
 __all__ = ["fused_checkpoint", "dispatch_counts", "reset_dispatch_counts", "last_fallback_reason",
-           "pack_layer_weights", "fuse_boundary_ops"]
+           "pack_layer_weights", "fuse_boundary_ops", "fuse_attention"]

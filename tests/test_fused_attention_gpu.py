@@ -1,0 +1,176 @@
+"""Fused attention outside the checkpoints (selective activation checkpointing).
+
+With the "llama_mlp_and_norms" preset the attention of every layer runs outside
+``checkpoint_fn``; ``fuse_attention`` gives those LlamaAttention modules a
+forward on the femtohip kernels (packed q/k/v GEMM, fh_rope, fh_attn, o GEMM).
+
+Checkers: the CPU fp32 oracle (config 1, 1e-5: loss and every gradient of the
+whole model), the reference path itself (stock HF attention, MLPs and norms
+under torch.utils.checkpoint) on the GPU in bf16 with the north star's
+tensor-level metric, and peak memory against that reference path.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import torch_llama as ot
+from tests.helpers import BF16_ATOL, BF16_RTOL, CFG1, CFG3, CFG4, llama_config, rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _model(c, layers, dtype, seed=42):
+    from femtotron_amd.model import build_llama_model, init_llama_weights_
+    return init_llama_weights_(build_llama_model(llama_config(c, layers=layers)), device=DEV,
+                               dtype=dtype, seed=seed)
+
+
+def _step(model, ids):
+    for p in model.parameters():
+        p.grad = None
+    loss = model(ids, labels=ids)["loss"]
+    loss.backward()
+    return loss.detach(), {n.replace("._checkpoint_wrapped_module", ""): p.grad
+                           for n, p in model.named_parameters()}
+
+
+def test_fused_attention_cfg1_fp32_vs_cpu_oracle():
+    """Config 1 end to end, selective policy plus fused attention: every
+    layer's attention on the kernels, loss and all grads within 1e-5 of the
+    CPU fp32 oracle."""
+    from femtotron_amd import dispatch_counts, fuse_attention, fused_checkpoint, reset_dispatch_counts
+    from femtotron_amd.fused_attention import attention_dispatch_counts, reset_attention_dispatch_counts
+    from femtotron_amd.scripts.presets import get_ac_policy
+    from femtotron_amd.training import apply_activation_checkpointing
+
+    c = CFG1
+    model = _model(c, c["layers"], torch.float32)
+    assert fuse_attention(model) == c["layers"]
+    apply_activation_checkpointing(model, get_ac_policy("llama_mlp_and_norms"), checkpoint_fn=fused_checkpoint)
+    ids = torch.randint(0, c["vocab"], (c["batch"], c["seq"]), generator=torch.Generator().manual_seed(2000))
+    reset_dispatch_counts()
+    reset_attention_dispatch_counts()
+    loss, grads = _step(model, ids.to(DEV))
+    assert dispatch_counts() == {"fused": 3 * c["layers"] + 1, "fallback": 0}
+    assert attention_dispatch_counts() == {"fused": c["layers"], "fallback": 0}
+    orc = ot.OracleLlama(vocab=c["vocab"], hidden=c["hidden"], n_layers=c["layers"], n_heads=c["heads"],
+                         n_kv=c["kv"], ffn=c["ffn"], theta=c["theta"])
+    _, oloss = orc.forward(ids, ids)
+    oloss.backward()
+    assert abs(loss.item() - oloss.item()) <= 1e-5 * abs(oloss.item())
+    for n, t in orc.named_params():
+        assert rel_err(grads[n], t.grad) < 1e-5, f"{n}: rel {rel_err(grads[n], t.grad):.3e}"
+
+
+@pytest.mark.parametrize("name,c,B,S", [("tinyllama", CFG3, 2, 1024), ("llama3-slice", CFG4, 1, 1024)])
+def test_fused_attention_bf16_matches_stock_selective(name, c, B, S):
+    """2-layer bf16 model, selective policy: fused MLPs/norms/attention vs the
+    reference path (stock HF modules, torch.utils.checkpoint).  Loss within
+    2e-2 relative, every gradient within the tensor-level metric."""
+    from femtotron_amd import fuse_attention, fused_checkpoint
+    from femtotron_amd.fused_attention import (attention_dispatch_counts, reset_attention_dispatch_counts,
+                                               unfuse_attention)
+    from femtotron_amd.scripts.presets import get_ac_policy
+    from femtotron_amd.training import apply_activation_checkpointing, remove_activation_checkpointing
+    from torch.utils.checkpoint import checkpoint
+
+    model = _model(c, 2, torch.bfloat16)
+    policy = get_ac_policy("llama_mlp_and_norms")
+    ids = torch.randint(0, c["vocab"], (B, S), generator=torch.Generator().manual_seed(2000)).to(DEV)
+    fuse_attention(model)
+    apply_activation_checkpointing(model, policy, checkpoint_fn=fused_checkpoint)
+    reset_attention_dispatch_counts()
+    loss_f, g_f = _step(model, ids)
+    assert attention_dispatch_counts() == {"fused": 2, "fallback": 0}
+    g_f = {n: g.clone() for n, g in g_f.items()}
+    remove_activation_checkpointing(model)
+    unfuse_attention(model)
+    apply_activation_checkpointing(model, policy, checkpoint_fn=checkpoint)
+    loss_r, g_r = _step(model, ids)
+    assert abs(loss_f.item() - loss_r.item()) <= BF16_RTOL * abs(loss_r.item())
+    assert g_f.keys() == g_r.keys()
+    for n in g_r:
+        a, b = g_f[n].float(), g_r[n].float()
+        err = float((a - b).abs().max())
+        lim = BF16_ATOL + BF16_RTOL * float(b.abs().max())
+        assert bool(torch.isfinite(a).all()) and err <= lim, f"{name} {n}: {err:.3e} > {lim:.3e}"
+
+
+def test_fused_attention_peak_memory_not_above_stock_selective():
+    """Peak memory of one fwd+bwd of a 2-layer TinyLlama-shaped model (B=2,
+    S=2048) under the selective policy: fused (with fuse_attention) <= the
+    reference path (stock attention, torch.utils.checkpoint)."""
+    from femtotron_amd import fuse_attention, fused_checkpoint
+    from femtotron_amd.fused_attention import unfuse_attention
+    from femtotron_amd.scripts.presets import get_ac_policy
+    from femtotron_amd.training import apply_activation_checkpointing, remove_activation_checkpointing
+    from torch.utils.checkpoint import checkpoint
+
+    c = CFG3
+    model = _model(c, 2, torch.bfloat16)
+    policy = get_ac_policy("llama_mlp_and_norms")
+    ids = torch.randint(0, c["vocab"], (2, 2048), generator=torch.Generator().manual_seed(2000)).to(DEV)
+
+    def peak(fused):
+        remove_activation_checkpointing(model)
+        (fuse_attention if fused else unfuse_attention)(model)
+        apply_activation_checkpointing(model, policy, checkpoint_fn=fused_checkpoint if fused else checkpoint)
+        for _ in range(2):  # the second pass measures, with grads already allocated
+            torch.cuda.synchronize()
+            torch.cuda.reset_peak_memory_stats()
+            base = torch.cuda.memory_allocated()
+            model(ids, labels=ids)["loss"].backward()
+            torch.cuda.synchronize()
+        return torch.cuda.max_memory_allocated() - base
+
+    p_fused = peak(True)
+    p_ref = peak(False)
+    assert p_fused <= p_ref, f"fused peak {p_fused / 2**20:.1f} MiB > reference {p_ref / 2**20:.1f} MiB"
+
+
+def test_fused_attention_falls_back_where_kernels_do_not_apply():
+    """An explicit attention mask and a hook on a projection both run the
+    module's own forward (same output as the unpatched module); under full
+    activation checkpointing the fused layer never calls the attention module."""
+    from transformers.models.llama import modeling_llama as hf
+    from femtotron_amd import dispatch_counts, fuse_attention, fused_checkpoint, reset_dispatch_counts
+    from femtotron_amd.fused_attention import (attention_dispatch_counts, last_attention_fallback_reason,
+                                               reset_attention_dispatch_counts, unfuse_attention)
+    from femtotron_amd.scripts.presets import get_ac_policy
+    from femtotron_amd.training import apply_activation_checkpointing
+
+    c = CFG1
+    model = _model(c, 1, torch.bfloat16)
+    attn = next(m for m in model.modules() if isinstance(m, hf.LlamaAttention))
+    B, S = 2, 64
+    g = torch.Generator(device=DEV).manual_seed(5)
+    y = torch.randn(B, S, c["hidden"], device=DEV, dtype=torch.bfloat16, generator=g)
+    cos, sin = model.model.rotary_emb(y, torch.arange(S, device=DEV)[None])
+    mask = torch.zeros(B, 1, S, S, device=DEV, dtype=torch.bfloat16)
+    mask.masked_fill_(torch.ones(S, S, device=DEV, dtype=torch.bool).triu(1), float("-inf"))
+    want_mask = attn(y, (cos, sin), attention_mask=mask)[0]
+    want = attn(y, (cos, sin))[0]
+    fuse_attention(model)
+    reset_attention_dispatch_counts()
+    assert torch.equal(attn(y, (cos, sin), attention_mask=mask)[0], want_mask)
+    assert last_attention_fallback_reason() == "explicit attention mask"
+    h = attn.q_proj.register_forward_hook(lambda *a: None)
+    assert torch.equal(attn(y, (cos, sin))[0], want)
+    assert last_attention_fallback_reason() == "hooks on the projections"
+    h.remove()
+    assert attention_dispatch_counts() == {"fused": 0, "fallback": 2}
+    out = attn(y, (cos, sin))[0]  # fused
+    assert attention_dispatch_counts()["fused"] == 1
+    err = float((out.float() - want.float()).abs().max())
+    assert err <= BF16_ATOL + BF16_RTOL * float(want.float().abs().max())
+    # full AC: the fused decoder layer does not call the (patched) attention module
+    apply_activation_checkpointing(model, get_ac_policy("llama_decoder_layer"), checkpoint_fn=fused_checkpoint)
+    reset_dispatch_counts()
+    reset_attention_dispatch_counts()
+    ids = torch.randint(0, c["vocab"], (B, S), generator=torch.Generator().manual_seed(1)).to(DEV)
+    model(ids, labels=ids)["loss"].backward()
+    assert dispatch_counts() == {"fused": 1, "fallback": 0}
+    assert attention_dispatch_counts() == {"fused": 0, "fallback": 0}
+    unfuse_attention(model)
