@@ -296,11 +296,14 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True,
                  achieved_tflops=round(bwd_flop / ms_b / 1e9, 1),
                  frac=round(bwd_flop / ms_b / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4))]
     # the hand-written weight-gradient GEMM, at the projections the layer routes to it
-    from femtotron_amd.fused_layer import GEMM_TN_MAX_TILES
-    for name, n_out, k_in in (("wgrad_qkv", Hq + 2 * Hkv, H), ("wgrad_o", H, Hq)):
+    from femtotron_amd.fused_layer import use_gemm_tn
+    for name, n_out, k_in in (("wgrad_qkv", Hq + 2 * Hkv, H), ("wgrad_o", H, Hq),
+                              ("wgrad_gate_up", 2 * F, H), ("wgrad_down", H, F)):
+        if sel and not fused_attention and name in ("wgrad_qkv", "wgrad_o"):
+            continue
         dy = rnd(T, n_out)
         xin = rnd(T, k_in)
-        if not ops.gemm_tn_supported(dy, xin) or (n_out // 256) * (k_in // 256) > GEMM_TN_MAX_TILES:
+        if not use_gemm_tn(dy, xin):
             continue
         ms = event_ms(torch, lambda i=0: ops.gemm_tn(dy, xin), iters)
         flop = 2 * T * n_out * k_in

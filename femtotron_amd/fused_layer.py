@@ -103,11 +103,19 @@ def layer_forward(x2: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, shp: L
 
 
 _side_streams: dict[int, torch.cuda.Stream] = {}
-# Weight gradients with at most this many 256 x 256 output tiles go to
-# fh_gemm_tn (TinyLlama: q/k/v 2560 x 2048 and o 2048 x 2048, measured 209 vs
-# 258 us and 151 vs 199 us against the tuned library GEMM); larger ones keep
-# the library GEMM, which measured faster there.
-GEMM_TN_MAX_TILES = 128
+# Weight gradients dW = dY^T X whose input X is at most this wide go to
+# fh_gemm_tn, wider ones to the tuned library GEMM.  Measured on a warm MI355X
+# against the shipped library solutions: at input width 2048 (TinyLlama's
+# q/k/v, o and gate/up) fh_gemm_tn took 175 / 143 / 760 us against 211-219 /
+# 162-168 / 846-854 us; at input width 4096 and above (the Llama-3-8B and
+# Llama-2-7B slices, and TinyLlama's down projection, input width 5632) the
+# library was as fast or faster in 10 of 11 shapes.
+GEMM_TN_MAX_INPUT = 2048
+
+
+def use_gemm_tn(dy: torch.Tensor, x: torch.Tensor) -> bool:
+    """Whether dW = dy^T x runs on fh_gemm_tn (see GEMM_TN_MAX_INPUT)."""
+    return ops.gemm_tn_supported(dy, x) and x.size(1) <= GEMM_TN_MAX_INPUT
 
 
 class _WgradStream:
@@ -130,12 +138,11 @@ class _WgradStream:
 
     def mm_tn(self, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
         """a^T @ b on the side stream: the hand-written token-split GEMM
-        (fh_gemm_tn) for outputs of at most GEMM_TN_MAX_TILES 256 x 256 tiles,
-        where the library's kernels leave most CUs idle, else the library GEMM."""
+        (fh_gemm_tn) where use_gemm_tn says it is the faster one, else the
+        library GEMM."""
         self.side.wait_stream(self.main)
         with torch.cuda.stream(self.side):
-            if (ops.gemm_tn_supported(a, b)
-                    and (a.size(1) // 256) * (b.size(1) // 256) <= GEMM_TN_MAX_TILES):
+            if use_gemm_tn(a, b):
                 out = ops.gemm_tn(a, b)
             else:
                 out = torch.mm(a.t(), b)
