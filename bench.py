@@ -95,7 +95,7 @@ def parse_args():
     ap.add_argument("--profile-kernel", default=None,
                     help="launch only this fused kernel (swiglu_fwd, swiglu_bwd, rmsnorm_fwd, "
                          "add_rmsnorm_fwd, rmsnorm_bwd, rope_fwd, residual_add, attn_fwd, attn_bwd; "
-                         "embedding_fwd, embedding_bwd; gemm_tn_qkv, gemm_tn_o (weight-gradient GEMM); "
+                         "embedding_fwd, embedding_bwd; gemm_tn_qkv, gemm_tn_o, gemm_tn_gate_up (weight-gradient GEMM); "
                          "adamw: one optimizer step over the workload's parameter shapes) at "
                          "--workload's step shape, after a 1 GiB device copy that calibrates HBM byte "
                          "counters, for rocprofv3 --pmc runs; prints one JSON line and exits")
@@ -384,8 +384,9 @@ def profile_kernel(torch, name: str, c: dict, launches: int = 10) -> dict:
             dys = [rnd(T, H) for _ in range(n)]
             fn = lambda i: ops.embedding_bwd(dys[i], ids, V)
             nbytes = 2 * T * H + 2 * V * H + 8 * T
-    elif name in ("gemm_tn_qkv", "gemm_tn_o"):
-        n_out, k_in = (Hq + 2 * Hkv, H) if name == "gemm_tn_qkv" else (H, Hq)
+    elif name in ("gemm_tn_qkv", "gemm_tn_o", "gemm_tn_gate_up"):
+        n_out, k_in = {"gemm_tn_qkv": (Hq + 2 * Hkv, H), "gemm_tn_o": (H, Hq),
+                       "gemm_tn_gate_up": (2 * F, H)}[name]
         dys = [rnd(T, n_out) for _ in range(2)]
         xs = [rnd(T, k_in) for _ in range(2)]
         fn = lambda i: ops.gemm_tn(dys[i % 2], xs[i % 2])
