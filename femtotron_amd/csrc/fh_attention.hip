@@ -492,6 +492,56 @@ struct DkdvFusedTiles {
   static constexpr int NT = 2 * NWH * 64;
 };
 
+// Direct-to-LDS variant of the Q/dO tile stream (the head_dim <= 64 dK/dV
+// kernel): each wave issues global_load_lds_dwordx4 for whole 1 KB runs of a
+// swizzled [BQ x HD] tile (lane i fills the 16-byte slot i of the run, so it
+// loads the chunk that the swizzle places there) plus, in the last wave, the
+// raw lse and delta of the tile's rows.  No registers hold the tile and no
+// vector stores write it; the caller waits for its own loads (vmcnt) before
+// the barrier that hands the stage to the other waves.  Rows past S re-read
+// row S - 1: the kernel masks their weights to zero.
+template <int HD, int BQ, int NT>
+struct QTileDma {
+  int qt = 0, hh = 0;  // the item to fetch next
+  __device__ __forceinline__ void start(int qt_end) {
+    qt = qt_end - 1;
+    hh = 0;
+  }
+  __device__ __forceinline__ void advance(int group) {
+    if (++hh == group) {
+      hh = 0;
+      --qt;
+    }
+  }
+  __device__ __forceinline__ void fetch(const uint16_t* q, int64_t ldq, const uint16_t* dO,
+                                        int64_t lddo, const float* lse, const float* delta,
+                                        int S, int qt0, int group, char* sq, char* sg, float* sl,
+                                        float* sd, int wave, int lane) {
+    typedef __attribute__((address_space(1))) const void* gptr;
+    typedef __attribute__((address_space(3))) void* lptr;
+    constexpr int CPR = HD / 8, RPW = 64 / CPR, RUNS = BQ / RPW, NW = NT / 64;
+    static_assert(BQ == 64, "one lse/delta load covers the tile's 64 rows");
+    const int qs = max(qt, qt0) * BQ;
+    const int64_t hcol = static_cast<int64_t>(hh) * HD;
+#pragma unroll
+    for (int j0 = 0; j0 < RUNS; j0 += NW) {
+      const int j = j0 + wave;  // wave-uniform
+      if (RUNS % NW == 0 || j < RUNS) {
+        const int r = j * RPW + lane / CPR, c = (lane % CPR) ^ swz<HD>(r);
+        const int64_t row = min(qs + r, S - 1);
+        __builtin_amdgcn_global_load_lds((gptr)(q + row * ldq + hcol + c * 8), (lptr)(sq + j * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((gptr)(dO + row * lddo + hcol + c * 8), (lptr)(sg + j * 1024), 16, 0, 0);
+      }
+    }
+    if (wave == NW - 1) {
+      const int64_t row = static_cast<int64_t>(hh) * S + min(qs + lane, S - 1);
+      __builtin_amdgcn_global_load_lds((gptr)(lse + row), (lptr)sl, 4, 0, 0);
+      __builtin_amdgcn_global_load_lds((gptr)(delta + row), (lptr)sd, 4, 0, 0);
+    }
+    advance(group);
+  }
+};
+
 // One wave's share of a query tile in the dK/dV kernel: the 32 queries at
 // row hrow of the LDS tiles Q and dO (first query qh) against the wave's 32
 // keys (first key kw, this lane's key ki), accumulated into dK^T and dV^T.
@@ -515,7 +565,7 @@ __device__ __forceinline__ void dkdv_tile(const char* Q, const char* G, const fl
   for (int g = 0; g < 4; ++g) {
     const float4 L4 = *reinterpret_cast<const float4*>(&sl[hrow + 8 * g + 4 * hl]);
     const float4 D4 = *reinterpret_cast<const float4*>(&sd[hrow + 8 * g + 4 * hl]);
-    const float Lv[4] = {L4.x, L4.y, L4.z, L4.w};
+    const float Lv[4] = {-L4.x * kLog2e, -L4.y * kLog2e, -L4.z * kLog2e, -L4.w * kLog2e};
     const float Dv[4] = {D4.x, D4.y, D4.z, D4.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -557,10 +607,11 @@ __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves
   constexpr int BKN = NWH * 32, BQ = DkdvFusedTiles<HD>::BQ, NS = HD / 16, ND = HD / 32;
   constexpr int TILE = BQ * 2 * HD;
   static_assert(BQ == 64 && BKN % BQ == 0, "two 32-query halves per tile; key blocks align with tiles");
-  __shared__ __align__(16) char sq[2 * TILE];
-  __shared__ __align__(16) char sg[2 * TILE];
-  __shared__ __align__(16) float slse[2][BQ];
-  __shared__ __align__(16) float sdl[2][BQ];
+  // Two LDS stages as separate arrays: the loop is unrolled by two, so every
+  // access names its stage statically and the compiler can tell that the
+  // direct-to-LDS loads into one stage do not alias the reads of the other.
+  __shared__ __align__(16) char sq0[TILE], sq1[TILE], sg0[TILE], sg1[TILE];
+  __shared__ __align__(16) float sl0[BQ], sl1[BQ], sd0[BQ], sd1[BQ];  // raw lse and delta
   __shared__ __align__(16) float xchg[2][NWH][ND * 16][64];  // [0]: dV of half 0, [1]: dK of half 1
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
@@ -603,49 +654,37 @@ __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves
     }
 
     // Iteration space: (query tiles from the key block's first key, last tile
-    // first) x (query heads of the group), n_it >= 1 items.  Two register
-    // stages take every other item: the tile of iteration it + 2 is loaded
-    // while iteration it computes and written to LDS at the end of iteration
-    // it + 1, so its global loads have two iterations to arrive.
+    // first) x (query heads of the group), n_it >= 1 items.  Item it + 1 is
+    // loaded straight into the other LDS stage while item it is multiplied;
+    // each wave waits for its own loads before the barrier that ends the item.
     const int qt0 = (jb * BKN) / BQ;
     const int n_it = group * (qt_end - qt0);
-    QTileStream<HD, BQ, NT> pa, pb;  // items 0, 2, 4, ... and 1, 3, 5, ...
-    pa.start(qt_end);
-    pb.start(qt_end);
-    pb.advance(group);
-    pa.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, tid);
-    pa.advance(group);
-    pb.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, tid);
-    pb.advance(group);
-    pa.commit(sq, sg, slse[0], sdl[0], tid);
+    QTileDma<HD, BQ, NT> pre;
+    pre.start(qt_end);
+    pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, sq0, sg0, sl0, sd0, wave, lane);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     int cqt = qt_end - 1, chh = 0;  // query tile and head of the current item
-    // One iteration: PF (free registers) fetches item IT + 2, PC (holding item
-    // IT + 1) is written to the other LDS stage once the tile is done.  The
-    // loop runs whole pairs and fetches unconditionally (items past the end
-    // are clamped reads, never used), so every path has one fetch's loads in
-    // flight at each commit.
-#define FH_DKDV_ITER(IT, PF, PC)                                                                  \
+    // Item IT from stage (QC, GC, LC, DC); item IT + 1 into stage (QN, GN, LN, DN).
+#define FH_DKDV_ITER(IT, QC, GC, LC, DC, QN, GN, LN, DN)                                          \
   {                                                                                               \
-    const int st = (IT) & 1;                                                                      \
     refresh_offsets(a_off, b0, b8);                                                               \
-    PF.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, tid);                                      \
-    PF.advance(group);                                                                            \
+    if ((IT) + 1 < n_it)                                                                          \
+      pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, QN, GN, LN, DN, wave, lane);            \
     const int qh = cqt * BQ + hrow; /* first query of this wave's half */                         \
     if ((IT) < n_it && qh + 31 >= kw) /* some query of the half reaches this wave's keys */      \
-      dkdv_tile<HD>(sq + st * TILE, sg + st * TILE, slse[st], sdl[st], kf, vf, dkacc, dvacc,     \
-                    a_off, b0, b8, hrow, qh, kw, ki, S, scale_log2, hl);                          \
-    if ((IT) + 1 < n_it)                                                                          \
-      PC.commit(sq + (st ^ 1) * TILE, sg + (st ^ 1) * TILE, slse[st ^ 1], sdl[st ^ 1], tid);      \
+      dkdv_tile<HD>(QC, GC, LC, DC, kf, vf, dkacc, dvacc, a_off, b0, b8, hrow, qh, kw, ki, S,      \
+                    scale_log2, hl);                                                              \
     if (++chh == group) {                                                                         \
       chh = 0;                                                                                    \
       --cqt;                                                                                      \
     }                                                                                             \
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");                                              \
     __syncthreads();                                                                              \
   }
     for (int it = 0; it < n_it; it += 2) {
-      FH_DKDV_ITER(it, pa, pb)
-      FH_DKDV_ITER(it + 1, pb, pa)
+      FH_DKDV_ITER(it, sq0, sg0, sl0, sd0, sq1, sg1, sl1, sd1)
+      FH_DKDV_ITER(it + 1, sq1, sg1, sl1, sd1, sq0, sg0, sl0, sd0)
     }
 #undef FH_DKDV_ITER
 
