@@ -113,9 +113,9 @@ __device__ __forceinline__ void store_rows_T(uint16_t* out_row, const f32x16 (&a
 
 // ------------------------------------------------------------ forward (bf16)
 // Block = 4 waves x (32*QT) queries of one (batch, head); loop over 64-key
-// blocks, double-buffered in LDS: the next block's K/V are loaded into
-// registers while the current one is multiplied, then written to the other
-// LDS stage; one barrier per block.  QT query tiles per wave: QT = 2 would
+// blocks, double-buffered in LDS: the next block's K/V are loaded straight
+// into the other LDS stage while the current one is multiplied (no registers
+// hold them in flight); one barrier per block.  QT query tiles per wave: QT = 2 would
 // let every K/V fragment read from LDS feed two MFMAs, but its registers cost
 // a wave of occupancy and it measured slower at head_dim 64 (342 vs 308 us at
 // the TinyLlama shape), so QT = 1.  Heaviest (latest) query blocks first.
@@ -124,6 +124,114 @@ struct FwdTiles {
   static constexpr int QT = 1;
 };
 
+// The key-block loop of the forward and dQ kernels (4 waves): block kb + 1's
+// K and V go straight into the other LDS stage (dma_tile) while
+// body(kb, K, V) multiplies block kb; each wave waits for its own loads
+// before the barrier that ends the block.  The two stages are separate
+// arrays and the loop is unrolled by two, so every access names its stage
+// and the compiler can tell that the loads into one stage do not alias the
+// reads of the other (it would otherwise wait for them before every read).
+template <int BN, int HD, class Body>
+__device__ __forceinline__ void kv_block_loop(const uint16_t* kb_ptr, int64_t ldk, const uint16_t* vb_ptr,
+                                              int64_t ldv, int nkb, int S, char* sk0, char* sk1, char* sv0,
+                                              char* sv1, int wave, int lane, Body&& body) {
+  dma_tile<BN, HD, 4>(kb_ptr, ldk, 0, S - 1, sk0, wave, lane);
+  dma_tile<BN, HD, 4>(vb_ptr, ldv, 0, S - 1, sv0, wave, lane);
+  wait_loads();
+  __syncthreads();
+  auto step = [&](int kb, const char* K, const char* V, char* KN, char* VN) __attribute__((always_inline)) {
+    if (kb + 1 < nkb) {
+      dma_tile<BN, HD, 4>(kb_ptr, ldk, (kb + 1) * BN, S - 1, KN, wave, lane);
+      dma_tile<BN, HD, 4>(vb_ptr, ldv, (kb + 1) * BN, S - 1, VN, wave, lane);
+    }
+    if (kb < nkb) body(kb, K, V);
+    wait_loads();
+    __syncthreads();
+  };
+  for (int kb = 0; kb < nkb; kb += 2) {
+    step(kb, sk0, sv0, sk1, sv1);
+    step(kb + 1, sk1, sv1, sk0, sv0);
+  }
+}
+
+// One 64-key block of the forward for one wave: raw scores from K (LDS),
+// online softmax update of (m, l, oacc), then oacc += P V (V from LDS).
+template <int HD, int QT>
+__device__ __forceinline__ void fwd_block(const char* K, const char* V, const bf16x8 (&qf)[QT][HD / 16],
+                                          f32x16 (&oacc)[QT][HD / 32], float (&m)[QT], float (&l)[QT],
+                                          int a_off, int b0, int b8, int k0, int qw, int l32, int hl,
+                                          int S, float scale_log2) {
+  constexpr int BN = 64, NS = HD / 16, ND = HD / 32;
+  f32x16 x[BN / 32][QT];  // raw scores S^T, rows = keys, column = query
+  __builtin_amdgcn_iglp_opt(0);  // LDS reads interleaved with MFMAs (head_dim 128: -3%)
+#pragma unroll
+  for (int t = 0; t < BN / 32; ++t) {
+#pragma unroll
+    for (int u = 0; u < QT; ++u) x[t][u] = zero16();
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const bf16x8 a = lds_frag<HD>(K, a_off, 32 * t, s);
+#pragma unroll
+      for (int u = 0; u < QT; ++u) x[t][u] = mfma(a, qf[u][s], x[t][u]);
+    }
+  }
+  const bool need_mask = (k0 + BN - 1 > qw) || (k0 + BN > S);
+#pragma unroll
+  for (int u = 0; u < QT; ++u) {
+    const int qi = qw + 32 * u + l32;
+    float mloc = -INFINITY;
+    if (need_mask) {  // diagonal or ragged block
+#pragma unroll
+      for (int t = 0; t < BN / 32; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int key = k0 + 32 * t + acc_row(j, hl);
+          x[t][u][j] = ((key > qi) | (key >= S)) ? -INFINITY : x[t][u][j];
+          mloc = fmaxf(mloc, x[t][u][j]);
+        }
+    } else {
+#pragma unroll
+      for (int t = 0; t < BN / 32; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) mloc = fmaxf(mloc, x[t][u][j]);
+    }
+    mloc = xor32_max(mloc) * scale_log2;
+    if (wave_any(mloc > m[u] + kRescaleSlack)) {
+      const float mnew = fmaxf(m[u], mloc);
+      const float alpha = fast_exp2(m[u] - mnew);
+      m[u] = mnew;
+      l[u] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) oacc[u][dt][j] *= alpha;
+    }
+    const float nm = -m[u];
+    float lsum = 0.f;
+#pragma unroll
+    for (int t = 0; t < BN / 32; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float p = fast_exp2(fmaf(x[t][u][j], scale_log2, nm));
+        x[t][u][j] = p;
+        lsum += p;
+      }
+    l[u] += lsum;
+  }
+#pragma unroll
+  for (int s = 0; s < BN / 16; ++s) {
+    bf16x8 pf[QT];
+#pragma unroll
+    for (int u = 0; u < QT; ++u) pf[u] = pack_frag(x[s >> 1][u], 8 * (s & 1));
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) {
+      const bf16x8 a = lds_frag_tr<HD>(V, b0, b8, 16 * s, dt);
+#pragma unroll
+      for (int u = 0; u < QT; ++u) oacc[u][dt] = mfma(a, pf[u], oacc[u][dt]);
+    }
+  }
+}
+
 template <int HD>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_fwd(
     const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
@@ -131,8 +239,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     float* __restrict__ lse, int S, int nh, int group, float scale_log2) {
   constexpr int QT = FwdTiles<HD>::QT;
   constexpr int BM = 4 * 32 * QT, BN = 64, NS = HD / 16, ND = HD / 32, TILE = BN * 2 * HD;
-  __shared__ __align__(16) char sk[2 * TILE];
-  __shared__ __align__(16) char sv[2 * TILE];
+  __shared__ __align__(16) char sk0[TILE], sk1[TILE], sv0[TILE], sv1[TILE];
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const XcdOrder ord = xcd_order();
@@ -166,98 +273,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   const int nkb = (kend + BN - 1) / BN;
   const uint16_t* kb_ptr = k + tok0 * ldk + static_cast<int64_t>(kvh) * HD;
   const uint16_t* vb_ptr = v + tok0 * ldv + static_cast<int64_t>(kvh) * HD;
-  TileRegs<BN, HD, 256> pk, pv;
-  pk.load(kb_ptr, ldk, S, tid);
-  pv.load(vb_ptr, ldv, S, tid);
-  pk.store(sk, tid);
-  pv.store(sv, tid);
-  __syncthreads();
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int k0 = kb * BN, st = kb & 1;
-    const bool more = kb + 1 < nkb;
-    refresh_offsets(a_off, b0, b8);
-    if (more) {
-      pk.load(kb_ptr + static_cast<int64_t>(k0 + BN) * ldk, ldk, S - k0 - BN, tid);
-      pv.load(vb_ptr + static_cast<int64_t>(k0 + BN) * ldv, ldv, S - k0 - BN, tid);
-    }
-    if (k0 <= qw + 32 * QT - 1) {  // some key of the block precedes some query of the wave
-      const char* K = sk + st * TILE;
-      const char* V = sv + st * TILE;
-      f32x16 x[BN / 32][QT];  // raw scores S^T, rows = keys, column = query
-      __builtin_amdgcn_iglp_opt(0);  // LDS reads interleaved with MFMAs (head_dim 128: -3%)
-#pragma unroll
-      for (int t = 0; t < BN / 32; ++t) {
-#pragma unroll
-        for (int u = 0; u < QT; ++u) x[t][u] = zero16();
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          const bf16x8 a = lds_frag<HD>(K, a_off, 32 * t, s);
-#pragma unroll
-          for (int u = 0; u < QT; ++u) x[t][u] = mfma(a, qf[u][s], x[t][u]);
-        }
-      }
-      const bool need_mask = (k0 + BN - 1 > qw) || (k0 + BN > S);
-#pragma unroll
-      for (int u = 0; u < QT; ++u) {
-        const int qi = qw + 32 * u + l32;
-        float mloc = -INFINITY;
-        if (need_mask) {  // diagonal or ragged block
-#pragma unroll
-          for (int t = 0; t < BN / 32; ++t)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-              const int key = k0 + 32 * t + acc_row(j, hl);
-              x[t][u][j] = ((key > qi) | (key >= S)) ? -INFINITY : x[t][u][j];
-              mloc = fmaxf(mloc, x[t][u][j]);
-            }
-        } else {
-#pragma unroll
-          for (int t = 0; t < BN / 32; ++t)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) mloc = fmaxf(mloc, x[t][u][j]);
-        }
-        mloc = xor32_max(mloc) * scale_log2;
-        if (wave_any(mloc > m[u] + kRescaleSlack)) {
-          const float mnew = fmaxf(m[u], mloc);
-          const float alpha = fast_exp2(m[u] - mnew);
-          m[u] = mnew;
-          l[u] *= alpha;
-#pragma unroll
-          for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) oacc[u][dt][j] *= alpha;
-        }
-        const float nm = -m[u];
-        float lsum = 0.f;
-#pragma unroll
-        for (int t = 0; t < BN / 32; ++t)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const float p = fast_exp2(fmaf(x[t][u][j], scale_log2, nm));
-            x[t][u][j] = p;
-            lsum += p;
-          }
-        l[u] += lsum;
-      }
-#pragma unroll
-      for (int s = 0; s < BN / 16; ++s) {
-        bf16x8 pf[QT];
-#pragma unroll
-        for (int u = 0; u < QT; ++u) pf[u] = pack_frag(x[s >> 1][u], 8 * (s & 1));
-#pragma unroll
-        for (int dt = 0; dt < ND; ++dt) {
-          const bf16x8 a = lds_frag_tr<HD>(V, b0, b8, 16 * s, dt);
-#pragma unroll
-          for (int u = 0; u < QT; ++u) oacc[u][dt] = mfma(a, pf[u], oacc[u][dt]);
-        }
-      }
-    }
-    if (more) {
-      pk.store(sk + (st ^ 1) * TILE, tid);
-      pv.store(sv + (st ^ 1) * TILE, tid);
-    }
-    __syncthreads();
-  }
+  kv_block_loop<BN, HD>(kb_ptr, ldk, vb_ptr, ldv, nkb, S, sk0, sk1, sv0, sv1, wave, lane,
+                        [&](int kb, const char* K, const char* V) __attribute__((always_inline)) {
+                          refresh_offsets(a_off, b0, b8);
+                          const int k0 = kb * BN;
+                          if (k0 <= qw + 32 * QT - 1)  // some key of the block precedes some query of the wave
+                            fwd_block<HD, QT>(K, V, qf, oacc, m, l, a_off, b0, b8, k0, qw, l32, hl, S,
+                                              scale_log2);
+                        });
 #pragma unroll
   for (int u = 0; u < QT; ++u) {
     const int qi = qw + 32 * u + l32;
@@ -301,6 +324,43 @@ __global__ __launch_bounds__(256) void k_attn_delta(const T* __restrict__ o, int
 // The prologue also forms delta = rowsum(dO * O) of its queries (the lane
 // holds half of each row; one exchange with lane i^32 completes it) and
 // stores it for the dK/dV kernel, which runs next on the same stream.
+// One 64-key block of the dQ kernel for one wave (query qi = qw + lane % 32).
+template <int HD>
+__device__ __forceinline__ void dq_block(const char* K, const char* V, const bf16x8 (&qf)[HD / 16],
+                                         const bf16x8 (&gf)[HD / 16], f32x16 (&dqacc)[HD / 32], float nlse2,
+                                         float dl, int a_off, int b0, int b8, int k0, int qw, int qi, int hl,
+                                         int S, float scale_log2) {
+  constexpr int BN = 64, NS = HD / 16, ND = HD / 32;
+  const bool need_mask = (k0 + BN - 1 > qw) || (k0 + BN > S);
+#pragma unroll
+  for (int t = 0; t < BN / 32; ++t) {
+    f32x16 x = zero16(), y = zero16();  // S^T, dP^T
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      x = mfma(lds_frag<HD>(K, a_off, 32 * t, s), qf[s], x);
+      y = mfma(lds_frag<HD>(V, a_off, 32 * t, s), gf[s], y);
+    }
+    if (need_mask) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int key = k0 + 32 * t + acc_row(j, hl);
+        const float p = fast_exp2(fmaf(x[j], scale_log2, nlse2));
+        x[j] = ((key > qi) | (key >= S)) ? 0.f : p * (y[j] - dl);  // dS^T
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) x[j] = fast_exp2(fmaf(x[j], scale_log2, nlse2)) * (y[j] - dl);
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const bf16x8 df = pack_frag(x, 8 * s2);
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt)
+        dqacc[dt] = mfma(lds_frag_tr<HD>(K, b0, b8, 32 * t + 16 * s2, dt), df, dqacc[dt]);
+    }
+  }
+}
+
 template <int HD>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_bwd_dq(
     const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
@@ -309,8 +369,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     float* __restrict__ delta, uint16_t* __restrict__ dq, int64_t lddq, int S, int nh, int group,
     float scale_log2, float scale) {
   constexpr int BM = 128, BN = 64, NS = HD / 16, ND = HD / 32, TILE = BN * 2 * HD;
-  __shared__ __align__(16) char sk[2 * TILE];
-  __shared__ __align__(16) char sv[2 * TILE];
+  __shared__ __align__(16) char sk0[TILE], sk1[TILE], sv0[TILE], sv1[TILE];
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const XcdOrder ord = xcd_order();
@@ -359,58 +418,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   const int nkb = (kend + BN - 1) / BN;
   const uint16_t* kb_ptr = k + tok0 * ldk + static_cast<int64_t>(kvh) * HD;
   const uint16_t* vb_ptr = v + tok0 * ldv + static_cast<int64_t>(kvh) * HD;
-  TileRegs<BN, HD, 256> pk, pv;
-  pk.load(kb_ptr, ldk, S, tid);
-  pv.load(vb_ptr, ldv, S, tid);
-  pk.store(sk, tid);
-  pv.store(sv, tid);
-  __syncthreads();
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int k0 = kb * BN, st = kb & 1;
-    const bool more = kb + 1 < nkb;
-    refresh_offsets(a_off, b0, b8);
-    if (more) {
-      pk.load(kb_ptr + static_cast<int64_t>(k0 + BN) * ldk, ldk, S - k0 - BN, tid);
-      pv.load(vb_ptr + static_cast<int64_t>(k0 + BN) * ldv, ldv, S - k0 - BN, tid);
-    }
-    if (k0 <= qw + 31) {
-      const char* K = sk + st * TILE;
-      const char* V = sv + st * TILE;
-      const bool need_mask = (k0 + BN - 1 > qw) || (k0 + BN > S);
-#pragma unroll
-      for (int t = 0; t < BN / 32; ++t) {
-        f32x16 x = zero16(), y = zero16();  // S^T, dP^T
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          x = mfma(lds_frag<HD>(K, a_off, 32 * t, s), qf[s], x);
-          y = mfma(lds_frag<HD>(V, a_off, 32 * t, s), gf[s], y);
-        }
-        if (need_mask) {
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int key = k0 + 32 * t + acc_row(j, hl);
-            const float p = fast_exp2(fmaf(x[j], scale_log2, nlse2));
-            x[j] = ((key > qi) | (key >= S)) ? 0.f : p * (y[j] - dl);  // dS^T
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < 16; ++j) x[j] = fast_exp2(fmaf(x[j], scale_log2, nlse2)) * (y[j] - dl);
-        }
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          const bf16x8 df = pack_frag(x, 8 * s2);
-#pragma unroll
-          for (int dt = 0; dt < ND; ++dt)
-            dqacc[dt] = mfma(lds_frag_tr<HD>(K, b0, b8, 32 * t + 16 * s2, dt), df, dqacc[dt]);
-        }
-      }
-    }
-    if (more) {
-      pk.store(sk + (st ^ 1) * TILE, tid);
-      pv.store(sv + (st ^ 1) * TILE, tid);
-    }
-    __syncthreads();
-  }
+  kv_block_loop<BN, HD>(kb_ptr, ldk, vb_ptr, ldv, nkb, S, sk0, sk1, sv0, sv1, wave, lane,
+                        [&](int kb, const char* K, const char* V) __attribute__((always_inline)) {
+                          refresh_offsets(a_off, b0, b8);
+                          const int k0 = kb * BN;
+                          if (k0 <= qw + 31)
+                            dq_block<HD>(K, V, qf, gf, dqacc, nlse2, dl, a_off, b0, b8, k0, qw, qi, hl, S,
+                                         scale_log2);
+                        });
   if (qi < S) store_rows_T<HD>(dq + (tok0 + qi) * lddq + static_cast<int64_t>(h) * HD, dqacc, scale, hl);
 }
 
@@ -519,20 +534,12 @@ struct QTileDma {
                                         float* sd, int wave, int lane) {
     typedef __attribute__((address_space(1))) const void* gptr;
     typedef __attribute__((address_space(3))) void* lptr;
-    constexpr int CPR = HD / 8, RPW = 64 / CPR, RUNS = BQ / RPW, NW = NT / 64;
+    constexpr int NW = NT / 64;
     static_assert(BQ == 64, "one lse/delta load covers the tile's 64 rows");
     const int qs = max(qt, qt0) * BQ;
     const int64_t hcol = static_cast<int64_t>(hh) * HD;
-#pragma unroll
-    for (int j0 = 0; j0 < RUNS; j0 += NW) {
-      const int j = j0 + wave;  // wave-uniform
-      if (RUNS % NW == 0 || j < RUNS) {
-        const int r = j * RPW + lane / CPR, c = (lane % CPR) ^ swz<HD>(r);
-        const int64_t row = min(qs + r, S - 1);
-        __builtin_amdgcn_global_load_lds((gptr)(q + row * ldq + hcol + c * 8), (lptr)(sq + j * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((gptr)(dO + row * lddo + hcol + c * 8), (lptr)(sg + j * 1024), 16, 0, 0);
-      }
-    }
+    dma_tile<BQ, HD, NW>(q + hcol, ldq, qs, S - 1, sq, wave, lane);
+    dma_tile<BQ, HD, NW>(dO + hcol, lddo, qs, S - 1, sg, wave, lane);
     if (wave == NW - 1) {
       const int64_t row = static_cast<int64_t>(hh) * S + min(qs + lane, S - 1);
       __builtin_amdgcn_global_load_lds((gptr)(lse + row), (lptr)sl, 4, 0, 0);
@@ -662,7 +669,7 @@ __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves
     QTileDma<HD, BQ, NT> pre;
     pre.start(qt_end);
     pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, sq0, sg0, sl0, sd0, wave, lane);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    wait_loads();
     __syncthreads();
     int cqt = qt_end - 1, chh = 0;  // query tile and head of the current item
     // Item IT from stage (QC, GC, LC, DC); item IT + 1 into stage (QN, GN, LN, DN).
@@ -679,7 +686,7 @@ __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves
       chh = 0;                                                                                    \
       --cqt;                                                                                      \
     }                                                                                             \
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");                                              \
+    wait_loads();                                              \
     __syncthreads();                                                                              \
   }
     for (int it = 0; it < n_it; it += 2) {

@@ -157,5 +157,34 @@ struct TileRegs {
   }
 };
 
+// Direct-to-LDS load of rows r0 .. r0+ROWS-1 of a bf16 [*, HD] matrix (row
+// stride ld elements) into a swizzled [ROWS x HD] LDS tile, shared by the NW
+// waves of a block: each global_load_lds_dwordx4 fills one 1 KB run of the
+// tile (RPR consecutive rows), lane i its 16-byte slot i, so the lane reads
+// the global chunk that the swizzle stores in that slot.  Rows past `last`
+// re-read row `last`.  The LDS writes complete asynchronously: each wave
+// waits for its own loads (s_waitcnt vmcnt) before the barrier that hands
+// the tile to the other waves.
+template <int ROWS, int HD, int NW>
+__device__ __forceinline__ void dma_tile(const uint16_t* src, int64_t ld, int r0, int last, char* dst,
+                                         int wave, int lane) {
+  typedef __attribute__((address_space(1))) const void* gptr;
+  typedef __attribute__((address_space(3))) void* lptr;
+  constexpr int CPR = HD / 8, RPR = 64 / CPR, RUNS = ROWS / RPR;
+  static_assert(64 % CPR == 0 && ROWS % RPR == 0, "the tile is whole 1 KB runs");
+#pragma unroll
+  for (int j0 = 0; j0 < RUNS; j0 += NW) {
+    const int j = j0 + wave;  // wave-uniform
+    if (RUNS % NW == 0 || j < RUNS) {
+      const int r = j * RPR + lane / CPR, c = (lane % CPR) ^ swz<HD>(r);
+      const int64_t row = min(r0 + r, last);
+      __builtin_amdgcn_global_load_lds((gptr)(src + row * ld + c * 8), (lptr)(dst + j * 1024), 16, 0, 0);
+    }
+  }
+}
+
+// Waits for this wave's outstanding global loads, including direct-to-LDS ones.
+__device__ __forceinline__ void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 }  // namespace
 }  // namespace fh
