@@ -429,92 +429,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   if (qi < S) store_rows_T<HD>(dq + (tok0 + qi) * lddq + static_cast<int64_t>(h) * HD, dqacc, scale, hl);
 }
 
-// Prefetch stage of the dK/dV kernels: the Q and dO tiles, lse and delta of
-// one (query tile, query head) item of the loop.  Items run from the last
-// query tile down to the key block's first (qt0), and over the group's query
-// heads within a tile: all blocks of one kv head start at the same tile and
-// move down together, so a tile loaded by one block is found in L2 by the
-// others.  q, dO, lse, delta point at the group's first query head;
-// lse/delta rows are [head][S].  fetch() is branch-free: every thread issues
-// the same loads, rows past S and tiles past the last item are clamped in
-// bounds (so it may run past the end), and every check and all arithmetic on
-// the loaded values wait for commit().  Arithmetic on a loaded value inside
-// fetch() would make the wave wait at once for all of this fetch's loads,
-// tile included, and a branch around a load would make the compiler wait for
-// every load in flight before the next commit().
-template <int HD, int BQ, int NT>
-struct QTileStream {
-  TileRegs<BQ, HD, NT> pq, pg;
-  float pl = 0.f, pd = 0.f;  // lse and delta of query row tid % BQ of the tile in flight
-  int valid = 0;             // rows of the tile in flight inside the sequence (>= 1)
-  int qt = 0, hh = 0;        // the item to fetch next
-  __device__ __forceinline__ void start(int qt_end) {
-    qt = qt_end - 1;
-    hh = 0;
-  }
-  __device__ __forceinline__ void fetch(const uint16_t* q, int64_t ldq, const uint16_t* dO,
-                                        int64_t lddo, const float* lse, const float* delta,
-                                        int S, int qt0, int group, int tid) {
-    const int qs = max(qt, qt0) * BQ;
-    const int64_t hcol = static_cast<int64_t>(hh) * HD;
-    valid = S - qs;
-    pq.load_clamped(q + static_cast<int64_t>(qs) * ldq + hcol, ldq, valid, tid);
-    pg.load_clamped(dO + static_cast<int64_t>(qs) * lddo + hcol, lddo, valid, tid);
-    const int64_t row = static_cast<int64_t>(hh) * S + min(qs + tid % BQ, S - 1);
-    pl = lse[row];
-    pd = delta[row];
-    advance(group);
-  }
-  // Steps to the next item without loading it.
-  __device__ __forceinline__ void advance(int group) {
-    if (++hh == group) {
-      hh = 0;
-      --qt;
-    }
-  }
-  __device__ __forceinline__ void commit(char* sq, char* sg, float* slse, float* sdl, int tid) const {
-    pq.store_valid(sq, valid, tid);
-    pg.store_valid(sg, valid, tid);
-    if (tid < BQ) {
-      const bool ok = tid < valid;
-      slse[tid] = ok ? -pl * kLog2e : 0.f;  // exp2 argument offset: -lse * log2(e)
-      sdl[tid] = ok ? pd : 0.f;
-    }
-  }
-};
-
-// ------------------------------------------ backward: dK, dV (bf16), fused roles
-// Used for head_dim <= 64.  Block = 8 waves for one (batch, kv head) and two
-// key blocks of 128 keys, j and nkb-1-j, taken one after the other (causal
-// work per key block grows with the number of later queries, so every block
-// carries the same work).  Within a key block, wave w holds K and V of keys
-// 32*(w%4)..+31 in registers, and each 64-query tile is split between the two
-// halves of the block: waves 0-3 take its queries 0-31, waves 4-7 queries
-// 32-63.  So all 8 waves (two per SIMD) are busy in every iteration, and every
-// block runs the same number of iterations.  The loop runs over the group's
-// query heads and 64-query tiles (double-buffered in LDS, prefetched through
-// registers):
-//   S = Q K^T, P = exp(S - lse), dP = dO V^T, dS = P (dP - delta),
-//   dV^T += dO^T P,  dK^T += Q^T dS,  dK = scale * dK.
-// At the end of a key block the halves' partial dK and dV are exchanged
-// through LDS and summed in a fixed order (half 0 + half 1): half 0 stores dK,
-// half 1 stores dV.  Each kv head's gradient is complete inside one block: no
-// atomics.
-template <int HD>
-struct DkdvFusedTiles {
-  static constexpr int BQ = 64;
-  static constexpr int NWH = 4;  // waves per query half (32 keys each)
-  static constexpr int NT = 2 * NWH * 64;
-};
-
-// Direct-to-LDS variant of the Q/dO tile stream (the head_dim <= 64 dK/dV
-// kernel): each wave issues global_load_lds_dwordx4 for whole 1 KB runs of a
-// swizzled [BQ x HD] tile (lane i fills the 16-byte slot i of the run, so it
-// loads the chunk that the swizzle places there) plus, in the last wave, the
-// raw lse and delta of the tile's rows.  No registers hold the tile and no
-// vector stores write it; the caller waits for its own loads (vmcnt) before
-// the barrier that hands the stage to the other waves.  Rows past S re-read
-// row S - 1: the kernel masks their weights to zero.
+// Load stage of the dK/dV kernels: the Q and dO tiles, lse and delta of one
+// (query tile, query head) item of the loop, loaded straight into an LDS
+// stage.  Items run from the last query tile down to the key block's first
+// (qt0), and over the group's query heads within a tile: all blocks of one kv
+// head start at the same tile and move down together, so a tile loaded by one
+// block is found in L2 by the others.  q, dO, lse, delta point at the group's
+// first query head; lse/delta rows are [head][S].  The tiles go through
+// dma_tile; the last wave loads the raw lse and delta of 64 rows from the
+// tile's first (sl and sd hold 64 floats; rows from BQ on are unused).  Rows
+// past S re-read row S - 1: the kernels mask their weights to zero.  No
+// registers hold the tiles; the caller waits for its own loads (vmcnt) before
+// the barrier that hands the stage to the other waves.
 template <int HD, int BQ, int NT>
 struct QTileDma {
   int qt = 0, hh = 0;  // the item to fetch next
@@ -535,7 +461,7 @@ struct QTileDma {
     typedef __attribute__((address_space(1))) const void* gptr;
     typedef __attribute__((address_space(3))) void* lptr;
     constexpr int NW = NT / 64;
-    static_assert(BQ == 64, "one lse/delta load covers the tile's 64 rows");
+    static_assert(BQ <= 64, "one lse/delta load covers the tile's rows");
     const int qs = max(qt, qt0) * BQ;
     const int64_t hcol = static_cast<int64_t>(hh) * HD;
     dma_tile<BQ, HD, NW>(q + hcol, ldq, qs, S - 1, sq, wave, lane);
@@ -548,6 +474,31 @@ struct QTileDma {
     advance(group);
   }
 };
+
+// ------------------------------------------ backward: dK, dV (bf16), fused roles
+// Used for head_dim <= 64.  Block = 8 waves for one (batch, kv head) and two
+// key blocks of 128 keys, j and nkb-1-j, taken one after the other (causal
+// work per key block grows with the number of later queries, so every block
+// carries the same work).  Within a key block, wave w holds K and V of keys
+// 32*(w%4)..+31 in registers, and each 64-query tile is split between the two
+// halves of the block: waves 0-3 take its queries 0-31, waves 4-7 queries
+// 32-63.  So all 8 waves (two per SIMD) are busy in every iteration, and every
+// block runs the same number of iterations.  The loop runs over the group's
+// query heads and 64-query tiles (double-buffered in LDS, loaded straight
+// into it):
+//   S = Q K^T, P = exp(S - lse), dP = dO V^T, dS = P (dP - delta),
+//   dV^T += dO^T P,  dK^T += Q^T dS,  dK = scale * dK.
+// At the end of a key block the halves' partial dK and dV are exchanged
+// through LDS and summed in a fixed order (half 0 + half 1): half 0 stores dK,
+// half 1 stores dV.  Each kv head's gradient is complete inside one block: no
+// atomics.
+template <int HD>
+struct DkdvFusedTiles {
+  static constexpr int BQ = 64;
+  static constexpr int NWH = 4;  // waves per query half (32 keys each)
+  static constexpr int NT = 2 * NWH * 64;
+};
+
 
 // One wave's share of a query tile in the dK/dV kernel: the 32 queries at
 // row hrow of the LDS tiles Q and dO (first query qh) against the wave's 32
@@ -732,7 +683,7 @@ __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves
 // (A) and dP (B), phase 2 the two accumulating products; both roles issue the
 // same number of MFMAs in each phase.  The loop runs over the GQA group's query
 // heads and the BQ-query tiles at or after the block's first key (Q, dO, lse
-// and delta double-buffered in LDS, prefetched through registers), so each kv
+// and delta double-buffered in LDS, loaded straight into it), so each kv
 // head's gradient is complete inside one block: no atomics.  Blocks are
 // numbered heaviest (earliest keys, most causal work) first.
 template <int HD>
@@ -751,10 +702,14 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) __attribute__((amdgpu_waves_per_
     float scale_log2, float scale) {
   constexpr int NKS = DkdvTiles<HD>::NKS, NT = DkdvTiles<HD>::NT, BQ = DkdvTiles<HD>::BQ;
   constexpr int BKN = NKS * 32, NS = HD / 16, ND = HD / 32, NQT = BQ / 32, TILE = BQ * 2 * HD;
-  __shared__ __align__(16) char sq[2 * TILE];
-  __shared__ __align__(16) char sg[2 * TILE];
-  __shared__ __align__(16) float slse[2][BQ];
-  __shared__ __align__(16) float sdl[2][BQ];
+  // Two LDS stages as separate arrays (the loop below is unrolled by two),
+  // each the Q tile followed by the dO tile: a role picks its tile by offset
+  // within the stage's array, so the compiler still knows which array each
+  // read touches (with a pointer chosen between two arrays it would wait for
+  // every load in flight first).  lse and delta rows are loaded 64 at a time;
+  // rows from BQ on are unused.
+  __shared__ __align__(16) char st0[2 * TILE], st1[2 * TILE];
+  __shared__ __align__(16) float sl0[64], sl1[64], sd0[64], sd1[64];  // raw lse and delta
   __shared__ __align__(16) float sp[NKS][NQT][16 * 64];  // P of each sub-tile, [j/4][lane][4]
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
@@ -787,29 +742,26 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) __attribute__((amdgpu_waves_per_
   const uint16_t* gg = dO + tok0 * lddo + h0 * HD;
   const float* lg = lse + (static_cast<int64_t>(b) * nh + h0) * S;
   const float* dg = delta + (static_cast<int64_t>(b) * nh + h0) * S;
-  QTileStream<HD, BQ, NT> pre;
+  QTileDma<HD, BQ, NT> pre;
   pre.start(qt_end);
-  if (n_it > 0) {
-    pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, tid);
-    pre.commit(sq, sg, slse[0], sdl[0], tid);
-  }
+  if (n_it > 0) pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, st0, st0 + TILE, sl0, sd0, wave, lane);
+  wait_loads();
   __syncthreads();
   int cqt = qt_end - 1, chh = 0;  // query tile and head of the current item
-  for (int it = 0; it < n_it; ++it) {
-    const int st = it & 1;
-    const bool more = it + 1 < n_it;
+  const int xoff = role_a ? 0 : TILE;  // phase 1 reads Q (A) or dO (B), phase 2 the other
+  // Item it from stage (T, L, D) while item it + 1 is loaded into stage (TN, LN, DN).
+  auto step = [&](int it, const char* T, const float* L, const float* D, char* TN, float* LN, float* DN)
+                  __attribute__((always_inline)) {
     refresh_offsets(a_off, b0, b8);
-    pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, tid);  // past the end: clamped, unused
+    if (it + 1 < n_it) pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, TN, TN + TILE, LN, DN, wave, lane);
     const int q0 = cqt * BQ;
     // some query of the tile reaches this sub-tile's keys (same answer for both roles)
-    const bool active = kw < S && q0 + BQ - 1 >= kw;
+    const bool active = it < n_it && kw < S && q0 + BQ - 1 >= kw;
     const bool need_mask = (q0 < kw + 31) || (q0 + BQ > S) || (kw + 32 > S);
-    const char* Q = sq + st * TILE;
-    const char* G = sg + st * TILE;
     f32x16 x[NQT];  // S then P (role A) / dP then dS (role B), rows = queries, column = key ki
-    // phase 1: S (A) or dP (B)
+    // phase 1: S = Q K^T, P = exp(S - lse) -> LDS (A) or dP = dO V^T (B)
     if (active) {
-      const char* X = role_a ? Q : G;
+      const char* X = T + xoff;
 #pragma unroll
       for (int u = 0; u < NQT; ++u) {
         x[u] = zero16();
@@ -821,12 +773,12 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) __attribute__((amdgpu_waves_per_
         for (int u = 0; u < NQT; ++u) {
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
-            const float4 L4 = *reinterpret_cast<const float4*>(&slse[st][32 * u + 8 * g + 4 * hl]);
-            const float Lv[4] = {L4.x, L4.y, L4.z, L4.w};
+            const float4 L4 = *reinterpret_cast<const float4*>(&L[32 * u + 8 * g + 4 * hl]);
+            const float Lv[4] = {-L4.x * kLog2e, -L4.y * kLog2e, -L4.z * kLog2e, -L4.w * kLog2e};
 #pragma unroll
             for (int e = 0; e < 4; ++e) x[u][4 * g + e] = fast_exp2(fmaf(x[u][4 * g + e], scale_log2, Lv[e]));
           }
-          if (need_mask) {
+          if (need_mask) {  // also zeroes the rows past S (their Q/dO rows repeat row S - 1)
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
               const int qa = q0 + 32 * u + acc_row(j, hl);
@@ -840,7 +792,7 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) __attribute__((amdgpu_waves_per_
         }
       }
     }
-    __syncthreads();
+    lds_barrier();  // P is in LDS; the loads into the other stage may still be in flight
     // phase 2: dV^T += dO^T P (A) or dS = P (dP - delta), dK^T += Q^T dS (B)
     if (active) {
       if (!role_a) {
@@ -848,7 +800,7 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) __attribute__((amdgpu_waves_per_
         for (int u = 0; u < NQT; ++u)
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
-            const float4 D4 = *reinterpret_cast<const float4*>(&sdl[st][32 * u + 8 * g + 4 * hl]);
+            const float4 D4 = *reinterpret_cast<const float4*>(&D[32 * u + 8 * g + 4 * hl]);
             const float4 P4 = *reinterpret_cast<const float4*>(&sp[sub][u][(g * 64 + lane) * 4]);
             const float Dv[4] = {D4.x, D4.y, D4.z, D4.w};
             const float Pv[4] = {P4.x, P4.y, P4.z, P4.w};
@@ -856,7 +808,7 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) __attribute__((amdgpu_waves_per_
             for (int e = 0; e < 4; ++e) x[u][4 * g + e] = Pv[e] * (x[u][4 * g + e] - Dv[e]);
           }
       }
-      const char* Y = role_a ? G : Q;
+      const char* Y = T + (TILE - xoff);
 #pragma unroll
       for (int u = 0; u < NQT; ++u)
 #pragma unroll
@@ -867,12 +819,16 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) __attribute__((amdgpu_waves_per_
             acc[dt] = mfma(lds_frag_tr<HD>(Y, b0, b8, 32 * u + 16 * s2, dt), f, acc[dt]);
         }
     }
-    if (more) pre.commit(sq + (st ^ 1) * TILE, sg + (st ^ 1) * TILE, slse[st ^ 1], sdl[st ^ 1], tid);
     if (++chh == group) {
       chh = 0;
       --cqt;
     }
+    wait_loads();
     __syncthreads();
+  };
+  for (int it = 0; it < n_it; it += 2) {
+    step(it, st0, sl0, sd0, st1, sl1, sd1);
+    step(it + 1, st1, sl1, sd1, st0, sl0, sd0);
   }
   if (ki < S) {
     if (role_a)

@@ -132,29 +132,6 @@ struct TileRegs {
       if (CHUNKS % NT == 0 || tid + i * NT < CHUNKS)
         *reinterpret_cast<uint4*>(p + i * RPP * (2 * HD)) = r[i];
   }
-  // Branch-free pair for software pipelines: every thread issues the same N
-  // loads whatever `valid` is (1 <= valid; rows at or beyond it re-read row
-  // valid - 1, threads past the tile re-read a chunk of it), so every path
-  // has the same loads in flight and the compiler waits for exactly one
-  // stage's loads before a store_valid().  store_valid() writes zeros for
-  // the rows at or beyond valid.
-  __device__ __forceinline__ void load_clamped(const uint16_t* src, int64_t ld, int valid, int tid) {
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      const int c = CHUNKS % NT == 0 ? tid + i * NT : (tid + i * NT) % CHUNKS;
-      const int row = min(c / CPR, valid - 1);
-      r[i] = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(row) * ld + (c % CPR) * 8);
-    }
-  }
-  __device__ __forceinline__ void store_valid(char* tile, int valid, int tid) const {
-    const int row = tid / CPR, ch = tid % CPR;
-    char* p = tile + row * (2 * HD) + ((ch ^ swz<HD>(row)) << 4);
-#pragma unroll
-    for (int i = 0; i < N; ++i)
-      if (CHUNKS % NT == 0 || tid + i * NT < CHUNKS)
-        *reinterpret_cast<uint4*>(p + i * RPP * (2 * HD)) =
-            row + i * RPP < valid ? r[i] : make_uint4(0, 0, 0, 0);
-  }
 };
 
 // Direct-to-LDS load of rows r0 .. r0+ROWS-1 of a bf16 [*, HD] matrix (row
@@ -185,6 +162,12 @@ __device__ __forceinline__ void dma_tile(const uint16_t* src, int64_t ld, int r0
 
 // Waits for this wave's outstanding global loads, including direct-to-LDS ones.
 __device__ __forceinline__ void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Barrier for LDS data written with ds_write: waits for this wave's LDS
+// operations only, not for direct-to-LDS loads still in flight into another
+// buffer (a __syncthreads() would wait for those too: its workgroup release
+// covers every pending LDS write).  Also a compiler barrier for memory.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 }  // namespace
 }  // namespace fh
