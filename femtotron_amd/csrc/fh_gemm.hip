@@ -11,7 +11,8 @@
 // Tiles: a 256 x 256 block of C per workgroup of 16 waves (4 per SIMD, so
 // memory latency is hidden across waves); each wave holds 64 (m) x 64 (n) as
 // 2 x 2 MFMA 32x32 accumulators.  Stages of 64 tokens of
-// A and B go through LDS (double-buffered, prefetched through registers), each
+// A and B go through LDS (double-buffered, loaded straight into it with
+// global_load_lds: stage s + 1 is in flight while stage s is multiplied), each
 // 256-wide operand stored as four swizzled [64 x 64] sub-tiles.  Both MFMA
 // operands have K (the token) down the tile rows and are read with
 // ds_read_b64_tr_b16 transpose reads in the same permuted K order, so their
@@ -38,7 +39,10 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(4)
     const uint16_t* __restrict__ a, int64_t lda, const uint16_t* __restrict__ b, int64_t ldb,
     uint16_t* __restrict__ c, int64_t ldc, float* __restrict__ part, int m, int n,
     int steps_per_slice, int total_steps, int tiles_m, int tiles_n) {
-  __shared__ __align__(16) char smem[2 * kStageBytes];  // 2 stages x (4 A sub-tiles, 4 B sub-tiles)
+  // Two stages (4 A sub-tiles, then 4 B sub-tiles) as separate arrays: the
+  // loop is unrolled by two, so every access names its stage and the
+  // compiler can tell the loads into one stage from the reads of the other.
+  __shared__ __align__(16) char smem0[kStageBytes], smem1[kStageBytes];
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 3, wn = wave >> 2;  // wave tile: m in [64 wm, +64), n in [64 wn, +64)
@@ -56,30 +60,17 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(4)
   const int s_end = min(total_steps, s_begin + steps_per_slice);
   int b0 = lane_off_b<kSub>(lane, 0), b8 = lane_off_b<kSub>(lane, 8);
 
-  // Staging: threads 0..511 carry the four A sub-tiles of a stage, 512..1023
-  // the four B sub-tiles, one 16-byte chunk of each.
-  const bool op_b = tid >= kGemmThreads / 2;
-  const int ltid = tid & (kGemmThreads / 2 - 1);
-  const uint16_t* src = op_b ? b + n0 : a + m0;
+  // Loads: wave w fills sub-tile w / 2 of a stage (A: 0-3, B: 4-7), half of
+  // its eight 1 KB runs each (dma_tile with two waves per sub-tile).
+  const int lsub = wave >> 1;
+  const bool op_b = lsub >= kTm / kSub;
+  const uint16_t* src = (op_b ? b + n0 : a + m0) + (lsub & 3) * kSub;
   const int64_t ld = op_b ? ldb : lda;
-  const int lds_op = op_b ? (kTm / kSub) * kSubBytes : 0;
-  TileRegs<kTk, kSub, kGemmThreads / 2> r0, r1, r2, r3;
-#define FH_GEMM_LOAD(step)                                                   \
-  do {                                                                       \
-    const uint16_t* p_ = src + static_cast<int64_t>(step) * kTk * ld;        \
-    r0.load(p_, ld, kTk, ltid);                                              \
-    r1.load(p_ + kSub, ld, kTk, ltid);                                       \
-    r2.load(p_ + 2 * kSub, ld, kTk, ltid);                                   \
-    r3.load(p_ + 3 * kSub, ld, kTk, ltid);                                   \
-  } while (0)
-#define FH_GEMM_STORE(st)                                                    \
-  do {                                                                       \
-    char* base_ = smem + (st) * kStageBytes + lds_op;                        \
-    r0.store(base_, ltid);                                                   \
-    r1.store(base_ + kSubBytes, ltid);                                       \
-    r2.store(base_ + 2 * kSubBytes, ltid);                                   \
-    r3.store(base_ + 3 * kSubBytes, ltid);                                   \
-  } while (0)
+  const int lds_dst = lsub * kSubBytes;
+  const int last_row = total_steps * kTk - 1;
+  auto load = [&](int step, char* stage) __attribute__((always_inline)) {
+    dma_tile<kTk, kSub, 2>(src, ld, step * kTk, last_row, stage + lds_dst, wave & 1, lane);
+  };
 
   f32x16 acc[2][2];  // [n block][m block], rows = n, column = m
 #pragma unroll
@@ -87,36 +78,37 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(4)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = zero16();
 
-  if (s_begin < s_end) {
-    FH_GEMM_LOAD(s_begin);
-    FH_GEMM_STORE(0);
-  }
+  if (s_begin < s_end) load(s_begin, smem0);
+  wait_loads();
   __syncthreads();
-  for (int step = s_begin; step < s_end; ++step) {
-    const int st = (step - s_begin) & 1;
-    const bool more = step + 1 < s_end;
+  // Stage `step` from `cur` while stage step + 1 is loaded into `nxt`.
+  auto step_fn = [&](int step, const char* cur, char* nxt) __attribute__((always_inline)) {
     asm volatile("" : "+v"(b0), "+v"(b8));  // keep the XORed read offsets recomputed
-    if (more) FH_GEMM_LOAD(step + 1);
-    const char* sa = smem + st * kStageBytes;
-    const char* sb = sa + (kTm / kSub) * kSubBytes;
+    if (step + 1 < s_end) load(step + 1, nxt);
+    if (step < s_end) {
+      const char* sa = cur;
+      const char* sb = cur + (kTm / kSub) * kSubBytes;
 #pragma unroll
-    for (int ks = 0; ks < kTk / 16; ++ks) {
-      bf16x8 fa[2], fb[2];
+      for (int ks = 0; ks < kTk / 16; ++ks) {
+        bf16x8 fa[2], fb[2];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {  // the wave's 64 m are sub-tile wm; its 64 n sub-tile wn
-        fa[i] = lds_frag_tr<kSub>(sa + wm * kSubBytes, b0, b8, 16 * ks, i);
-        fb[i] = lds_frag_tr<kSub>(sb + wn * kSubBytes, b0, b8, 16 * ks, i);
+        for (int i = 0; i < 2; ++i) {  // the wave's 64 m are sub-tile wm; its 64 n sub-tile wn
+          fa[i] = lds_frag_tr<kSub>(sa + wm * kSubBytes, b0, b8, 16 * ks, i);
+          fb[i] = lds_frag_tr<kSub>(sb + wn * kSubBytes, b0, b8, 16 * ks, i);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[i][j] = mfma(fb[i], fa[j], acc[i][j]);
       }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma(fb[i], fa[j], acc[i][j]);
     }
-    if (more) FH_GEMM_STORE(st ^ 1);
+    wait_loads();
     __syncthreads();
+  };
+  for (int step = s_begin; step < s_end; step += 2) {
+    step_fn(step, smem0, smem1);
+    step_fn(step + 1, smem1, smem0);
   }
-#undef FH_GEMM_LOAD
-#undef FH_GEMM_STORE
 
   // lane: column m = m0 + 64 wm + 32 j + l32; rows n = n0 + 64 wn + 32 i + 8 g + 4 hl + 0..3
 #pragma unroll
