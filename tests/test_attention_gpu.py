@@ -76,6 +76,8 @@ def _tensor_err(a, b):
     (3, 65, 2, 2, 64),      # S just past one key block
     (1, 300, 4, 2, 64),     # odd count of 128-key blocks: the middle block is paired with itself
     (1, 1, 4, 2, 64),       # single token: output is v
+    (2, 77, 4, 2, 32),      # hd 32, ragged
+    (1, 33, 4, 4, 128),     # hd 128, one partial 32-query tile past a full one
 ])
 def test_attention_bf16_matches_closed_form(B, S, nh, nkv, hd):
     got, ref = _run(B, S, nh, nkv, hd, torch.bfloat16)
@@ -97,6 +99,32 @@ def test_attention_fp32_matches_closed_form_1e5(B, S, nh, nkv, hd):
         e = _tensor_err(got[name], ref[name])
         assert e < 1e-5, f"{name}: {e:.3e}"
     assert (got["lse"] - ref["lse"]).abs().max() < 1e-5
+
+
+@pytest.mark.parametrize("hd", [32, 64, 128])
+def test_attention_ragged_tiles_stay_inside_their_sequence(hd):
+    """Tiles that run past S load clamped rows of their own sequence, never the
+    next one: with every q/k/v/dO value of sequence 1 set to NaN, sequence 0's
+    output, lse and gradients are bit-identical to a run with finite values
+    there (a read of sequence 1 would carry a NaN through P V or dS Q)."""
+    ops = _ops()
+    B, S, nh, nkv = 2, 77, 4, 2
+    hq, hkv = nh * hd, nkv * hd
+    buf, do = _inputs(B, S, nh, nkv, hd, torch.bfloat16, 9)
+    outs = []
+    for poison in (False, True):
+        g, d = buf.clone().to(DEV), do.clone().to(DEV)
+        if poison:
+            g[S:] = float("nan")
+            d[S:] = float("nan")
+        q, k, v = g[:, :hq], g[:, hq:hq + hkv], g[:, hq + hkv:]
+        o, lse = ops.attn_fwd(q, k, v, B, S, nh, nkv, hd, hd ** -0.5)
+        dg = torch.empty_like(g)
+        ops.attn_bwd(q, k, v, o, d, lse, dg[:, :hq], dg[:, hq:hq + hkv], dg[:, hq + hkv:], B, S, nh, nkv, hd,
+                     hd ** -0.5)
+        outs.append((o[:S].cpu(), lse.view(B, nh, S)[0].cpu(), dg[:S].cpu()))
+    for a, b in zip(*outs):
+        assert torch.isfinite(a).all() and torch.equal(a, b)
 
 
 def test_attention_single_token_is_v():
