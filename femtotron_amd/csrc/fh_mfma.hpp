@@ -93,47 +93,6 @@ __device__ __forceinline__ bf16x8 lds_frag_tr(const char* tile, int b0, int b8, 
 // Row (M index) of accumulator entry j for lane half hl.
 __device__ __forceinline__ int acc_row(int j, int hl) { return 8 * (j >> 2) + 4 * hl + (j & 3); }
 
-// Per-thread registers holding one ROWS x HD bf16 tile in flight from global
-// memory to LDS (the software pipeline's prefetch stage): load() issues the
-// 16-byte global loads (rows at or beyond `valid` read as zero), store()
-// writes them swizzled into an LDS tile.  Consecutive threads take
-// consecutive 16-byte chunks of a row; every pass covers a multiple of 16
-// rows, so a thread's swizzle is the same in every pass.
-template <int ROWS, int HD, int NT>
-struct TileRegs {
-  static constexpr int CPR = HD / 8;
-  static constexpr int CHUNKS = ROWS * CPR;
-  static constexpr int N = (CHUNKS + NT - 1) / NT;
-  static constexpr int RPP = NT / CPR;  // rows per pass
-  static_assert(NT % CPR == 0 && RPP % 16 == 0, "pass must cover a multiple of 16 rows");
-  uint4 r[N];
-  __device__ __forceinline__ void load(const uint16_t* src, int64_t ld, int valid, int tid) {
-    const int row = tid / CPR, col = (tid % CPR) * 8;
-    const uint16_t* p = src + static_cast<int64_t>(row) * ld + col;
-    if (valid >= ROWS) {  // whole tile in range (the common case): no per-row guard
-#pragma unroll
-      for (int i = 0; i < N; ++i)
-        if (CHUNKS % NT == 0 || tid + i * NT < CHUNKS)
-          r[i] = *reinterpret_cast<const uint4*>(p + static_cast<int64_t>(i * RPP) * ld);
-      return;
-    }
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      r[i] = make_uint4(0, 0, 0, 0);
-      if ((CHUNKS % NT == 0 || tid + i * NT < CHUNKS) && row + i * RPP < valid)
-        r[i] = *reinterpret_cast<const uint4*>(p + static_cast<int64_t>(i * RPP) * ld);
-    }
-  }
-  __device__ __forceinline__ void store(char* tile, int tid) const {
-    const int row = tid / CPR, ch = tid % CPR;
-    char* p = tile + row * (2 * HD) + ((ch ^ swz<HD>(row)) << 4);
-#pragma unroll
-    for (int i = 0; i < N; ++i)
-      if (CHUNKS % NT == 0 || tid + i * NT < CHUNKS)
-        *reinterpret_cast<uint4*>(p + i * RPP * (2 * HD)) = r[i];
-  }
-};
-
 // Direct-to-LDS load of rows r0 .. r0+ROWS-1 of a bf16 [*, HD] matrix (row
 // stride ld elements) into a swizzled [ROWS x HD] LDS tile, shared by the NW
 // waves of a block: each global_load_lds_dwordx4 fills one 1 KB run of the
