@@ -85,6 +85,18 @@ def assert_close(a: torch.Tensor, b: torch.Tensor, rtol: float, atol: float, nam
             f"max|a-b|={err.max():.3e}, max|b|={b.abs().max():.3e}")
 
 
+def assert_tensor_close(a: torch.Tensor, b: torch.Tensor, rtol: float, atol: float, name: str = "") -> None:
+    """The reference's implementation-vs-implementation metric, per tensor:
+    max|a-b| <= atol + rtol * max|b| (femtotron/test/unit/test_pipeline_stage.py:82-128)."""
+    a = a.detach().float().cpu()
+    b = b.detach().float().cpu()
+    assert a.shape == b.shape, f"{name}: shape {tuple(a.shape)} vs {tuple(b.shape)}"
+    assert torch.isfinite(a).all(), f"{name}: non-finite values"
+    err = float((a - b).abs().max())
+    lim = atol + rtol * float(b.abs().max())
+    assert err <= lim, f"{name}: max|a-b|={err:.3e} > {lim:.3e}"
+
+
 def rel_err(a: torch.Tensor, b: torch.Tensor) -> float:
     a = a.detach().float().cpu()
     b = b.detach().float().cpu()
