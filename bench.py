@@ -85,6 +85,14 @@ def parse_args():
     ap.add_argument("--tune-gemms", default=None, metavar="CSV",
                     help="run TunableOp's search for every projection GEMM of --workload, write "
                          "the results to CSV and exit")
+    ap.add_argument("--gemm", choices=("auto", "hand", "library"), default="auto",
+                    help="projection GEMMs: per-shape choice from the measured table "
+                         "(femtotron_amd/tuned/gemm_dispatch_gfx950.json), the hand-written "
+                         "fh_gemm_bf16 wherever it applies, or the library GEMM")
+    ap.add_argument("--tune-gemm-dispatch", action="store_true",
+                    help="time fh_gemm_bf16 against the library GEMM for every projection GEMM of "
+                         "the three workloads, write femtotron_amd/tuned/gemm_dispatch_gfx950.json "
+                         "and exit")
     ap.add_argument("--stock-boundary", action="store_true",
                     help="keep the reference's nn.Embedding and final LlamaRMSNorm (no fuse_boundary_ops)")
     ap.add_argument("--stock-attention", action="store_true",
@@ -95,7 +103,8 @@ def parse_args():
     ap.add_argument("--profile-kernel", default=None,
                     help="launch only this fused kernel (swiglu_fwd, swiglu_bwd, rmsnorm_fwd, "
                          "add_rmsnorm_fwd, rmsnorm_bwd, rope_fwd, residual_add, attn_fwd, attn_bwd; "
-                         "embedding_fwd, embedding_bwd; gemm_tn_qkv, gemm_tn_o, gemm_tn_gate_up (weight-gradient GEMM); "
+                         "embedding_fwd, embedding_bwd; gemm_<nt|nn|tn>_<qkv|o|gate_up|down> "
+                         "(fh_gemm_bf16 at that projection GEMM); "
                          "adamw: one optimizer step over the workload's parameter shapes) at "
                          "--workload's step shape, after a 1 GiB device copy that calibrates HBM byte "
                          "counters, for rocprofv3 --pmc runs; prints one JSON line and exits")
@@ -295,24 +304,47 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True,
                  launches_per_step=L, flop_per_launch=bwd_flop, ms_per_launch=round(ms_b, 4),
                  achieved_tflops=round(bwd_flop / ms_b / 1e9, 1),
                  frac=round(bwd_flop / ms_b / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4))]
-    # the hand-written weight-gradient GEMM, at the projections the layer routes to it
-    from femtotron_amd.fused_layer import use_gemm_tn
-    for name, n_out, k_in in (("wgrad_qkv", Hq + 2 * Hkv, H), ("wgrad_o", H, Hq),
-                              ("wgrad_gate_up", 2 * F, H), ("wgrad_down", H, F)):
-        if sel and not fused_attention and name in ("wgrad_qkv", "wgrad_o"):
-            continue
-        dy = rnd(T, n_out)
-        xin = rnd(T, k_in)
-        if not use_gemm_tn(dy, xin):
-            continue
-        ms = event_ms(torch, lambda i=0: ops.gemm_tn(dy, xin), iters)
-        flop = 2 * T * n_out * k_in
-        mfma.append(dict(kernel=name, symbol="k_gemm_tn (+ k_gemm_tn_reduce)", launches_per_step=L,
-                         flop_per_launch=flop, ms_per_launch=round(ms, 4),
-                         achieved_tflops=round(flop / ms / 1e9, 1),
-                         frac=round(flop / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)))
-        del dy, xin
+    mfma += projection_gemm_rows(torch, c, iters, sel, fused_attention, rnd)
     return rows, mfma
+
+
+def projection_gemm_rows(torch, c: dict, iters: int, sel: bool, fused_attention: bool, rnd) -> list:
+    """Every projection GEMM of the step at its shape: the hand-written
+    fh_gemm_bf16 and the library GEMM timed side by side (HIP events), the one
+    the dispatch policy runs marked `path`, its MFMA fraction in `frac`."""
+    from femtotron_amd import ops, projections
+    T, H, F, L = c["batch"] * c["seq"], c["hidden"], c["ffn"], c["layers"]
+    hd = H // c["heads"]
+    Hq, Hkv = c["heads"] * hd, c["kv"] * hd
+    # launches per step: full AC runs the q/k/v, o and gate/up forward twice
+    # (forward and recompute) and down once; selective AC recomputes the MLP's
+    # gate/up only (attention runs once, outside the checkpoints)
+    projs = [("qkv", Hq + 2 * Hkv, H, 1 if sel else 2), ("o", H, Hq, 1 if sel else 2),
+             ("gate_up", 2 * F, H, 2), ("down", H, F, 1)]
+    out = []
+    for name, n_out, k_in, fwd_per_layer in projs:
+        if sel and not fused_attention and name in ("qkv", "o"):
+            continue
+        x, w, dy = rnd(T, k_in), rnd(n_out, k_in), rnd(T, n_out)
+        flop = 2 * T * n_out * k_in
+        for op, a, b, lib, per_layer in (("nt", x, w, lambda: torch.mm(x, w.t()), fwd_per_layer),
+                                         ("nn", dy, w, lambda: torch.mm(dy, w), 1),
+                                         ("tn", dy, x, lambda: torch.mm(dy.t(), x), 1)):
+            ms_hand = event_ms(torch, lambda i=0: ops.gemm(op, a, b), iters)
+            ms_lib = event_ms(torch, lambda i=0: lib(), iters)
+            hand = projections.gemm_policy() != "library" and (
+                projections.gemm_policy() == "hand"
+                or ops.gemm_dims(op, a, b) not in projections._library_shapes()[op])
+            ms = ms_hand if hand else ms_lib
+            out.append(dict(kernel=f"gemm_{op}_{name}", m_n_k=list(ops.gemm_dims(op, a, b)),
+                            path="fh_gemm_bf16 (k_gemm)" if hand else "library (torch.mm)",
+                            launches_per_step=per_layer * L, flop_per_launch=flop,
+                            ms_per_launch=round(ms, 4), hand_ms=round(ms_hand, 4),
+                            library_ms=round(ms_lib, 4),
+                            achieved_tflops=round(flop / ms / 1e9, 1),
+                            frac=round(flop / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)))
+        del x, w, dy
+    return out
 
 
 def profile_kernel(torch, name: str, c: dict, launches: int = 10) -> dict:
@@ -384,12 +416,15 @@ def profile_kernel(torch, name: str, c: dict, launches: int = 10) -> dict:
             dys = [rnd(T, H) for _ in range(n)]
             fn = lambda i: ops.embedding_bwd(dys[i], ids, V)
             nbytes = 2 * T * H + 2 * V * H + 8 * T
-    elif name in ("gemm_tn_qkv", "gemm_tn_o", "gemm_tn_gate_up"):
-        n_out, k_in = {"gemm_tn_qkv": (Hq + 2 * Hkv, H), "gemm_tn_o": (H, Hq),
-                       "gemm_tn_gate_up": (2 * F, H)}[name]
-        dys = [rnd(T, n_out) for _ in range(2)]
+    elif name.startswith("gemm_"):
+        _, op, proj = name.split("_", 2)
+        n_out, k_in = {"qkv": (Hq + 2 * Hkv, H), "o": (H, Hq), "gate_up": (2 * F, H),
+                       "down": (H, F)}[proj]
         xs = [rnd(T, k_in) for _ in range(2)]
-        fn = lambda i: ops.gemm_tn(dys[i % 2], xs[i % 2])
+        ws = [rnd(n_out, k_in) for _ in range(2)]
+        dys = [rnd(T, n_out) for _ in range(2)]
+        operands = {"nt": (xs, ws), "nn": (dys, ws), "tn": (dys, xs)}[op]
+        fn = lambda i: ops.gemm(op, operands[0][i % 2], operands[1][i % 2])
         nbytes = None  # MFMA-bound: 2*T*n_out*k_in FLOP per launch
     elif name == "adamw":
         from femtotron_amd.optim import FusedAdamW
@@ -508,6 +543,14 @@ def main() -> int:
         return 0
     tuned = False if args.no_tuned_gemms else gemm_tuning.use_tuned_gemms()
     log(f"library GEMMs: {'shipped TunableOp solutions' if tuned else 'default heuristics'}")
+    from femtotron_amd import projections
+    if args.tune_gemm_dispatch:
+        wls = {name: (w["batch"] * w["seq"], w["hidden"], w["hidden"], w["kv"] * w["hidden"] // w["heads"],
+                      w["ffn"]) for name, (w, _, _) in WORKLOADS.items()}
+        path = projections.measure_dispatch(wls, log=log)
+        print(json.dumps({"gemm_dispatch": str(path)}), flush=True)
+        return 0
+    projections.set_gemm_policy(args.gemm)
 
     if args.profile_kernel:
         print(json.dumps(profile_kernel(torch, args.profile_kernel, WORKLOADS[args.workload][0])),
@@ -542,6 +585,7 @@ def main() -> int:
 
     reset_dispatch_counts()
     reset_attention_dispatch_counts()
+    projections.reset_gemm_dispatch_counts()
     log(f"fused path ({args.ac} AC): {args.warmup} warm-up + {args.steps} timed steps")
     fused_head = not args.stock_loss_head
     sec = time_steps(torch, model, ids, args.steps, args.warmup, materialize_logits=not fused_head)
@@ -553,7 +597,11 @@ def main() -> int:
         acounts = attention_dispatch_counts()
         assert acounts == {"fused": L * (args.steps + args.warmup), "fallback": 0}, acounts
     tok_s = T / sec
-    log(f"fused: {sec * 1e3:.2f} ms/step, {tok_s:.0f} tokens/s")
+    gemm_counts = projections.gemm_dispatch_counts()
+    n_steps = args.steps + args.warmup
+    gemm_counts = {k: v // n_steps for k, v in gemm_counts.items()}
+    log(f"fused: {sec * 1e3:.2f} ms/step, {tok_s:.0f} tokens/s; projection GEMMs per step: "
+        f"{gemm_counts['hand']} hand-written, {gemm_counts['library']} library")
 
     log("per-kernel HIP-event timings at the step's shapes")
     rows, mfma = kernel_table(torch, c, args.kernel_iters, args.ac, boundary=bool(boundary),
@@ -626,8 +674,12 @@ def main() -> int:
         "roofline": roofline,
         "fused_kernels_hbm": rows,
         "mfma_kernels": mfma,
-        "gemms": ("hipBLASLt/rocBLAS, TunableOp solutions from femtotron_amd/tuned/"
-                  "tunableop_gfx950.csv" if tuned else "hipBLASLt default heuristics"),
+        "gemms": {"policy": args.gemm,
+                  "projection_gemms_per_step": gemm_counts,
+                  "hand_written": "fh_gemm_bf16 (femtotron_amd/csrc/fh_gemm.hip)",
+                  "library": ("hipBLASLt/rocBLAS, TunableOp solutions from femtotron_amd/tuned/"
+                              "tunableop_gfx950.csv" if tuned else "hipBLASLt default heuristics"),
+                  "table": "femtotron_amd/tuned/gemm_dispatch_gfx950.json"},
         "weights": f"q/k/v and gate/up packed contiguously ({packed_groups} groups)",
         "boundary_ops": ("fused embedding (deterministic scatter-add backward) and final RMSNorm"
                          if boundary else "reference nn.Embedding and LlamaRMSNorm"),

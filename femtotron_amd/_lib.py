@@ -12,12 +12,16 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_size_t, c_void_
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libfemtohip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 FH_BF16 = 0
 FH_F32 = 1
 
 FH_OK = 0
+
+FH_GEMM_NT = 0
+FH_GEMM_NN = 1
+FH_GEMM_TN = 2
 
 _V = c_void_p
 _I64 = c_int64
@@ -50,8 +54,8 @@ SIGNATURES: dict[str, tuple] = {
                             _I64, _I64, _I64, _I64, _I64, _F, _V]),
     "fh_ce_fwd_bwd": (c_int, [c_int, _V, _I64, _V, _I64, _I64, _I64, _V, POINTER(c_float), _V]),
     "fh_adamw_workspace_size": (c_size_t, [_I64]),
-    "fh_gemm_tn_workspace_size": (c_size_t, [_I64, _I64, _I64]),
-    "fh_gemm_tn": (c_int, [c_int, _V, _I64, _V, _I64, _V, _I64, _I64, _I64, _I64, _V, _V]),
+    "fh_gemm_bf16_workspace_size": (c_size_t, [c_int, _I64, _I64, _I64]),
+    "fh_gemm_bf16": (c_int, [c_int, _V, _I64, _V, _I64, _V, _I64, _V, _I64, _I64, _I64, _I64, _V, _V]),
     "fh_embedding_fwd": (c_int, [c_int, _V, _V, _V, _I64, _I64, _I64, _V]),
     "fh_embedding_bwd_workspace_size": (c_size_t, [_I64, _I64]),
     "fh_embedding_bwd": (c_int, [c_int, _V, _V, _V, _I64, _I64, _I64, _I64, _V, _V]),

@@ -37,9 +37,10 @@ import types
 
 import torch
 
-from . import _lib, attention, ops
+from . import _lib, ops
 from .fused_checkpoint import _aligned, _check_params, _linear_weight
-from .fused_layer import LayerShape, _WgradStream, _cat_rows, _mm_nt
+from .fused_layer import LayerShape, _WgradStream, _cat_rows, attn_bwd, attn_fwd
+from .projections import linear, linear_dgrad
 
 _ACCEPTED_KWARGS = {"position_ids", "use_cache", "cache_position"}
 _counts_lock = threading.Lock()
@@ -70,10 +71,10 @@ class FusedAttentionFunction(torch.autograd.Function):
     def forward(ctx, y, cos, sin, shp, wq, wk, wv, wo):
         B, S, H = y.shape
         y2 = y.reshape(B * S, H)
-        qkv = _mm_nt(y2, _cat_rows(wq, wk, wv))
+        qkv = linear(y2, _cat_rows(wq, wk, wv))
         ops.rope_fwd_(qkv, shp.n_heads + shp.n_kv_heads, shp.head_dim, S, cos, sin)
-        o, lse = attention.attn_fwd(qkv, B, S, shp, need_lse=True)
-        a = _mm_nt(o, wo)
+        o, lse = attn_fwd(qkv, B, S, shp, need_lse=True)
+        a = linear(o, wo)
         ctx.save_for_backward(y, cos, sin, qkv, o, lse, wq, wk, wv, wo)
         ctx.shp = shp
         return a.view(B, S, H)
@@ -87,12 +88,12 @@ class FusedAttentionFunction(torch.autograd.Function):
         with torch.no_grad():
             side = _WgradStream(da2.device)
             dwo = side.mm_tn(da2, o)
-            do = torch.mm(da2, wo)
-            dqkv = attention.attn_bwd(do, qkv, o, lse, B, S, shp)
+            do = linear_dgrad(da2, wo)
+            dqkv = attn_bwd(do, qkv, o, lse, B, S, shp)
             del do
             ops.rope_bwd_(dqkv, shp.n_heads + shp.n_kv_heads, shp.head_dim, S, cos, sin)
             dwqkv = side.mm_tn(dqkv, y.reshape(B * S, H))
-            dy = torch.mm(dqkv, _cat_rows(wq, wk, wv))
+            dy = linear_dgrad(dqkv, _cat_rows(wq, wk, wv))
             side.join()
         hq, hkv = shp.hq, shp.hkv
         return (dy.view(B, S, H), None, None, None, dwqkv[:hq], dwqkv[hq:hq + hkv],

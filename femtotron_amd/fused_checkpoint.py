@@ -222,8 +222,10 @@ def _plan_layer(module: Any, x: torch.Tensor, kwargs: dict):
         return "unexpected o/mlp weight shapes"
     if nkv == 0 or nh % nkv:
         return "n_heads not a multiple of n_kv_heads"
-    if hd % 16 or H % 8 or F_ % 8 or H > 8192:
-        return "head_dim % 16, hidden % 8, ffn % 8 and hidden <= 8192 required"
+    if hd not in (32, 64, 128):
+        return f"head_dim {hd} (the attention kernels take 32, 64 or 128)"
+    if H % 8 or F_ % 8 or H > 8192:
+        return "hidden % 8, ffn % 8 and hidden <= 8192 required"
     shp = LayerShape(hidden=H, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn=F_,
                      eps1=float(ln1.variance_epsilon), eps2=float(ln2.variance_epsilon),
                      scale=float(attn.scaling))

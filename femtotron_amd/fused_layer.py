@@ -16,11 +16,16 @@ Layer arithmetic (transformers 5.15.0, models/llama/modeling_llama.py:284-325):
     h     = x + o Wo^T;  z = RMSNorm2(h)         (fh_add_rmsnorm_fwd)
     g,u   = z Wg^T, z Wu^T                       -> one GEMM over [Wg;Wu]
     p     = silu(g)*u                            (fh_swiglu_fwd)
-    out   = h + p Wd^T                           (fh_add)
+    out   = h + p Wd^T                           (residual add in the GEMM epilogue)
+
+The projections' GEMMs go through femtotron_amd.projections (fh_gemm_bf16 or
+the tuned library GEMM, per shape).
 
 Token-major layout everywhere: activations are [T, features] with T = B*S, so
 q/k/v are column ranges of one [T, Hq+2Hkv] buffer and attention reads and
-writes heads as column blocks (no transposes).
+writes heads as column blocks (no transposes); the attention backward writes
+dq, dk, dv into the same column ranges of one dqkv buffer, which the q/k/v
+weight-gradient and input-gradient GEMMs consume whole.
 """
 from __future__ import annotations
 
@@ -28,7 +33,8 @@ from dataclasses import dataclass
 
 import torch
 
-from . import attention, ops
+from . import ops
+from .projections import linear, linear_dgrad, linear_residual, linear_wgrad
 from .weight_packing import packed
 
 
@@ -52,16 +58,34 @@ class LayerShape:
         return self.n_kv_heads * self.head_dim
 
 
-def _mm_nt(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-    """a[M,K] @ b[N,K]^T (nn.Linear orientation)."""
-    return torch.mm(a, b.t())
-
-
 def _cat_rows(*ws: torch.Tensor) -> torch.Tensor:
     """[W1; W2; ...]: a view when the weights are packed contiguously
     (femtotron_amd.weight_packing), else a concatenated copy."""
     view = packed(*ws)
     return view if view is not None else torch.cat(ws, 0)
+
+
+def _qkv_split(buf: torch.Tensor, shp: "LayerShape"):
+    hq, hkv = shp.hq, shp.hkv
+    return buf[:, :hq], buf[:, hq:hq + hkv], buf[:, hq + hkv:hq + 2 * hkv]
+
+
+def attn_fwd(qkv: torch.Tensor, batch: int, seq: int, shp: "LayerShape", *, need_lse: bool):
+    """Causal GQA attention over the [T, Hq+2Hkv] qkv buffer (fh_attn_fwd)."""
+    q, k, v = _qkv_split(qkv, shp)
+    return ops.attn_fwd(q, k, v, batch, seq, shp.n_heads, shp.n_kv_heads, shp.head_dim, shp.scale,
+                        need_lse=need_lse)
+
+
+def attn_bwd(do: torch.Tensor, qkv: torch.Tensor, o: torch.Tensor, lse: torch.Tensor, batch: int,
+             seq: int, shp: "LayerShape") -> torch.Tensor:
+    """dqkv [T, Hq+2Hkv] of attn_fwd (fh_attn_bwd)."""
+    q, k, v = _qkv_split(qkv, shp)
+    dqkv = torch.empty_like(qkv)
+    dq, dk, dv = _qkv_split(dqkv, shp)
+    ops.attn_bwd(q, k, v, o, do, lse, dq, dk, dv, batch, seq, shp.n_heads, shp.n_kv_heads,
+                 shp.head_dim, shp.scale)
+    return dqkv
 
 
 
@@ -83,14 +107,14 @@ def layer_forward(x2: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, shp: L
     y1 = ops.rmsnorm_fwd(x2, w1, shp.eps1, rstd=rstd1)
 
     wqkv = _cat_rows(wq, wk, wv)
-    qkv = _mm_nt(y1, wqkv)
+    qkv = linear(y1, wqkv)
     ops.rope_fwd_(qkv, shp.n_heads + shp.n_kv_heads, shp.head_dim, seq, cos, sin)
-    o, lse = attention.attn_fwd(qkv, batch, seq, shp, need_lse=keep)
-    a = _mm_nt(o, wo)
+    o, lse = attn_fwd(qkv, batch, seq, shp, need_lse=keep)
+    a = linear(o, wo)
     rstd2 = torch.empty(T, dtype=torch.float32, device=dev) if keep else None
     h, z = ops.add_rmsnorm_fwd(x2, a, w2, shp.eps2, rstd=rstd2)
     del a
-    gu = _mm_nt(z, _cat_rows(wg, wu))
+    gu = linear(z, _cat_rows(wg, wu))
     F_ = shp.ffn
     p = ops.swiglu_fwd(gu[:, :F_], gu[:, F_:])
     if keep:
@@ -98,24 +122,10 @@ def layer_forward(x2: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, shp: L
         acts.h, acts.rstd2, acts.z, acts.gu, acts.p = h, rstd2, z, gu, p
         return acts
     del gu, qkv, o, y1, z
-    m = _mm_nt(p, wd)
-    return ops.add(h, m, out=m)
+    return linear_residual(p, wd, h)
 
 
 _side_streams: dict[int, torch.cuda.Stream] = {}
-# Weight gradients dW = dY^T X whose input X is at most this wide go to
-# fh_gemm_tn, wider ones to the tuned library GEMM.  Measured on a warm MI355X
-# against the shipped library solutions: at input width 2048 (TinyLlama's
-# q/k/v, o and gate/up) fh_gemm_tn took 175 / 143 / 760 us against 211-219 /
-# 162-168 / 846-854 us; at input width 4096 and above (the Llama-3-8B and
-# Llama-2-7B slices, and TinyLlama's down projection, input width 5632) the
-# library was as fast or faster in 10 of 11 shapes.
-GEMM_TN_MAX_INPUT = 2048
-
-
-def use_gemm_tn(dy: torch.Tensor, x: torch.Tensor) -> bool:
-    """Whether dW = dy^T x runs on fh_gemm_tn (see GEMM_TN_MAX_INPUT)."""
-    return ops.gemm_tn_supported(dy, x) and x.size(1) <= GEMM_TN_MAX_INPUT
 
 
 class _WgradStream:
@@ -137,15 +147,10 @@ class _WgradStream:
         self.side = side
 
     def mm_tn(self, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-        """a^T @ b on the side stream: the hand-written token-split GEMM
-        (fh_gemm_tn) where use_gemm_tn says it is the faster one, else the
-        library GEMM."""
+        """a^T @ b on the side stream (projections.linear_wgrad)."""
         self.side.wait_stream(self.main)
         with torch.cuda.stream(self.side):
-            if use_gemm_tn(a, b):
-                out = ops.gemm_tn(a, b)
-            else:
-                out = torch.mm(a.t(), b)
+            out = linear_wgrad(a, b)
         a.record_stream(self.side)
         b.record_stream(self.side)
         out.record_stream(self.main)
@@ -162,14 +167,14 @@ def layer_backward(dout2: torch.Tensor, x2: torch.Tensor, cos: torch.Tensor, sin
     wg_stream = _WgradStream(dout2.device)
     # MLP: m = p Wd^T
     dwd = wg_stream.mm_tn(dout2, acts.p)
-    dp = torch.mm(dout2, wd)
+    dp = linear_dgrad(dout2, wd)
     acts.p = None
     dgu = torch.empty_like(acts.gu)
     ops.swiglu_bwd(dp, acts.gu[:, :F_], acts.gu[:, F_:], dgu[:, :F_], dgu[:, F_:])
     del dp
     acts.gu = None
     dwgu = wg_stream.mm_tn(dgu, acts.z)
-    dz = torch.mm(dgu, _cat_rows(wg, wu))
+    dz = linear_dgrad(dgu, _cat_rows(wg, wu))
     del dgu
     acts.z = None
     # post-attention norm + residual: dh = dout + RMSNorm2^T(dz)
@@ -178,13 +183,13 @@ def layer_backward(dout2: torch.Tensor, x2: torch.Tensor, cos: torch.Tensor, sin
     acts.h = None
     # attention output projection
     dwo = wg_stream.mm_tn(dh, acts.o)
-    do = torch.mm(dh, wo)
-    dqkv = attention.attn_bwd(do, acts.qkv, acts.o, acts.lse, batch, seq, shp)
+    do = linear_dgrad(dh, wo)
+    dqkv = attn_bwd(do, acts.qkv, acts.o, acts.lse, batch, seq, shp)
     del do
     acts.o = acts.lse = acts.qkv = None
     ops.rope_bwd_(dqkv, shp.n_heads + shp.n_kv_heads, shp.head_dim, seq, cos, sin)
     dwqkv = wg_stream.mm_tn(dqkv, acts.y1)
-    dy1 = torch.mm(dqkv, _cat_rows(wq, wk, wv))
+    dy1 = linear_dgrad(dqkv, _cat_rows(wq, wk, wv))
     del dqkv
     acts.y1 = None
     dx, dw1 = ops.rmsnorm_bwd(dy1, x2, w1, shp.eps1, rstd=acts.rstd1, dres=dh)

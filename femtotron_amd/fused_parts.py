@@ -22,7 +22,8 @@ from __future__ import annotations
 import torch
 
 from . import ops
-from .fused_layer import _cat_rows, _mm_nt, _WgradStream
+from .fused_layer import _cat_rows, _WgradStream
+from .projections import linear, linear_dgrad
 
 
 def mlp_forward(z2: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor, wd: torch.Tensor, *,
@@ -30,12 +31,12 @@ def mlp_forward(z2: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor, wd: torch.
     """z2 [T, H] -> m [T, H]; keep=True stops after the SwiGLU product and
     returns (gu, p) for the backward."""
     F_ = wg.shape[0]
-    gu = _mm_nt(z2, _cat_rows(wg, wu))
+    gu = linear(z2, _cat_rows(wg, wu))
     p = ops.swiglu_fwd(gu[:, :F_], gu[:, F_:])
     if keep:
         return gu, p
     del gu
-    return _mm_nt(p, wd)
+    return linear(p, wd)
 
 
 def mlp_backward(dm2: torch.Tensor, z2: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor,
@@ -43,13 +44,13 @@ def mlp_backward(dm2: torch.Tensor, z2: torch.Tensor, wg: torch.Tensor, wu: torc
     F_ = wg.shape[0]
     wg_stream = _WgradStream(dm2.device)
     dwd = wg_stream.mm_tn(dm2, p)
-    dp = torch.mm(dm2, wd)
+    dp = linear_dgrad(dm2, wd)
     del p
     dgu = torch.empty_like(gu)
     ops.swiglu_bwd(dp, gu[:, :F_], gu[:, F_:], dgu[:, :F_], dgu[:, F_:])
     del dp, gu
     dwgu = wg_stream.mm_tn(dgu, z2)
-    dz = torch.mm(dgu, _cat_rows(wg, wu))
+    dz = linear_dgrad(dgu, _cat_rows(wg, wu))
     wg_stream.join()
     return dz, dwgu[:F_], dwgu[F_:], dwd
 

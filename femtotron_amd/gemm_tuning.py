@@ -43,16 +43,21 @@ WORKLOADS = {
 def use_tuned_gemms(path: str | Path | None = None) -> bool:
     """Serve ``torch.mm`` from the recorded solutions in ``path`` (default: the
     shipped gfx950 file).  Returns False, changing nothing, when the file is
-    absent or no HIP device is present."""
+    absent, no HIP device is present, or TunableOp rejects the file (its
+    validators -- torch, HIP, hipBLASLt, rocBLAS versions and the GPU
+    architecture -- do not match this process)."""
     path = Path(path) if path is not None else RESULTS_FILE
     if not path.is_file() or not torch.cuda.is_available():
         return False
     tunable = torch.cuda.tunable
+    was_enabled = tunable.is_enabled()
     tunable.enable(True)
     tunable.tuning_enable(False)
     tunable.record_untuned_enable(False)
     tunable.set_filename(str(path))
-    tunable.read_file(str(path))
+    if not tunable.read_file(str(path)):
+        tunable.enable(was_enabled)
+        return False
     return True
 
 

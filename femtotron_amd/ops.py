@@ -313,30 +313,68 @@ def embedding_bwd(dy: torch.Tensor, ids: torch.Tensor, vocab: int,
 
 
 # ------------------------------------------------------------- GEMM
-def gemm_tn_supported(a: torch.Tensor, b: torch.Tensor) -> bool:
-    """Whether gemm_tn takes a [k, m] and b [k, n]: bf16 on one HIP device, last
-    dims contiguous, m and n multiples of 256, k a multiple of 64, aligned."""
+_GEMM_OPS = {"nt": _lib.FH_GEMM_NT, "nn": _lib.FH_GEMM_NN, "tn": _lib.FH_GEMM_TN}
+
+
+def gemm_dims(op: str, a: torch.Tensor, b: torch.Tensor):
+    """(m, n, k) of op(a) @ op(b), or None if the shapes do not chain."""
+    if a.dim() != 2 or b.dim() != 2:
+        return None
+    if op == "nt":
+        (m, k), (n, kb) = a.shape, b.shape
+    elif op == "nn":
+        (m, k), (kb, n) = a.shape, b.shape
+    elif op == "tn":
+        (k, m), (kb, n) = a.shape, b.shape
+    else:
+        raise ValueError(f"gemm: op must be 'nt', 'nn' or 'tn', got {op!r}")
+    return (m, n, k) if k == kb else None
+
+
+def gemm_supported(op: str, a: torch.Tensor, b: torch.Tensor) -> bool:
+    """Whether fh_gemm_bf16 takes these operands: bf16 on one HIP device, 2-D
+    with a contiguous last dim, k a multiple of 64, n (and for 'tn' also m) a
+    multiple of 8, row strides multiples of 8 and 16-byte aligned data."""
     if not (a.is_cuda and b.is_cuda and a.device == b.device and a.dtype == b.dtype == torch.bfloat16):
         return False
-    if a.dim() != 2 or b.dim() != 2 or a.size(0) != b.size(0) or a.stride(1) != 1 or b.stride(1) != 1:
+    dims = gemm_dims(op, a, b)
+    if dims is None:
         return False
-    k, m = a.shape
-    n = b.size(1)
-    return (m % 256 == 0 and n % 256 == 0 and k % 64 == 0 and k > 0 and a.stride(0) % 8 == 0
-            and b.stride(0) % 8 == 0 and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0)
+    m, n, k = dims
+    if min(m, n, k) <= 0 or k % 64 or n % 8 or (op == "tn" and m % 8):
+        return False
+    for t in (a, b):
+        if t.stride(1) != 1 or t.stride(0) % 8 or t.data_ptr() % 16:
+            return False
+    return True
 
 
-def gemm_tn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-    """a^T @ b for a [k, m], b [k, n] (bf16, token-major): [m, n], fp32 accumulation."""
-    _require_gpu(a, b)
-    if not gemm_tn_supported(a, b):
-        raise ValueError(f"gemm_tn: unsupported operands {tuple(a.shape)} {a.stride()} x "
-                         f"{tuple(b.shape)} {b.stride()} ({a.dtype})")
-    k, m = a.shape
-    n = b.size(1)
-    c = torch.empty(m, n, dtype=a.dtype, device=a.device)
-    nbytes = _lib.lib().fh_gemm_tn_workspace_size(m, n, k)
+def gemm(op: str, a: torch.Tensor, b: torch.Tensor, *, residual: torch.Tensor | None = None,
+         out: torch.Tensor | None = None) -> torch.Tensor:
+    """op(a) @ op(b) in bf16 with fp32 accumulation (fh_gemm_bf16):
+    'nt': a [m,k] @ b[n,k]^T (nn.Linear forward), 'nn': a [m,k] @ b [k,n]
+    (input gradient), 'tn': a[k,m]^T @ b [k,n] (weight gradient).  With
+    `residual` ([m, n]) returns residual + to_bf16(product), rounded again;
+    `out` may be `residual` itself."""
+    _require_gpu(a, b, residual, out)
+    if not gemm_supported(op, a, b):
+        raise ValueError(f"gemm({op}): unsupported operands {tuple(a.shape)} {a.stride()} x "
+                         f"{tuple(b.shape)} {b.stride()} ({a.dtype}, {b.dtype})")
+    m, n, k = gemm_dims(op, a, b)
+    c = torch.empty(m, n, dtype=a.dtype, device=a.device) if out is None else out
+    for t, name in ((c, "out"), (residual, "residual")):
+        if t is None:
+            continue
+        if t.dtype != torch.bfloat16 or tuple(t.shape) != (m, n) or t.stride(1) != 1:
+            raise ValueError(f"gemm({op}): {name} must be a bf16 [{m}, {n}] row-major view")
+        if t.stride(0) % 4 or t.data_ptr() % 8:
+            raise ValueError(f"gemm({op}): {name} must be 8-byte aligned with a row stride % 4 == 0")
+    code = _GEMM_OPS[op]
+    nbytes = _lib.lib().fh_gemm_bf16_workspace_size(code, m, n, k)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device) if nbytes else None
-    _lib.call("fh_gemm_tn", _dtype_code(a), _ptr(a), a.stride(0), _ptr(b), b.stride(0), _ptr(c), n,
-              m, n, k, _ptr(ws), _stream(a))
+    _lib.call("fh_gemm_bf16", code, _ptr(a), a.stride(0), _ptr(b), b.stride(0), _ptr(c), c.stride(0),
+              _ptr(residual), 0 if residual is None else residual.stride(0), m, n, k, _ptr(ws),
+              _stream(a))
     return c
+
+

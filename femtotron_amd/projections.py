@@ -1,0 +1,175 @@
+"""The GEMMs of the layer's seven projections, routed per shape.
+
+Every projection of the decoder layer is femtotron's Column/RowParallelLinear
+at one rank (femtotron/parallel/tensor_parallel/linear.py:66-80, 194-214),
+i.e. ``F.linear(x, W)`` with W [out, in] and no bias.  Its three GEMMs are:
+
+    forward          y  = x W^T        fh_gemm_bf16 FH_GEMM_NT   (linear)
+    input gradient   dx = dy W         fh_gemm_bf16 FH_GEMM_NN   (linear_dgrad)
+    weight gradient  dW = dy^T x       fh_gemm_bf16 FH_GEMM_TN   (linear_wgrad)
+
+plus ``residual + x W^T`` with the residual add fused into the forward GEMM's
+epilogue (linear_residual; modeling_llama.py:323 rounds the projection output
+to bf16, then the sum).
+
+Each call runs either the hand-written gfx950 kernel or the tuned library
+GEMM (``torch.mm`` on hipBLASLt/rocBLAS), by policy:
+
+* ``"auto"`` (default): the shipped per-shape table
+  ``tuned/gemm_dispatch_gfx950.json`` names the shapes measured on an MI355X
+  where the library was faster than the hand-written kernel; those run on the
+  library, every other supported shape on the hand-written kernel;
+* ``"hand"``: the hand-written kernel wherever it supports the operands;
+* ``"library"``: always the library.
+
+Operands the kernel does not take (fp32, k not a multiple of 64, ...) go to
+the library under every policy.  ``gemm_dispatch_counts()`` tells tests and
+the benchmark which path ran.
+"""
+from __future__ import annotations
+
+import json
+import threading
+from pathlib import Path
+
+import torch
+
+from . import ops
+
+TABLE_FILE = Path(__file__).resolve().parent / "tuned" / "gemm_dispatch_gfx950.json"
+
+_lock = threading.Lock()
+_policy = ["auto"]
+_table: dict[str, set] | None = None
+_counts = {"hand": 0, "library": 0}
+
+
+def set_gemm_policy(policy: str) -> None:
+    """'auto' (measured table), 'hand' (hand-written wherever supported) or 'library'."""
+    if policy not in ("auto", "hand", "library"):
+        raise ValueError(f"gemm policy must be 'auto', 'hand' or 'library', got {policy!r}")
+    _policy[0] = policy
+
+
+def gemm_policy() -> str:
+    return _policy[0]
+
+
+def gemm_dispatch_counts() -> dict[str, int]:
+    with _lock:
+        return dict(_counts)
+
+
+def reset_gemm_dispatch_counts() -> None:
+    with _lock:
+        _counts["hand"] = 0
+        _counts["library"] = 0
+
+
+def _library_shapes() -> dict[str, set]:
+    global _table
+    if _table is None:
+        shapes: dict[str, set] = {"nt": set(), "nn": set(), "tn": set()}
+        if TABLE_FILE.is_file():
+            data = json.loads(TABLE_FILE.read_text())
+            for op in shapes:
+                shapes[op] = {tuple(s) for s in data.get("library", {}).get(op, [])}
+        _table = shapes
+    return _table
+
+
+def _use_hand(op: str, a: torch.Tensor, b: torch.Tensor) -> bool:
+    pol = _policy[0]
+    use = pol != "library" and ops.gemm_supported(op, a, b)
+    if use and pol == "auto":
+        use = ops.gemm_dims(op, a, b) not in _library_shapes()[op]
+    with _lock:
+        _counts["hand" if use else "library"] += 1
+    return use
+
+
+def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """x [T, in] @ w[out, in]^T."""
+    if _use_hand("nt", x, w):
+        return ops.gemm("nt", x, w)
+    return torch.mm(x, w.t())
+
+
+def linear_residual(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+    """residual + to_dtype(x @ w^T), written into `residual`'s memory."""
+    if _use_hand("nt", x, w) and residual.is_contiguous():
+        return ops.gemm("nt", x, w, residual=residual, out=residual)
+    m = torch.mm(x, w.t())
+    return ops.add(residual, m, out=m)
+
+
+def linear_dgrad(dy: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """dy [T, out] @ w [out, in]."""
+    if _use_hand("nn", dy, w):
+        return ops.gemm("nn", dy, w)
+    return torch.mm(dy, w)
+
+
+def linear_wgrad(dy: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """dy [T, out]^T @ x [T, in]: the [out, in] weight gradient."""
+    if _use_hand("tn", dy, x):
+        return ops.gemm("tn", dy, x)
+    return torch.mm(dy.t(), x)
+
+
+def layer_gemm_forms(tokens: int, hidden: int, q_width: int, kv_width: int, ffn: int):
+    """(op, m, n, k) of every GEMM a fused decoder layer issues (packed q/k/v and
+    gate/up), in fh_gemm_bf16's convention."""
+    projs = [(q_width + 2 * kv_width, hidden), (hidden, q_width), (2 * ffn, hidden), (hidden, ffn)]
+    forms = []
+    for out_f, in_f in projs:
+        forms += [("nt", tokens, out_f, in_f), ("nn", tokens, in_f, out_f), ("tn", out_f, in_f, tokens)]
+    return forms
+
+
+def measure_dispatch(workloads: dict, path: str | Path = TABLE_FILE, *, iters: int = 20,
+                     log=print) -> Path:
+    """Time the hand-written kernel against the library GEMM (with whatever
+    library solutions the process has enabled) for every layer GEMM of
+    `workloads` ({name: (tokens, hidden, q width, kv width, ffn)}) and write
+    the shapes where the library was faster.  Needs a HIP device."""
+    dev, bf = "cuda", torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(0)
+    lib_faster: dict[str, list] = {"nt": [], "nn": [], "tn": []}
+    rows = []
+
+    def timed(fn) -> float:
+        for _ in range(3):
+            fn()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(iters):
+            fn()
+        e.record()
+        e.synchronize()
+        return s.elapsed_time(e) / iters * 1e3
+
+    for name, (T, H, hq, hkv, F) in workloads.items():
+        for op, m, n, k in layer_gemm_forms(T, H, hq, hkv, F):
+            a_shape = (k, m) if op == "tn" else (m, k)
+            b_shape = (n, k) if op == "nt" else (k, n)
+            a = torch.randn(*a_shape, device=dev, generator=g).to(bf)
+            b = torch.randn(*b_shape, device=dev, generator=g).to(bf)
+            lib = {"nt": lambda: torch.mm(a, b.t()), "nn": lambda: torch.mm(a, b),
+                   "tn": lambda: torch.mm(a.t(), b)}[op]
+            t_hand = timed(lambda: ops.gemm(op, a, b))
+            t_lib = timed(lib)
+            rows.append(dict(workload=name, op=op, m=m, n=n, k=k, hand_us=round(t_hand, 1),
+                             library_us=round(t_lib, 1)))
+            if t_lib < t_hand and [m, n, k] not in lib_faster[op]:
+                lib_faster[op].append([m, n, k])
+            log(f"[gemm-dispatch] {name} {op} m={m} n={n} k={k}: hand {t_hand:.1f} us, "
+                f"library {t_lib:.1f} us")
+            del a, b
+    data = {"note": "shapes (m, n, k of fh_gemm_bf16) where the tuned library GEMM measured faster "
+                    "than the hand-written kernel on an MI355X; everything else runs hand-written",
+            "library": lib_faster, "measurements": rows}
+    Path(path).write_text(json.dumps(data, indent=1) + "\n")
+    global _table
+    _table = None
+    return Path(path)

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define FH_ABI_VERSION 1
+#define FH_ABI_VERSION 2
 
 typedef enum fh_dtype {
   FH_BF16 = 0, /* bfloat16 storage, fp32 arithmetic */
@@ -262,19 +262,37 @@ int fh_embedding_bwd(fh_dtype dt, const void* dy, const int64_t* ids, void* dwei
                      void* workspace, hipStream_t stream);
 
 /* ------------------------------------------------------------------------
- * Weight-gradient GEMM of the projections: C[m, n] = sum_t A[t, m] * B[t, n]
- * (C = A^T B), the grad_weight = grad_output^T @ input of every F.linear in the
- * layer backward (femtotron/parallel/tensor_parallel/linear.py:72, 206; HF
- * nn.Linear at one rank).  A [k, m] (row stride lda), B [k, n] (ldb), C [m, n]
- * (ldc), all bf16, row-major, 16-byte aligned; m, n multiples of 256, k a
- * multiple of 64.  fp32 accumulation, C rounded to bf16 once.  When the
- * output has few 256 x 256 tiles the k range is split into slices whose fp32
- * partial sums go to `workspace` (fh_gemm_tn_workspace_size bytes, 0 = none
- * needed) and are added in slice order: deterministic.
+ * GEMMs of the layer's seven projections, the F.linear of femtotron's
+ * Column/RowParallelLinear at one rank (femtotron/parallel/tensor_parallel/
+ * linear.py:66-80 forward, :194-214; HF nn.Linear) in its three layouts:
+ *   FH_GEMM_NT  C[m,n] = sum_k A[m,k] B[n,k]   A [m,k], B [n,k]   y = x W^T
+ *   FH_GEMM_NN  C[m,n] = sum_k A[m,k] B[k,n]   A [m,k], B [k,n]   dx = dy W
+ *   FH_GEMM_TN  C[m,n] = sum_k A[k,m] B[k,n]   A [k,m], B [k,n]   dW = dy^T x
+ * bf16, row-major with leading dims lda/ldb/ldc (elements); fp32 accumulation,
+ * C rounded to bf16 once, as torch's bf16 matmul does.  If `residual` (bf16
+ * [m, n], row stride ldr) is given, C = to_bf16(residual + to_bf16(A.B)): the
+ * projection output rounded, then the residual add `hidden_states = residual +
+ * hidden_states` of modeling_llama.py:323 fused into the epilogue with its own
+ * rounding.  `residual` may be C itself (same ldc), any other overlap is not
+ * allowed.
+ * Requirements: k % 64 == 0; n % 8 == 0 (and m % 8 == 0 for FH_GEMM_TN); lda,
+ * ldb multiples of 8, ldc and ldr of 4; A and B 16-byte aligned, C and the
+ * residual 8-byte aligned; m, n, k < 2^30.
+ * When the output has few 256 x 256 tiles the k range is split into slices
+ * whose fp32 partial sums go to `workspace` (fh_gemm_bf16_workspace_size bytes;
+ * 0 = none needed) and are added in slice order, so results are bitwise
+ * deterministic.
  */
-size_t fh_gemm_tn_workspace_size(int64_t m, int64_t n, int64_t k);
-int fh_gemm_tn(fh_dtype dt, const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
-               int64_t ldc, int64_t m, int64_t n, int64_t k, void* workspace, hipStream_t stream);
+typedef enum fh_gemm_op {
+  FH_GEMM_NT = 0,
+  FH_GEMM_NN = 1,
+  FH_GEMM_TN = 2
+} fh_gemm_op;
+
+size_t fh_gemm_bf16_workspace_size(int op, int64_t m, int64_t n, int64_t k);
+int fh_gemm_bf16(int op, const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
+                 int64_t ldc, const void* residual, int64_t ldr, int64_t m, int64_t n,
+                 int64_t k, void* workspace, hipStream_t stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

@@ -201,3 +201,15 @@ def test_library_validates_arguments_on_host():
     assert L.fh_swiglu_fwd(0, None, None, 8, None, 8, 0, 8, None) == 0           # empty is a no-op
     assert L.fh_rmsnorm_bwd_workspace_size(0, 64) == 0
     assert L.fh_rmsnorm_bwd_workspace_size(16384, 2048) > 0
+    # projection GEMM: op, k % 64 and alignment are checked before any launch
+    assert L.fh_gemm_bf16(7, None, 64, None, 64, None, 64, None, 0, 64, 64, 64, None, None) == 1
+    assert b"op" in L.fh_last_error()
+    assert L.fh_gemm_bf16(_lib.FH_GEMM_NN, None, 96, None, 64, None, 64, None, 0, 64, 64, 96,
+                          None, None) == 1
+    assert b"multiple of 64" in L.fh_last_error()
+    assert L.fh_gemm_bf16(_lib.FH_GEMM_NT, None, 64, None, 64, None, 64, None, 0, 64, 64, 64,
+                          None, None) == 1  # null pointers
+    # a 512 x 512 weight gradient over 16384 tokens is split into k slices
+    assert L.fh_gemm_bf16_workspace_size(_lib.FH_GEMM_TN, 512, 512, 16384) > 0
+    assert L.fh_gemm_bf16_workspace_size(_lib.FH_GEMM_NT, 16384, 2048, 2048) == 0
+    assert L.fh_gemm_bf16_workspace_size(_lib.FH_GEMM_NT, 64, 64, 96) == 0

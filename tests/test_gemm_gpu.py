@@ -1,64 +1,138 @@
-"""Weight-gradient GEMM fh_gemm_tn (femtotron_amd/ops.py gemm_tn): C = A^T B.
+"""Projection GEMMs fh_gemm_bf16 (femtotron_amd/ops.py gemm): NT, NN and TN.
 
-Checker: the exact product of the same bf16 inputs in fp32 (torch on the GPU,
-fp32 inputs); the kernel accumulates in fp32 and rounds once, so every output
-must be within half a bf16 ulp of it plus the fp32 accumulation error (bound
-used: one bf16 ulp at 2^-8 relative, plus 1e-3 absolute for near-zero
-sums).  Shapes cover one slice (many output tiles) and the token-split path
-(few tiles: fp32 partials summed in slice order), and leading dimensions wider
-than the operand (column views of a packed buffer); results must be bitwise
-deterministic.  The reference path computes the same product with
-torch.mm(dY.t(), X) (F.linear's weight gradient) in bf16: within one bf16 ulp
-of it as well.
+Checked against a product of the same bf16 operands accumulated in fp32 (fp64
+for the small shapes): every output must lie within half a bf16 ulp of the
+exact value plus the accumulation bound K * 2^-24 * (|A| |B|) -- a correctly
+rounded fp32-accumulated product can be no further off; a dropped term, a
+wrong operand row or an untransposed layout is off by O(|A||B|/sqrt(K)).  The
+bound doubles where the reference itself is fp32.  Results must be bitwise
+identical between two launches (no atomics: split-K partials are summed in
+slice order).  Shapes: every projection GEMM of BASELINE configs 3/4/5 in all
+three layouts, plus ragged, strided and split-K cases.
 """
 from __future__ import annotations
 
 import pytest
 import torch
 
+from femtotron_amd import _lib, ops
+
 pytestmark = pytest.mark.gpu
-DEV = "cuda:0"
+
+DEV = "cuda"
+BF = torch.bfloat16
 
 
-def _check(a, b, c):
-    ref = torch.mm(a.float().t(), b.float())
-    bound = ref.abs() * 2.0 ** -8 + 1e-3
-    err = (c.float() - ref).abs()
-    assert bool((err <= bound).all()), f"max excess {float((err - bound).max()):.3e}"
-    lib = torch.mm(a.t(), b).float()
-    assert bool(((c.float() - lib).abs() <= lib.abs() * 2.0 ** -7 + 1e-3).all())
+def _ref(op, a, b, dtype):
+    x, y = a.to(dtype), b.to(dtype)
+    if op == "nt":
+        return x @ y.t(), x.abs() @ y.abs().t()
+    if op == "nn":
+        return x @ y, x.abs() @ y.abs()
+    return x.t() @ y, x.t().abs() @ y.abs()
 
 
-@pytest.mark.parametrize("k,m,n", [(64, 256, 256), (1024, 512, 768), (4096, 2560, 2048),
-                                   (16384, 2048, 2048), (8192, 11264, 2048), (2048, 256, 5632)])
-def test_gemm_tn_matches_fp32_product(k, m, n):
-    from femtotron_amd import ops
-    g = torch.Generator(device=DEV).manual_seed(k + m + n)
-    a = torch.randn(k, m, device=DEV, generator=g).bfloat16()
-    b = torch.randn(k, n, device=DEV, generator=g).bfloat16()
-    c = ops.gemm_tn(a, b)
-    _check(a, b, c)
-    assert torch.equal(c, ops.gemm_tn(a, b))  # deterministic, also on the split path
+def _check(op, a, b, c, *, exact=True):
+    """Error of c against the product, relative to the rounding + accumulation bound."""
+    m, n, k = ops.gemm_dims(op, a, b)
+    ref, absref = _ref(op, a, b, torch.float64 if exact else torch.float32)
+    ulp = torch.exp2(torch.floor(torch.log2(ref.abs().double().clamp_min(1e-300))) - 7)
+    tol = 0.5 * ulp * 1.0001 + (1 if exact else 2) * k * 2.0 ** -24 * absref.double()
+    ratio = ((c.double() - ref.double()).abs() / tol).max().item()
+    assert ratio <= 1.0, f"{op} {m}x{n}x{k}: error {ratio:.3f} x the bound"
+    return ratio
 
 
-def test_gemm_tn_strided_operands_and_slices():
-    """Operands as column views of wider buffers (lda, ldb > m, n), and the
-    slice count the host picks for this shape is > 1 (workspace used)."""
-    from femtotron_amd import _lib, ops
-    g = torch.Generator(device=DEV).manual_seed(3)
-    k, m, n = 8192, 512, 512
-    abuf = torch.randn(k, m + 256, device=DEV, generator=g).bfloat16()
-    bbuf = torch.randn(k, n + 512, device=DEV, generator=g).bfloat16()
-    a, b = abuf[:, 256:], bbuf[:, :n]
-    assert _lib.lib().fh_gemm_tn_workspace_size(m, n, k) > 0
-    _check(a, b, ops.gemm_tn(a, b))
+def _operands(op, m, n, k, g, pad=0):
+    def r(*s):
+        return torch.randn(*s, device=DEV, generator=g).to(BF)
+    if op == "nt":
+        return r(m, k + pad)[:, :k], r(n, k + pad)[:, :k]
+    if op == "nn":
+        return r(m, k + pad)[:, :k], r(k, n + pad)[:, :n]
+    return r(k, m + pad)[:, :m], r(k, n + pad)[:, :n]
 
 
-def test_gemm_tn_rejects_unsupported_shapes():
-    from femtotron_amd import ops
-    a = torch.zeros(64, 200, device=DEV, dtype=torch.bfloat16)
-    b = torch.zeros(64, 256, device=DEV, dtype=torch.bfloat16)
-    assert not ops.gemm_tn_supported(a, b)
+# (T, out, in) of the projection GEMMs: packed q/k/v, o, packed gate/up, down
+PROJECTIONS = {
+    "cfg3": (16384, [(2560, 2048), (2048, 2048), (11264, 2048), (2048, 5632)]),
+    "cfg4": (8192, [(6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)]),
+    "cfg5": (32768, [(12288, 4096), (4096, 4096), (22016, 4096), (4096, 11008)]),
+}
+CASES = [(cfg, T, o, i, op) for cfg, (T, shapes) in PROJECTIONS.items() for (o, i) in shapes
+         for op in ("nt", "nn", "tn")]
+
+
+@pytest.mark.parametrize("cfg,T,out_f,in_f,op", CASES,
+                         ids=[f"{c}-{o}x{i}-{op}" for c, _, o, i, op in CASES])
+def test_projection_gemm_matches_fp32_product(cfg, T, out_f, in_f, op):
+    g = torch.Generator(device=DEV).manual_seed(out_f * 7 + in_f)
+    x = torch.randn(T, in_f, device=DEV, generator=g).to(BF)
+    w = torch.randn(out_f, in_f, device=DEV, generator=g).to(BF)
+    dy = torch.randn(T, out_f, device=DEV, generator=g).to(BF)
+    a, b = {"nt": (x, w), "nn": (dy, w), "tn": (dy, x)}[op]
+    c = ops.gemm(op, a, b)
+    _check(op, a, b, c, exact=False)
+    assert torch.equal(c, ops.gemm(op, a, b)), "not bitwise deterministic"
+
+
+SMALL = [(256, 256, 64, 0), (512, 768, 256, 8), (264, 520, 192, 0), (1000, 264, 128, 8),
+         (256, 2048, 16384, 0), (8, 8, 64, 0), (2048, 2048, 4096, 0), (24, 1032, 640, 16)]
+
+
+@pytest.mark.parametrize("op", ["nt", "nn", "tn"])
+@pytest.mark.parametrize("m,n,k,pad", SMALL)
+def test_gemm_ragged_strided_split(op, m, n, k, pad):
+    if op == "tn" and m % 8:
+        pytest.skip("FH_GEMM_TN needs m % 8 == 0")
+    g = torch.Generator(device=DEV).manual_seed(m + 3 * n + 7 * k)
+    a, b = _operands(op, m, n, k, g, pad)
+    c = ops.gemm(op, a, b)
+    _check(op, a, b, c, exact=True)
+    assert torch.equal(c, ops.gemm(op, a, b))
+
+
+def test_split_k_path_is_used_and_matches():
+    # 512 x 512 outputs are 4 tiles: the k range is split into slices
+    m = n = 512
+    k = 16384
+    assert _lib.lib().fh_gemm_bf16_workspace_size(_lib.FH_GEMM_TN, m, n, k) > 0
+    g = torch.Generator(device=DEV).manual_seed(5)
+    a, b = _operands("tn", m, n, k, g)
+    c = ops.gemm("tn", a, b)
+    _check("tn", a, b, c, exact=True)
+    assert torch.equal(c, ops.gemm("tn", a, b))
+
+
+@pytest.mark.parametrize("op", ["nt", "nn", "tn"])
+@pytest.mark.parametrize("m,n,k", [(512, 768, 256), (264, 520, 192), (512, 512, 16384)])
+def test_residual_epilogue_rounds_like_the_unfused_add(op, m, n, k):
+    """C = to_bf16(R + to_bf16(A.B)) -- the projection output rounded, then the
+    residual add of modeling_llama.py:323 rounded again -- bit for bit."""
+    g = torch.Generator(device=DEV).manual_seed(m + n)
+    a, b = _operands(op, m, n, k, g)
+    r = torch.randn(m, n, device=DEV, generator=g).to(BF)
+    fused = ops.gemm(op, a, b, residual=r)
+    unfused = (r.float() + ops.gemm(op, a, b).float()).to(BF)
+    assert torch.equal(fused, unfused)
+    inplace = r.clone()
+    ops.gemm(op, a, b, residual=inplace, out=inplace)
+    assert torch.equal(inplace, fused)
+
+
+def test_gemm_rejects_unsupported_operands():
+    a = torch.randn(128, 96, device=DEV).to(BF)  # k = 96 is not a multiple of 64
+    b = torch.randn(256, 96, device=DEV).to(BF)
+    assert not ops.gemm_supported("nt", a, b)
     with pytest.raises(ValueError):
-        ops.gemm_tn(a, b)
-    assert not ops.gemm_tn_supported(b.float(), b.float())
+        ops.gemm("nt", a, b)
+    assert not ops.gemm_supported("nt", a.float(), b.float())
+    x = torch.randn(256, 128, device=DEV).to(BF)
+    assert not ops.gemm_supported("tn", x[:, :100], x)  # m % 8 for TN
+    # the C ABI itself refuses bad arguments with a message, never aborts
+    st = _lib.lib().fh_gemm_bf16(7, x.data_ptr(), 128, x.data_ptr(), 128, x.data_ptr(), 128, None, 0,
+                                 128, 128, 128, None, None)
+    assert st == 1 and b"op" in _lib.lib().fh_last_error()
+    st = _lib.lib().fh_gemm_bf16(_lib.FH_GEMM_NT, x.data_ptr(), 128, x.data_ptr(), 128, x.data_ptr(),
+                                 128, None, 0, 128, 128, 96, None, None)
+    assert st == 1 and b"multiple of 64" in _lib.lib().fh_last_error()
