@@ -41,6 +41,8 @@ SIGNATURES: dict[str, tuple] = {
     "fh_add_rmsnorm_fwd": (c_int, [c_int, _V, _V, _V, _V, _V, POINTER(c_float), _I64, _I64, _F, _V]),
     "fh_rmsnorm_bwd_workspace_size": (c_size_t, [_I64, _I64]),
     "fh_rmsnorm_bwd": (c_int, [c_int, _V, _V, _V, POINTER(c_float), _V, _V, _V, _V, _I64, _I64, _F, _V]),
+    "fh_rmsnorm_bwd_noalloc_max_workspace": (c_size_t, []),
+    "fh_rmsnorm_bwd_noalloc": (c_int, [c_int, _V, _V, _V, POINTER(c_float), _V, _V, _V, _I64, _I64, _F, _V]),
     "fh_rope_fwd": (c_int, [c_int, _V, _I64, _I64, _I64, _I64, _I64, _V, _V, c_int, _V]),
     "fh_rope_bwd": (c_int, [c_int, _V, _I64, _I64, _I64, _I64, _I64, _V, _V, c_int, _V]),
     "fh_swiglu_fwd": (c_int, [c_int, _V, _V, _I64, _V, _I64, _I64, _I64, _V]),

@@ -11,6 +11,8 @@
 // with the first data, so its latency is never on a row's critical path.
 #include "fh_common.hpp"
 
+#include <mutex>
+
 namespace fh {
 namespace {
 
@@ -448,6 +450,45 @@ extern "C" size_t fh_rmsnorm_bwd_workspace_size(int64_t rows, int64_t cols) {
   return static_cast<size_t>(nrows) * static_cast<size_t>(cols) * sizeof(float);
 }
 
+namespace fh {
+namespace {
+
+// Scratch of the allocation-free backward: the fp32 partial rows of the
+// largest valid call (kMaxBwdBlocks partial rows + kReduceGroups stage rows of
+// at most 8192 columns), 17.3 MB per device, held until the process ends.
+constexpr size_t kNoAllocScratchFloats = static_cast<size_t>(kMaxBwdBlocks + kReduceGroups) * 8192;
+__device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+// Device address of `scratch` on the current device, looked up once per
+// device (each device holds its own copy of the array at its own address;
+// the host-side symbol is only a stand-in and must never reach a kernel).
+float* scratch_on_current_device(int* status) {
+  constexpr int kMaxDevices = 64;
+  static std::once_flag once[kMaxDevices];
+  static float* addr[kMaxDevices] = {};
+  static hipError_t err[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    *status = fail(FH_ERR_LAUNCH, "rmsnorm_bwd_noalloc: no current HIP device");
+    return nullptr;
+  }
+  std::call_once(once[dev], [dev]() {
+    void* p = nullptr;
+    err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    addr[dev] = static_cast<float*>(p);
+  });
+  if (err[dev] != hipSuccess || addr[dev] == nullptr) {
+    *status = fail(FH_ERR_LAUNCH, std::string("rmsnorm_bwd_noalloc: hipGetSymbolAddress failed: ") +
+                                      hipGetErrorString(err[dev]));
+    return nullptr;
+  }
+  *status = FH_OK;
+  return addr[dev];
+}
+
+}  // namespace
+}  // namespace fh
+
 extern "C" int fh_rmsnorm_bwd(fh_dtype dt, const void* dy, const void* x, const void* w,
                               const float* rstd, const void* dres, void* dx, void* dw,
                               void* workspace, int64_t rows, int64_t cols, float eps,
@@ -478,4 +519,22 @@ extern "C" int fh_rmsnorm_bwd(fh_dtype dt, const void* dy, const void* x, const 
     return 0;
   });
   return check_launch("fh_rmsnorm_bwd");
+}
+
+extern "C" size_t fh_rmsnorm_bwd_noalloc_max_workspace(void) {
+  return kNoAllocScratchFloats * sizeof(float);
+}
+
+extern "C" int fh_rmsnorm_bwd_noalloc(fh_dtype dt, const void* dy, const void* x, const void* w,
+                                      const float* rstd, const void* dres, void* dx, void* dw,
+                                      int64_t rows, int64_t cols, float eps, hipStream_t stream) {
+  if (int e = validate_rows(dt, rows, cols)) return e;
+  FH_REQUIRE(fh_rmsnorm_bwd_workspace_size(rows, cols) <= kNoAllocScratchFloats * sizeof(float),
+             "rmsnorm_bwd_noalloc: the call needs more scratch than the library holds");
+  if (rows == 0)  // no scratch needed: dw = 0
+    return fh_rmsnorm_bwd(dt, dy, x, w, rstd, dres, dx, dw, nullptr, rows, cols, eps, stream);
+  int status = FH_OK;
+  float* ws = scratch_on_current_device(&status);
+  if (ws == nullptr) return status;
+  return fh_rmsnorm_bwd(dt, dy, x, w, rstd, dres, dx, dw, ws, rows, cols, eps, stream);
 }

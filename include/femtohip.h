@@ -91,6 +91,25 @@ int fh_rmsnorm_bwd(fh_dtype dt, const void* dy, const void* x, const void* w,
                    void* workspace, int64_t rows, int64_t cols, float eps,
                    hipStream_t stream);
 
+/* fh_rmsnorm_bwd without a workspace argument.  No counterpart in the
+ * reference (whose RMSNorm backward is autograd over aten ops): it is for
+ * callers that cannot allocate device memory -- code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc.  Same arguments,
+ * results (bit for bit) and errors as fh_rmsnorm_bwd; the fp32 partial rows go
+ * to a scratch array the library holds in device memory, one per device
+ * (fh_rmsnorm_bwd_noalloc_max_workspace() bytes, 17.3 MB, enough for every
+ * valid rows x cols since cols <= 8192), kept until the process ends.  Calls
+ * no allocating routine.  All calls on one device share that scratch: calls
+ * that may overlap on one device (different streams, or different host
+ * threads, without ordering between them) race and must be serialised by the
+ * caller.  The first call on each device looks up the scratch's device
+ * address (hipGetSymbolAddress) once.
+ */
+size_t fh_rmsnorm_bwd_noalloc_max_workspace(void);
+int fh_rmsnorm_bwd_noalloc(fh_dtype dt, const void* dy, const void* x, const void* w,
+                           const float* rstd, const void* dres, void* dx, void* dw,
+                           int64_t rows, int64_t cols, float eps, hipStream_t stream);
+
 /* --------------------------------------------------------------------- RoPE
  * In-place rotate-half rotary embedding, replacing apply_rotary_pos_emb +
  * rotate_half (modeling_llama.py:130-160) for q and k together:
