@@ -213,3 +213,31 @@ def test_library_validates_arguments_on_host():
     assert L.fh_gemm_bf16_workspace_size(_lib.FH_GEMM_TN, 512, 512, 16384) > 0
     assert L.fh_gemm_bf16_workspace_size(_lib.FH_GEMM_NT, 16384, 2048, 2048) == 0
     assert L.fh_gemm_bf16_workspace_size(_lib.FH_GEMM_NT, 64, 64, 96) == 0
+
+
+def test_linear_weight_accepts_tensor_parallel_wrappers_at_world_size_1():
+    """The dispatcher takes femtotron's Column/RowParallelLinear at one rank
+    (tensor_parallel/linear.py:42-64, 170-191: weight, bias, world_size,
+    gather_output / scatter_input) and refuses them otherwise."""
+    import torch
+    from femtotron_amd.fused_checkpoint import _linear_weight
+
+    class Col(torch.nn.Module):
+        def __init__(self, ws=1, gather=False, bias=False):
+            super().__init__()
+            self.weight = torch.nn.Parameter(torch.zeros(4, 8))
+            self.bias = torch.nn.Parameter(torch.zeros(4)) if bias else None
+            self.world_size, self.rank, self.gather_output = ws, 0, gather
+
+    class Row(torch.nn.Module):
+        def __init__(self, ws=1, scatter=False):
+            super().__init__()
+            self.weight = torch.nn.Parameter(torch.zeros(8, 4))
+            self.bias = None
+            self.world_size, self.rank, self.scatter_input = ws, 0, scatter
+
+    assert _linear_weight(Col()) is not None and _linear_weight(Row()) is not None
+    assert _linear_weight(torch.nn.Linear(8, 4, bias=False)) is not None
+    for bad in (Col(ws=2), Col(gather=True), Col(bias=True), Row(ws=2), Row(scatter=True),
+                torch.nn.Linear(8, 4)):
+        assert _linear_weight(bad) is None
