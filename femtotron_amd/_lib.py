@@ -31,7 +31,7 @@ _F = c_float
 class FhAdamHyper(ctypes.Structure):
     """FhAdamHyper of include/femtohip.h (passed by value to fh_adamw_step)."""
     _fields_ = [("one_minus_beta1", c_float), ("beta2", c_float), ("one_minus_beta2", c_float),
-                ("eps", c_float), ("step_size", c_float), ("bias_correction2_sqrt", c_float)]
+                ("eps", c_float)]
 
 # name -> (restype, argtypes); mirrors include/femtohip.h exactly.
 SIGNATURES: dict[str, tuple] = {

@@ -155,8 +155,8 @@ __global__ __launch_bounds__(kAdamThreads) void k_adamw(const FhAdamTensor* __re
     p *= t.decay;                                               // mul_(1 - lr*wd)
     m = m + hp.one_minus_beta1 * (gj - m);                      // lerp_(g, 1 - beta1)
     v = __fmul_rn(v, hp.beta2) + hp.one_minus_beta2 * gj * gj;  // mul_(beta2).addcmul_(g, g, 1 - beta2)
-    const float denom = sqrtf(v) / hp.bias_correction2_sqrt + hp.eps;
-    p = p - hp.step_size * (m / denom);                         // addcdiv_(m, denom, -step_size)
+    const float denom = sqrtf(v) / t.bias_correction2_sqrt + hp.eps;
+    p = p - t.step_size * (m / denom);                          // addcdiv_(m, denom, -step_size)
   };
   if (i + 8 <= t.numel) {
     float g[8], p[8], m[8], v[8];
@@ -201,7 +201,6 @@ extern "C" int fh_adamw_step(fh_dtype dt, const FhAdamTensor* table, const int64
   if (n_tensors == 0 || total_chunks == 0) return FH_OK;
   FH_REQUIRE(table && chunk_start && workspace, "adamw_step: null pointer");
   FH_REQUIRE(total_chunks <= 0x7fffffff, "adamw_step: too many chunks");
-  FH_REQUIRE(hyper.bias_correction2_sqrt > 0.f, "adamw_step: bias_correction2_sqrt must be > 0");
   float* part = static_cast<float*>(workspace);
   float* coef = part + total_chunks;  // coef, norm
   float* folded = coef + 2;

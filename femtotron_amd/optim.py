@@ -33,7 +33,8 @@ CHUNK = 2048  # elements per workgroup of fh_adamw_step
 class _Tensor(ctypes.Structure):
     _fields_ = [("param", ctypes.c_void_p), ("grad", ctypes.c_void_p), ("master", ctypes.c_void_p),
                 ("exp_avg", ctypes.c_void_p), ("exp_avg_sq", ctypes.c_void_p),
-                ("numel", ctypes.c_int64), ("decay", ctypes.c_float), ("reserved", ctypes.c_float)]
+                ("numel", ctypes.c_int64), ("decay", ctypes.c_float), ("step_size", ctypes.c_float),
+                ("bias_correction2_sqrt", ctypes.c_float), ("reserved", ctypes.c_float)]
 
 
 def get_param_groups(model: torch.nn.Module, weight_decay: float = 0.01) -> list[dict]:
@@ -63,7 +64,14 @@ class FusedAdamW(torch.optim.Optimizer):
     device in one dtype (bf16 or fp32) and be contiguous and 16-byte aligned; at a
     step every group must have the same lr, betas and eps (weight decay may differ).
     ``max_grad_norm`` <= 0 or None disables clipping.  Per-parameter state:
-    ``master``, ``exp_avg``, ``exp_avg_sq`` (fp32), created at construction."""
+    ``master``, ``exp_avg``, ``exp_avg_sq`` (fp32), created at construction, and
+    ``step``, the number of steps that updated the parameter; each tensor's bias
+    corrections follow its own count (as torch.optim.AdamW's per-parameter
+    ``step``).  A parameter without ``.grad`` takes the step with a zero
+    gradient, as the reference's MixedPrecisionManager.copy_grads_to_master
+    fills missing gradients with zeros before the inner optimizer's step
+    (femtotron/training/mixed_precision_manager.py:224-229), so every
+    parameter steps every time, as there."""
 
     def __init__(self, params: Iterable, lr: float = 1e-4, betas=(0.9, 0.95), eps: float = 1e-8,
                  weight_decay: float = 0.0, max_grad_norm: float | None = 1.0):
@@ -83,11 +91,12 @@ class FusedAdamW(torch.optim.Optimizer):
                 if not p.is_contiguous() or not _aligned(p):
                     raise ValueError("FusedAdamW: parameters must be contiguous and 16-byte aligned")
                 master = p.detach().float().clone()
-                self.state[p] = {"master": master, "exp_avg": torch.zeros_like(master),
+                self.state[p] = {"step": 0, "master": master, "exp_avg": torch.zeros_like(master),
                                  "exp_avg_sq": torch.zeros_like(master)}
         self.dtype, self.device = dtype, device
         self.grad_norm: torch.Tensor | None = None
         self._cache = None  # (table bytes, device table, device chunk_start, total chunks)
+        self._staging = [None, None]  # two pinned upload buffers, used alternately
 
     @property
     def entries(self) -> list[tuple[torch.Tensor, float, torch.Tensor, torch.Tensor, torch.Tensor]]:
@@ -111,52 +120,67 @@ class FusedAdamW(torch.optim.Optimizer):
                 raise ValueError("FusedAdamW: all parameter groups must share lr, betas and eps")
         return float(lr), float(b1), float(b2), float(eps)
 
-    def _device_table(self, live: list, lr: float) -> tuple[torch.Tensor, torch.Tensor, int]:
-        """The tensor table and chunk prefix sums on the device.  Rebuilt only
-        when a gradient pointer, the live set or the learning rate changed (with
-        the caching allocator, gradients usually come back at the same addresses
-        step after step); a rebuild goes through pinned memory without blocking
-        the host on the stream."""
+    def _device_table(self, live: list, grads: list, lr: float, b1: float, b2: float
+                      ) -> tuple[torch.Tensor, torch.Tensor, int]:
+        """The tensor table and chunk prefix sums on the device, for the step
+        that is about to run (each live parameter's step count already
+        incremented).  Uploaded through one of two pinned buffers used in turn,
+        without blocking the host on the stream; a buffer is reused only after
+        the copy that last read it has completed."""
         table = (_Tensor * len(live))()
         starts = [0]
-        for i, (p, wd, master, m, v) in enumerate(live):
-            g = p.grad
+        for i, ((p, wd, master, m, v), g) in enumerate(zip(live, grads)):
             if g.dtype != p.dtype or not g.is_contiguous() or not _aligned(g) or g.shape != p.shape \
                     or g.device != p.device:
                 raise ValueError("FusedAdamW: gradients must be contiguous, aligned, of the parameter's "
                                  "dtype, shape and device")
+            t = self.state[p]["step"]
+            # torch.optim.AdamW (single-tensor and foreach): bias corrections in
+            # double precision on the host, step_size = lr / bias_correction1
+            step_size = lr / (1.0 - b1 ** t)
+            bc2_sqrt = math.sqrt(1.0 - b2 ** t)
             table[i] = _Tensor(p.data_ptr(), g.data_ptr(), master.data_ptr(), m.data_ptr(), v.data_ptr(),
-                               p.numel(), 1.0 - lr * wd, 0.0)
+                               p.numel(), 1.0 - lr * wd, step_size, bc2_sqrt, 0.0)
             starts.append(starts[-1] + (p.numel() + CHUNK - 1) // CHUNK)
         key = bytes(table)
+        n_tab, n_cs = len(key), 8 * len(starts)
         if self._cache is None or self._cache[0] != key:
-            n_tab, n_cs = len(key), 8 * len(starts)
-            host = torch.empty(n_tab + n_cs, dtype=torch.uint8, pin_memory=True)
+            slot = self._staging.pop(0)
+            if slot is None or slot[0].numel() < n_tab + n_cs:
+                host = torch.empty(n_tab + n_cs, dtype=torch.uint8, pin_memory=True)
+                slot = (host, torch.cuda.Event())
+            else:
+                slot[1].synchronize()  # the upload that last read this buffer is done
+            host = slot[0]
             ctypes.memmove(host.data_ptr(), key, n_tab)
             ctypes.memmove(host.data_ptr() + n_tab, (ctypes.c_int64 * len(starts))(*starts), n_cs)
-            dev = host.to(self.device, non_blocking=True)
+            dev = host[:n_tab + n_cs].to(self.device, non_blocking=True)
+            slot[1].record(torch.cuda.current_stream(self.device))
+            self._staging.append(slot)
             self._cache = (key, dev[:n_tab], dev[n_tab:], starts[-1])
         return self._cache[1], self._cache[2], self._cache[3]
 
     @torch.no_grad()
     def step(self, closure=None):
-        """One optimizer step on every parameter that has a gradient (all in one
-        ``fh_adamw_step`` call).  ``grad_norm`` then holds the pre-clipping
+        """One optimizer step on every parameter (all in one ``fh_adamw_step``
+        call; a missing gradient counts as zeros).  ``grad_norm`` then holds the pre-clipping
         global gradient norm as a device scalar."""
         loss = None
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
-        live = [e for e in self.entries if e[0].grad is not None]
+        live = self.entries
         if not live:
             return loss
+        grads = [e[0].grad if e[0].grad is not None else torch.zeros_like(e[0]) for e in live]
         lr, b1, b2, eps = self._hyper()
-        tab, chunk_start, total = self._device_table(live, lr)
         self.step_count += 1
+        for e in live:
+            self.state[e[0]]["step"] += 1
+        tab, chunk_start, total = self._device_table(live, grads, lr, b1, b2)
         ws = torch.empty(max(_lib.lib().fh_adamw_workspace_size(total), 4) // 4, dtype=torch.float32,
                          device=self.device)
-        t = self.step_count
-        hyper = FhAdamHyper(1.0 - b1, b2, 1.0 - b2, eps, lr / (1.0 - b1 ** t), math.sqrt(1.0 - b2 ** t))
+        hyper = FhAdamHyper(1.0 - b1, b2, 1.0 - b2, eps)
         dt = 0 if self.dtype == torch.bfloat16 else 1
         stream = torch.cuda.current_stream(self.device).cuda_stream
         _lib.call("fh_adamw_step", dt, tab.data_ptr(), chunk_start.data_ptr(), len(live), total,
@@ -165,8 +189,9 @@ class FusedAdamW(torch.optim.Optimizer):
         return loss
 
     def state_dict(self) -> dict:
-        """torch's optimizer format (state by parameter index, param_groups)
-        plus ``fused_step``, the step count used for bias correction."""
+        """torch's optimizer format (state by parameter index, param_groups:
+        per parameter ``step``, ``master``, ``exp_avg``, ``exp_avg_sq``) plus
+        ``fused_step``, the number of ``step()`` calls."""
         sd = super().state_dict()
         sd["fused_step"] = self.step_count
         return sd
@@ -187,4 +212,6 @@ class FusedAdamW(torch.optim.Optimizer):
                 st = state_dict["state"][idx]
                 for k in ("master", "exp_avg", "exp_avg_sq"):
                     self.state[p][k].copy_(st[k])
+                self.state[p]["step"] = int(st.get("step", state_dict.get("fused_step", 0)))
         self.step_count = int(state_dict.get("fused_step", 0))
+        self._cache = None

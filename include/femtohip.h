@@ -221,8 +221,10 @@ int fh_ce_fwd_bwd(fh_dtype dt, void* logits, int64_t ld, const int64_t* labels, 
  * device int64 [n_tensors + 1], chunk_start[i] = sum over j < i of
  * ceil(numel_j / 2048), chunk_start[n] = total_chunks.  All pointers 16-byte
  * aligned; param/grad in dt (FH_BF16 or FH_F32), the rest fp32.
- * hyper: per-step scalars (step_size = lr / (1 - beta1^step),
- * bias_correction2_sqrt = sqrt(1 - beta2^step)); per-tensor decay = 1 - lr * wd.
+ * hyper: the betas and eps.  Per tensor: decay = 1 - lr * wd and the bias
+ * corrections of the tensor's own step count t (torch.optim.AdamW counts steps
+ * per parameter, skipping parameters without a gradient): step_size =
+ * lr / (1 - beta1^t), bias_correction2_sqrt = sqrt(1 - beta2^t).
  * max_grad_norm <= 0 disables clipping.  workspace: fh_adamw_workspace_size
  * bytes; after the call it holds, at float index total_chunks, the clipping
  * coefficient and then the gradient norm (before clipping).
@@ -234,7 +236,9 @@ typedef struct {
   float* exp_avg;         /* fp32 first moment */
   float* exp_avg_sq;      /* fp32 second moment */
   int64_t numel;
-  float decay;            /* 1 - lr * weight_decay of this tensor's group */
+  float decay;                  /* 1 - lr * weight_decay of this tensor's group */
+  float step_size;              /* lr / (1 - beta1^t), t = this tensor's step */
+  float bias_correction2_sqrt;  /* sqrt(1 - beta2^t), > 0 */
   float reserved;
 } FhAdamTensor;
 
@@ -243,8 +247,6 @@ typedef struct {
   float beta2;
   float one_minus_beta2;
   float eps;
-  float step_size;
-  float bias_correction2_sqrt;
 } FhAdamHyper;
 
 size_t fh_adamw_workspace_size(int64_t total_chunks);

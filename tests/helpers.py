@@ -86,8 +86,10 @@ def assert_close(a: torch.Tensor, b: torch.Tensor, rtol: float, atol: float, nam
 
 
 def assert_tensor_close(a: torch.Tensor, b: torch.Tensor, rtol: float, atol: float, name: str = "") -> None:
-    """The reference's implementation-vs-implementation metric, per tensor:
-    max|a-b| <= atol + rtol * max|b| (femtotron/test/unit/test_pipeline_stage.py:82-128)."""
+    """Per tensor max|a-b| <= atol + rtol * max|b|: the form of the reference's
+    compare_grads (femtotron/test/unit/test_pipeline_stage.py:82-128, rtol
+    1.5e-3 there, for paths with identical arithmetic); callers pass the north
+    star's rtol 2e-2 / atol 2e-3 for independent bf16 implementations."""
     a = a.detach().float().cpu()
     b = b.detach().float().cpu()
     assert a.shape == b.shape, f"{name}: shape {tuple(a.shape)} vs {tuple(b.shape)}"

@@ -59,9 +59,10 @@ def _oracle_layer(c, B, S, dtype, *, norm_mean=1.0, seed=42):
 
 
 def _compare(got, ref, rtol, atol, tag):
-    """Per tensor, the reference's own implementation-vs-implementation metric
-    max|a-b| <= atol + rtol*max|b| (femtotron/test/unit/test_pipeline_stage.py:82-128)
-    with the north star's rtol 2e-2 / atol 2e-3.  An element-wise bound cannot be
+    """Per tensor max|a-b| <= atol + rtol*max|b|, the form of the reference's
+    compare_grads (femtotron/test/unit/test_pipeline_stage.py:82-128, whose rtol
+    1.5e-3 is for paths running identical arithmetic), with the north star's
+    rtol 2e-2 / atol 2e-3 for two independent bf16 implementations.  An element-wise bound cannot be
     the bar in bf16: the reference's own bf16 path differs from the exact math of
     the same layer by several times its magnitude on entries near zero (outputs
     and input grads are sums such as x + attn(x) that cancel, weight grads are

@@ -136,7 +136,8 @@ def test_fused_adamw_on_a_model_step():
         assert torch.equal(p, m.to(torch.bfloat16))
     # resume: the state of step 4, then step 5 twice from it
     saved = {k: v for k, v in opt.state_dict().items()}
-    saved["state"] = {i: {k: t.clone() for k, t in st.items()} for i, st in saved["state"].items()}
+    saved["state"] = {i: {k: t.clone() if torch.is_tensor(t) else t for k, t in st.items()}
+                      for i, st in saved["state"].items()}
     params0 = [p.detach().clone() for p in model.parameters()]
     train_step()
     after = [p.detach().clone() for p in model.parameters()]
@@ -148,3 +149,74 @@ def test_fused_adamw_on_a_model_step():
     train_step()
     for p, a in zip(model.parameters(), after):
         assert torch.equal(p, a)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_parameter_without_grad_steps_like_the_reference(dtype):
+    """Three steps where one parameter has no gradient on step 2: the
+    reference's MixedPrecisionManager fills it with zeros before
+    torch.optim.AdamW's step (mixed_precision_manager.py:224-229), so the
+    parameter still decays and its moments and step count advance; the fused
+    step must match that sequence, bias corrections included."""
+    from femtotron_amd.optim import FusedAdamW
+    ps_f, groups_f = _setup(dtype, 3)
+    ps_r, groups_r = _setup(dtype, 3)
+    kw = dict(lr=3e-3, betas=(0.9, 0.95), eps=1e-8)
+    fused = FusedAdamW(groups_f, max_grad_norm=1.0, **kw)
+    masters_r = [p.detach().float().clone().requires_grad_(True) for p in ps_r]
+    mgroups = [{"params": [m for m, p in zip(masters_r, ps_r) if any(p is q for q in g["params"])],
+                "weight_decay": g["weight_decay"]} for g in groups_r]
+    ref = torch.optim.AdamW(mgroups, foreach=True, **kw)
+    gen = torch.Generator().manual_seed(9)
+    skip = 0  # the [256, 688] weight (weight-decay group) has no gradient on step 2
+    for step in range(3):
+        grads = [torch.randn(*s, generator=gen) for s in SHAPES]
+        for i, (pf, pr, gr) in enumerate(zip(ps_f, ps_r, grads)):
+            if step == 1 and i == skip:
+                pf.grad = None
+                pr.grad = torch.zeros_like(pr)  # the reference's zeros_like fill
+            else:
+                pf.grad = gr.to(DEV, dtype)
+                pr.grad = gr.to(DEV, dtype)
+        fused.step()
+        _reference_step(ps_r, masters_r, ref, 1.0)
+        by_param = {id(e[0]): e for e in fused.entries}
+        for pf, pr, mr in zip(ps_f, ps_r, masters_r):
+            p, _, m, e1, e2 = by_param[id(pf)]
+            st = ref.state[mr]
+            assert fused.state[pf]["step"] == int(st["step"]) == step + 1
+            for a, b, n in ((m, mr, "master"), (e1, st["exp_avg"], "exp_avg"), (e2, st["exp_avg_sq"], "exp_avg_sq")):
+                b = b.detach()
+                err = float((a - b).abs().max())
+                assert err <= 1e-6 * float(b.abs().max()) + 1e-12, f"step {step} {n}: {err:.3e}"
+
+
+def test_per_tensor_step_counts_after_restore():
+    """Tensors whose restored step counts differ get their own bias
+    corrections: state with steps (5, 1) then one step equals torch AdamW
+    restored to the same per-parameter state."""
+    from femtotron_amd.optim import FusedAdamW
+    g = torch.Generator().manual_seed(4)
+    shapes = [(64, 40), (96,)]
+    ps = [torch.randn(*s, generator=g).mul_(0.02).to(DEV, torch.float32) for s in shapes]
+    masters = [p.detach().clone().requires_grad_(True) for p in ps]
+    kw = dict(lr=1e-2, betas=(0.9, 0.95), eps=1e-8)
+    fused = FusedAdamW([{"params": ps, "weight_decay": 0.1}], max_grad_norm=0.0, **kw)
+    ref = torch.optim.AdamW([{"params": masters, "weight_decay": 0.1}], foreach=False, **kw)
+    m1 = [torch.randn(*s, generator=g).mul_(0.01) for s in shapes]
+    m2 = [torch.randn(*s, generator=g).abs().mul_(1e-4) for s in shapes]
+    sd = fused.state_dict()
+    for i, steps in enumerate((5, 1)):
+        sd["state"][i] = {"step": steps, "master": ps[i].detach().float().clone(),
+                          "exp_avg": m1[i].to(DEV), "exp_avg_sq": m2[i].to(DEV)}
+        ref.state[masters[i]] = {"step": torch.tensor(float(steps)), "exp_avg": m1[i].to(DEV).clone(),
+                                 "exp_avg_sq": m2[i].to(DEV).clone()}
+    fused.load_state_dict(sd)
+    grads = [torch.randn(*s, generator=g).to(DEV) for s in shapes]
+    for p, m, gr in zip(ps, masters, grads):
+        p.grad = gr.clone()
+        m.grad = gr.clone()
+    fused.step()
+    ref.step()
+    for p, m in zip(ps, masters):
+        assert float((p - m.detach()).abs().max()) <= 1e-6 * float(m.detach().abs().max())
