@@ -35,13 +35,20 @@ COMMON_FLAGS = [
     "-Wno-unused-function",
     # Packed fp32 (v_pk_*_f32) code generation stays off for all device code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # MFMA accumulators in VGPRs: the attention softmax rescales its output
-    # accumulators every key block, which in AGPRs costs a read and a write
-    # per register per block.
-    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]
+
+# MFMA accumulators in VGPRs: the attention softmax rescales its output
+# accumulators every key block, which in AGPRs costs a read and a write per
+# register per block.  The GEMM keeps its 256 accumulator registers per lane in
+# AGPRs (one wave per SIMD, 128 x 128 outputs each), so it is built without.
+VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+AGPR_FORM_SOURCES = {"fh_gemm.hip"}
+
+
+def flags_for(src: Path) -> list:
+    return COMMON_FLAGS + ([] if src.name in AGPR_FORM_SOURCES else VGPR_FORM)
 
 
 def hipcc() -> str:
@@ -53,7 +60,7 @@ def hipcc() -> str:
 
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, "-x", "hip", "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *flags_for(src), "-x", "hip", "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stdout}\n{res.stderr}")

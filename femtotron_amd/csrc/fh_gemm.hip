@@ -10,11 +10,18 @@
 //   TN  C = A^T B  (A [K, M], B [K, N])  weight gradient:    dY^T X
 // All operands are row-major with a leading dimension (elements).
 //
-// Block tile 256 (m) x 256 (n), stages of 64 k.  Operand stages go straight
-// from global memory into LDS (global_load_lds_dwordx4, two stages of 64 KB:
-// A and B, 32 KB each); every load covers whole 128-byte lines (half-line
-// requests cost a full line's L2 and DRAM throughput).  Tiles are
-// XOR-swizzled so that both read patterns below are free of bank conflicts:
+// Block tile 256 (m) x 256 (n), stages of 64 k, four waves (one per SIMD),
+// each owning a 128 x 128 part of the tile in 16 AGPR accumulators of
+// v_mfma_f32_32x32x16_bf16.  Operands go straight from global memory into LDS
+// (global_load_lds_dwordx4, 1 KB per instruction; every load covers whole
+// 128-byte lines, as half-line requests cost a full line's L2 and DRAM
+// throughput).  LDS holds a ring of five operand slots (A or B of one stage,
+// 32 KB each: 160 KB), so the loads of stage x+2 can start while stage x is
+// multiplied and are spread over its 64 MFMAs: the load instructions issue at
+// ~1 KB per 16 cycles per CU, and a burst of them right after a barrier would
+// hold up the MFMAs behind it.  Fragments are read from LDS one k16 step ahead
+// of the MFMAs that use them.  Tiles are XOR-swizzled so that both read
+// patterns are free of bank conflicts:
 //   * an operand with K contiguous ("KC": A of NT/NN, B of NT) is stored as
 //     its [256 x 64] tile; a fragment is one ds_read_b128 per lane (row i%32,
 //     k 8*(i/32)..+7);
@@ -22,15 +29,9 @@
 //     stored as four [64 k x 64] sub-tiles; a fragment is two
 //     ds_read_b64_tr_b16 transposing reads that deliver the same natural K
 //     order, so any two operands can be paired.
-// Eight waves, two per SIMD, each own a 128 (m) x 64 (n) part of the tile (8
-// accumulators of v_mfma_f32_32x32x16_bf16).  The two waves of a SIMD take
-// turns ("ping-pong"): while one multiplies 32 k of a stage out of registers,
-// the other reads its fragments of the next 32 k from LDS and issues the
-// global loads of the next stage; a workgroup barrier ends each half-period.
-// Waves 4-7 start one half-period late.
-//
 // The MFMA is issued as (B fragment, A fragment), so accumulator rows run
-// along n (C's contiguous index) and every lane stores 4 consecutive outputs.
+// along n (C's contiguous index).  The finished tile goes through LDS so that
+// every global store writes whole rows.
 //
 // Few output tiles (a weight gradient of 2048 x 2048 has 64) would leave most
 // of the 256 CUs idle, so the K range can be split into S slices whose fp32
@@ -38,12 +39,12 @@
 #include "fh_common.hpp"
 #include "fh_mfma.hpp"
 
+#include <type_traits>
+
 namespace fh {
 namespace {
 
-constexpr int kThreads = 512;                  // 8 waves
 constexpr int kTm = 256, kTn = 256, kTk = 64;  // block tile and stage depth
-constexpr int kOpBytes = 256 * kTk * 2;        // one operand's stage: 32 KB
 constexpr int kSubBytes = kTk * 128;           // KO sub-tile: [64 k x 64] bf16
 
 enum Epi { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_PARTIAL = 2 };
@@ -87,37 +88,48 @@ __device__ __forceinline__ bf16x8 frag_ko(const char* tile, int t0, int t4, int 
   return as_bf16x8(make_uint4(ulo.x, ulo.y, uhi.x, uhi.y));
 }
 
-// Global -> LDS copy of one wave's quarter (8 runs of 1 KB) of an operand's
-// stage.  KC: tile rows 64q .. 64q+63 (clamped to `last`), k0 .. k0+63.  KO:
-// sub-tile q, i.e. k rows k0 .. k0+63, columns o0 + 64q .. +63 (chunks
-// clamped to `last`, the last 8-column chunk start).  Run jj covers 8 rows of
-// 128 bytes; lane i fills 16-byte slot i%8 of row i/8, i.e. it loads the
-// chunk the swizzle puts there.  Each address is a wave-uniform 64-bit base
-// (clamped too, so the lane offset is never negative) plus a 32-bit lane
-// offset (leading dims < 2^26 keep it in range).
+// One 1 KB direct-to-LDS copy: lane i loads the 16 bytes at sbase + voff into
+// LDS at lds + 16 i.  Issued as inline asm so that the compiler does not track
+// it (it would otherwise wait for every load in flight before any LDS read):
+// the kernel waits for its loads itself (s_waitcnt vmcnt) before the barrier
+// that hands a stage to the other waves.  M0 carries the LDS address; nothing
+// else in these kernels uses M0, which the compiler reserves (hence the
+// diagnostic it would print for the clobber).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Run jj (0..7) of wave q's quarter of an operand's stage, into its 1 KB slot
+// (8q + jj) of the stage's tile at `dst`.  KC: tile rows 64q + 8jj .. +7
+// (clamped to `last`), k0 .. k0+63: lane i fills 16-byte slot i%8 of row i/8,
+// i.e. it loads the chunk the swizzle puts there.  KO: sub-tile q, k rows
+// k0 + 8jj .. +7, columns o0 + 64q .. +63 (chunks clamped to `last`, the last
+// 8-column chunk start).  The address is a wave-uniform 64-bit base (clamped
+// too, so the lane offset is never negative) plus a 32-bit lane offset
+// (leading dims < 2^26 keep it in range).
 template <bool KO>
-__device__ __forceinline__ void dma_quarter(const uint16_t* base, int64_t ld, int o0, int last,
-                                            int k0, int q, char* dst, int lane) {
-  typedef __attribute__((address_space(1))) const void* gptr;
-  typedef __attribute__((address_space(3))) void* lptr;
+__device__ __forceinline__ void dma_one(const uint16_t* base, int64_t ld, int o0, int last, int k0, int q,
+                                        char* dst, int lane, int jj) {
+  typedef __attribute__((address_space(3))) char* lptr;
   const int lr = lane >> 3;
-#pragma unroll
-  for (int jj = 0; jj < 8; ++jj) {
-    const int c = (lane & 7) ^ swz<64>(8 * jj + lr);
-    const char* sp;
-    uint32_t off;
-    if constexpr (KO) {
-      const int col0 = min(o0 + 64 * q, last);
-      sp = reinterpret_cast<const char*>(base + static_cast<int64_t>(k0 + 8 * jj) * ld + col0);
-      off = static_cast<uint32_t>(lr * static_cast<int>(ld) + min(o0 + 64 * q + 8 * c, last) - col0) * 2u;
-    } else {
-      const int row0 = min(o0 + 64 * q + 8 * jj, last);
-      sp = reinterpret_cast<const char*>(base + static_cast<int64_t>(row0) * ld + k0);
-      off = static_cast<uint32_t>((min(o0 + 64 * q + 8 * jj + lr, last) - row0) * static_cast<int>(ld) +
-                                  8 * c) * 2u;
-    }
-    __builtin_amdgcn_global_load_lds((gptr)(sp + off), (lptr)(dst + (8 * q + jj) * 1024), 16, 0, 0);
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lptr)dst));
+  const int c = (lane & 7) ^ swz<64>(8 * jj + lr);
+  const char* sp;
+  uint32_t off;
+  if constexpr (KO) {
+    const int col0 = min(o0 + 64 * q, last);
+    sp = reinterpret_cast<const char*>(base + static_cast<int64_t>(k0 + 8 * jj) * ld + col0);
+    off = static_cast<uint32_t>(lr * static_cast<int>(ld) + min(o0 + 64 * q + 8 * c, last) - col0) * 2u;
+  } else {
+    const int row0 = min(o0 + 64 * q + 8 * jj, last);
+    sp = reinterpret_cast<const char*>(base + static_cast<int64_t>(row0) * ld + k0);
+    off = static_cast<uint32_t>((min(o0 + 64 * q + 8 * jj + lr, last) - row0) * static_cast<int>(ld) + 8 * c) * 2u;
   }
+  dma16(off, sp, lds0 + (8 * q + jj) * 1024);
 }
 
 __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
@@ -131,26 +143,25 @@ __device__ __forceinline__ void bar() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
+constexpr int kSlot = 32768;  // one operand's stage: [256 x 64] bf16
+constexpr int kRing = 5;      // operand slots in LDS (160 KB)
+
+template <int N>
+__device__ __forceinline__ void wait_vm_n() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ int mod5(int v) { return v >= 5 ? v - 5 : v; }
+
 template <bool A_KO, bool B_KO, int EPI>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm(GemmArgs g) {
-  // The two stages as separate arrays (A at 0, B at 32 KB): the loop is
-  // unrolled over them, so every LDS access names its stage and the compiler
-  // can tell the reads of one stage from the direct-to-LDS loads in flight
-  // into the other.
-  __shared__ __align__(16) char st0[2 * kOpBytes], st1[2 * kOpBytes];
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_gemm(GemmArgs g) {
+  __shared__ __align__(16) char ring[kRing * kSlot];
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int grp = wave >> 2;  // 0: waves 0-3, 1: waves 4-7 (one of each per SIMD)
-
-  // Workgroup L runs on XCD L % 8 (each XCD has its own L2): logical block
-  // (L % 8) * (grid / 8) + L / 8 gives every XCD a contiguous run of the
-  // logical order below.  The grid is padded to a multiple of 8.
   const int nb8 = gridDim.x >> 3;
   const int lid = (blockIdx.x & 7) * nb8 + (blockIdx.x >> 3);
   if (lid >= g.grid) return;
   const int slice = lid / g.tiles, t = lid - slice * g.tiles;
-  // Logical order inside a slice: groups of 4 m tiles, m fastest, so the
-  // ~32 tiles an XCD runs at once cover 4 m tiles x 8 n tiles.
   constexpr int GM = 4;
   const int width = GM * g.tiles_n;
   const int gi = t / width, first_m = gi * GM;
@@ -161,145 +172,187 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   const int s_begin = slice * g.steps_per_slice;
   const int nst = min(g.total_steps - s_begin, g.steps_per_slice);
 
-  // Loads: waves 0-3 copy quarter (wave & 3) of A, waves 4-7 of B.
-  const int q = wave & 3;
-  auto load = [&](int step, char* stage) __attribute__((always_inline)) {
-    const int k0 = (s_begin + step) * kTk;
-    if (grp == 0) {
-      if constexpr (A_KO) dma_quarter<true>(g.a, g.lda, m0, g.m - 8, k0, q, stage, lane);
-      else dma_quarter<false>(g.a, g.lda, m0, g.m - 1, k0, q, stage, lane);
+  // Run jj of wave `wave`'s quarter of operand OP (0: A, 1: B) of stage
+  // `step` into ring slot `slot`.  Stages past the slice's end re-load its
+  // last stage (in bounds, never used): the loop has no branches.
+  auto dma = [&](auto op_tag, int step, int slot, int jj) __attribute__((always_inline)) {
+    constexpr int OP = decltype(op_tag)::value;
+    const int k0 = (s_begin + min(step, nst - 1)) * kTk;
+    char* dst = ring + slot * kSlot;
+    if constexpr (OP == 0) {
+      if constexpr (A_KO) dma_one<true>(g.a, g.lda, m0, g.m - 8, k0, wave, dst, lane, jj);
+      else dma_one<false>(g.a, g.lda, m0, g.m - 1, k0, wave, dst, lane, jj);
     } else {
-      if constexpr (B_KO) dma_quarter<true>(g.b, g.ldb, n0, g.n - 8, k0, q, stage + kOpBytes, lane);
-      else dma_quarter<false>(g.b, g.ldb, n0, g.n - 1, k0, q, stage + kOpBytes, lane);
+      if constexpr (B_KO) dma_one<true>(g.b, g.ldb, n0, g.n - 8, k0, wave, dst, lane, jj);
+      else dma_one<false>(g.b, g.ldb, n0, g.n - 1, k0, wave, dst, lane, jj);
     }
   };
+  using OpA = std::integral_constant<int, 0>;
+  using OpB = std::integral_constant<int, 1>;
 
-  // Wave tile: m 128*wm .. +127, n 64*wn .. +63.
   const int wm = wave & 1, wn = wave >> 1;
   const int a_off = lane_off_a<64>(lane);
   const int t0 = lane_off_tr(lane, 0), t4 = lane_off_tr(lane, 4);
-  bf16x8 fa[2][4], fb[2][2];  // [k16 step of the half][block]
-  // Fragments of half h (k 32h .. 32h+31) of a stage.
-  auto mem = [&](const char* stage, int h) __attribute__((always_inline)) {
-    const char* sa = stage;
-    const char* sb = stage + kOpBytes;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int o = 128 * wm + 32 * j;
-        fa[ks][j] = A_KO ? frag_ko(sa, t0, t4, o, 2 * h + ks) : frag_kc(sa, a_off, o, 2 * h + ks);
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int o = 64 * wn + 32 * i;
-        fb[ks][i] = B_KO ? frag_ko(sb, t0, t4, o, 2 * h + ks) : frag_kc(sb, a_off, o, 2 * h + ks);
-      }
+  bf16x8 fa[2][4], fb[2][4];
+  // Fragment r = 0..7 of k16 step ks (order B0, A0, A1, A2, A3, B1, B2, B3:
+  // the order the MFMAs first use them) from slots sa (A) and sb (B).
+  auto rd1 = [&](int sa, int sb, int ks, int buf, int r) __attribute__((always_inline)) {
+    if (r >= 1 && r <= 4) {
+      const char* tile = ring + sa * kSlot;
+      const int j = r - 1, o = 128 * wm + 32 * j;
+      fa[buf][j] = A_KO ? frag_ko(tile, t0, t4, o, ks) : frag_kc(tile, a_off, o, ks);
+    } else {
+      const char* tile = ring + sb * kSlot;
+      const int i = r == 0 ? 0 : r - 4, o = 128 * wn + 32 * i;
+      fb[buf][i] = B_KO ? frag_ko(tile, t0, t4, o, ks) : frag_kc(tile, a_off, o, ks);
     }
   };
-  f32x16 acc[2][4];  // [n block][m block]; rows = n, column = m
+  f32x16 acc[4][4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = zero16();
-  // The products of a half; `after_first` runs once the first k16 step's
-  // fragments are consumed (their registers are free again).
-  auto comp = [&](auto after_first) __attribute__((always_inline)) {
-    __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma(fb[ks][i], fa[ks][j], acc[i][j]);
-      if (ks == 0) {
-        __builtin_amdgcn_sched_barrier(0);
-        after_first();
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    __builtin_amdgcn_s_setprio(0);
+  auto mf1 = [&](int buf, int nn) __attribute__((always_inline)) {
+    const int i = nn >> 2, j = nn & 3;
+    acc[i][j] = mfma(fb[buf][i], fa[buf][j], acc[i][j]);
   };
-  auto nothing = []() __attribute__((always_inline)) {};
 
-  // Half-steps u = 2x + h (stage x, half h).  Phase P(2u): waves 0-3 read half
-  // u, waves 4-7 multiply half u-1; phase P(2u+1): the reverse.  Stage x+1 is
-  // loaded during P(4x) by all waves, into the stage buffer stage x-1 used
-  // (free once P(4x-1) ended), and waited for at the end of P(4x+3), when
-  // both groups have read all of stage x.  Every phase ends with a workgroup
-  // barrier.
-  load(0, st0);
-  wait_vm();
+  // Operand u (A of stage x: u = 2x, B: 2x+1) lives in ring slot u % 5.
+  // Prologue: stages 0 and 1 (B of 1 without its last two runs, which
+  // stage 0 issues), wait for stage 0.
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) dma(OpA(), 0, 0, jj);
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) dma(OpB(), 0, 1, jj);
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) dma(OpA(), 1, 2, jj);
+#pragma unroll
+  for (int jj = 0; jj < 6; ++jj) dma(OpB(), 1, 3, jj);
+  wait_vm_n<14>();
   bar();
-  if (grp == 0) {
-    auto half = [&](int x, int h, const char* cur, char* nxt) __attribute__((always_inline)) {
-      if (h == 0 && x + 1 < nst) load(x + 1, nxt);
-      mem(cur, h);
-      wait_lds();
-      bar();
-      comp(nothing);
-      if (h == 1) wait_vm();
-      bar();
-    };
-    for (int x = 0; x < nst; x += 2) {
-      half(x, 0, st0, st1);
-      half(x, 1, st0, st1);
-      if (x + 1 < nst) {
-        half(x + 1, 0, st1, st0);
-        half(x + 1, 1, st1, st0);
-      }
-    }
-    bar();  // matches the late start of waves 4-7
-  } else {
-    if (1 < nst) load(1, st1);
-    bar();
-    auto half = [&](int x, int h, const char* cur, char* nxt) __attribute__((always_inline)) {
-      mem(cur, h);
-      wait_lds();
-      if (h == 1) wait_vm();
-      bar();
-      comp([&]() __attribute__((always_inline)) {
-        if (h == 1 && x + 2 < nst) load(x + 2, nxt);
-      });
-      bar();
-    };
-    for (int x = 0; x < nst; x += 2) {
-      half(x, 0, st0, st0);
-      half(x, 1, st0, st0);
-      if (x + 1 < nst) {
-        half(x + 1, 0, st1, st1);
-        half(x + 1, 1, st1, st1);
-      }
-    }
-  }
+#pragma unroll
+  for (int r = 0; r < 8; ++r) rd1(0, 1, 0, 0, r);
 
-  // lane: m = m0 + 128 wm + 32 j + l32; n = n0 + 64 wn + 32 i + 8 e + 4 hl + 0..3
+  // Stage x: 64 MFMAs (k16 steps 0..3 x 16) on fragments read one step
+  // ahead.  Loads issued during stage x (slot s = 2x % 5):
+  //   B(x+1) runs 6, 7 at MFMAs 0, 2        (slot s+3, free since stage x-1)
+  //   A(x+2) runs 0..7 at MFMAs 6..46       (slot s+4, free since stage x-1)
+  //   B(x+2) runs 0..5 at MFMAs 56..61      (slot s, after this stage's reads)
+  // Before the barrier in step 3 each wave waits for all but its last 8 loads
+  // (A(x+2)): stage x+1 is then complete in LDS.
+  int s = 0;
+  for (int x = 0; x < nst; ++x) {
+    const int sB = mod5(s + 1), nA = mod5(s + 2), nB = mod5(s + 3), fA = mod5(s + 4);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int mrow = m0 + 128 * wm + 32 * j + l32;
-    if (mrow >= g.m) continue;
+    for (int ks = 0; ks < 3; ++ks) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+      for (int nn = 0; nn < 16; ++nn) {
+        const int p = 16 * ks + nn;
+        if ((nn & 1) == 0) rd1(s, sB, ks + 1, (ks + 1) & 1, nn >> 1);
+        if (p == 0) dma(OpB(), x + 1, nB, 6);
+        if (p == 2) dma(OpB(), x + 1, nB, 7);
+        if (p >= 6 && p <= 46 && (p - 6) % 6 == 0 && (p - 6) / 6 < 7) dma(OpA(), x + 2, fA, (p - 6) / 6);
+        if (p == 46) dma(OpA(), x + 2, fA, 7);
+        mf1(ks & 1, nn);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    wait_lds();
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int col = n0 + 64 * wn + 32 * i + 8 * e + 4 * hl;
-        if (col >= g.n) continue;
-        const f32x16& v = acc[i][j];
-        if constexpr (EPI == EPI_PARTIAL) {
-          float* dst = g.part + (static_cast<int64_t>(slice) * g.m + mrow) * g.n + col;
-          *reinterpret_cast<float4*>(dst) = make_float4(v[4 * e], v[4 * e + 1], v[4 * e + 2], v[4 * e + 3]);
-        } else if constexpr (EPI == EPI_RESIDUAL) {
-          const uint2 rv = *reinterpret_cast<const uint2*>(g.r + mrow * g.ldr + col);
-          const float r0 = __uint_as_float(rv.x << 16), r1 = __uint_as_float(rv.x & 0xffff0000u);
-          const float r2 = __uint_as_float(rv.y << 16), r3 = __uint_as_float(rv.y & 0xffff0000u);
-          *reinterpret_cast<uint2*>(g.c + mrow * g.ldc + col) =
-              make_uint2(pk_bf16(r0 + round_bf(v[4 * e]), r1 + round_bf(v[4 * e + 1])),
-                         pk_bf16(r2 + round_bf(v[4 * e + 2]), r3 + round_bf(v[4 * e + 3])));
-        } else {
-          *reinterpret_cast<uint2*>(g.c + mrow * g.ldc + col) =
-              make_uint2(pk_bf16(v[4 * e], v[4 * e + 1]), pk_bf16(v[4 * e + 2], v[4 * e + 3]));
+    for (int nn = 0; nn < 8; ++nn) mf1(1, nn);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vm_n<8>();
+    bar();
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt) {
+      if (tt < 6) dma(OpB(), x + 2, s, tt);
+      rd1(nA, nB, 0, 0, tt);
+      mf1(1, 8 + tt);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    s = nA;
+  }
+  // The re-loads past the end and the last stale fragment reads complete
+  // before the ring is reused for the output tile.
+  wait_vm();
+  wait_lds();
+  bar();
+
+  if constexpr (EPI == EPI_PARTIAL) {
+    // The fp32 tile goes through LDS in two halves of 128 rows ([128 rows x
+    // 256 columns], 16-byte chunk c of row r stored at chunk c ^ (r % 16));
+    // lane i of a wave then stores chunk i of a 1 KB row.
+    float* part = g.part + static_cast<int64_t>(slice) * g.m * g.n;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      if (wm == half) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = 32 * j + l32;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int chunk = 32 * wn + 8 * i + 2 * e + hl;
+              const f32x16& v = acc[i][j];
+              *reinterpret_cast<float4*>(ring + r * 1024 + ((chunk ^ (r & 15)) << 4)) =
+                  make_float4(v[4 * e], v[4 * e + 1], v[4 * e + 2], v[4 * e + 3]);
+            }
         }
       }
+      wait_lds();
+      bar();
+      const int col = n0 + 4 * lane;
+#pragma unroll 4
+      for (int q2 = 0; q2 < 32; ++q2) {
+        const int r = 32 * wave + q2;
+        const float4 v = *reinterpret_cast<const float4*>(ring + r * 1024 + ((lane ^ (r & 15)) << 4));
+        const int mrow = m0 + 128 * half + r;
+        if (mrow < g.m && col < g.n) *reinterpret_cast<float4*>(part + static_cast<int64_t>(mrow) * g.n + col) = v;
+      }
+      wait_lds();
+      bar();
+    }
+  } else {
+    // The bf16 tile goes through LDS ([256 rows x 256 columns], 16-byte chunk
+    // c of row r stored at chunk c ^ (r % 16)) so that every global store
+    // writes whole rows: lane i of a wave stores chunk i % 32 of row 2q + i / 32.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = 128 * wm + 32 * j + l32;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int chunk = 16 * wn + 4 * i + e;
+          const f32x16& v = acc[i][j];
+          *reinterpret_cast<uint2*>(ring + r * 512 + ((chunk ^ (r & 15)) << 4) + 8 * hl) =
+              make_uint2(pk_bf16(v[4 * e], v[4 * e + 1]), pk_bf16(v[4 * e + 2], v[4 * e + 3]));
+        }
+    }
+    wait_lds();
+    bar();
+    const int chunk = lane & 31;
+    const int col = n0 + 8 * chunk;
+#pragma unroll 4
+    for (int q2 = 0; q2 < 32; ++q2) {
+      const int r = 64 * wave + 2 * q2 + hl;
+      const uint4 v = *reinterpret_cast<const uint4*>(ring + r * 512 + ((chunk ^ (r & 15)) << 4));
+      const int mrow = m0 + r;
+      if (mrow >= g.m || col >= g.n) continue;
+      if constexpr (EPI == EPI_RESIDUAL) {
+        const uint4 rv = *reinterpret_cast<const uint4*>(g.r + mrow * g.ldr + col);
+        auto add2 = [](uint32_t res, uint32_t c) {
+          return pk_bf16(__uint_as_float(res << 16) + __uint_as_float(c << 16),
+                         __uint_as_float(res & 0xffff0000u) + __uint_as_float(c & 0xffff0000u));
+        };
+        *reinterpret_cast<uint4*>(g.c + mrow * g.ldc + col) =
+            make_uint4(add2(rv.x, v.x), add2(rv.y, v.y), add2(rv.z, v.z), add2(rv.w, v.w));
+      } else {
+        *reinterpret_cast<uint4*>(g.c + mrow * g.ldc + col) = v;
+      }
+    }
   }
 }
 
@@ -372,11 +425,11 @@ int gemm_slices(int64_t m, int64_t n, int64_t k) {
 template <bool A_KO, bool B_KO>
 void launch(const GemmArgs& g, unsigned blocks, bool partial, bool resid, hipStream_t stream) {
   if (partial)
-    hipLaunchKernelGGL((k_gemm<A_KO, B_KO, EPI_PARTIAL>), dim3(blocks), dim3(kThreads), 0, stream, g);
+    hipLaunchKernelGGL((k_gemm<A_KO, B_KO, EPI_PARTIAL>), dim3(blocks), dim3(256), 0, stream, g);
   else if (resid)
-    hipLaunchKernelGGL((k_gemm<A_KO, B_KO, EPI_RESIDUAL>), dim3(blocks), dim3(kThreads), 0, stream, g);
+    hipLaunchKernelGGL((k_gemm<A_KO, B_KO, EPI_RESIDUAL>), dim3(blocks), dim3(256), 0, stream, g);
   else
-    hipLaunchKernelGGL((k_gemm<A_KO, B_KO, EPI_STORE>), dim3(blocks), dim3(kThreads), 0, stream, g);
+    hipLaunchKernelGGL((k_gemm<A_KO, B_KO, EPI_STORE>), dim3(blocks), dim3(256), 0, stream, g);
 }
 
 bool valid_op(int op) { return op == FH_GEMM_NT || op == FH_GEMM_NN || op == FH_GEMM_TN; }
@@ -459,3 +512,4 @@ extern "C" int fh_gemm_bf16(int op, const void* a, int64_t lda, const void* b, i
   }
   return check_launch("fh_gemm_bf16");
 }
+
