@@ -89,6 +89,9 @@ def parse_args():
                     help="projection GEMMs: per-shape choice from the measured table "
                          "(femtotron_amd/tuned/gemm_dispatch_gfx950.json), the hand-written "
                          "fh_gemm_bf16 wherever it applies, or the library GEMM")
+    ap.add_argument("--wgrad-stream", choices=("serial", "side"), default="serial",
+                    help="weight-gradient GEMMs in series with the input-gradient chain (measured "
+                         "faster with the hand-written GEMMs) or on a side stream next to it")
     ap.add_argument("--tune-gemm-dispatch", action="store_true",
                     help="time fh_gemm_bf16 against the library GEMM for every projection GEMM of "
                          "the three workloads, write femtotron_amd/tuned/gemm_dispatch_gfx950.json "
@@ -551,6 +554,8 @@ def main() -> int:
         print(json.dumps({"gemm_dispatch": str(path)}), flush=True)
         return 0
     projections.set_gemm_policy(args.gemm)
+    from femtotron_amd.fused_layer import set_wgrad_side_stream
+    set_wgrad_side_stream(args.wgrad_stream == "side")
 
     if args.profile_kernel:
         print(json.dumps(profile_kernel(torch, args.profile_kernel, WORKLOADS[args.workload][0])),
@@ -679,7 +684,9 @@ def main() -> int:
                   "hand_written": "fh_gemm_bf16 (femtotron_amd/csrc/fh_gemm.hip)",
                   "library": ("hipBLASLt/rocBLAS, TunableOp solutions from femtotron_amd/tuned/"
                               "tunableop_gfx950.csv" if tuned else "hipBLASLt default heuristics"),
-                  "table": "femtotron_amd/tuned/gemm_dispatch_gfx950.json"},
+                  "table": "femtotron_amd/tuned/gemm_dispatch_gfx950.json",
+                  "weight_gradients": ("in series with the input-gradient chain" if args.wgrad_stream == "serial"
+                                       else "side stream")},
         "weights": f"q/k/v and gate/up packed contiguously ({packed_groups} groups)",
         "boundary_ops": ("fused embedding (deterministic scatter-add backward) and final RMSNorm"
                          if boundary else "reference nn.Embedding and LlamaRMSNorm"),

@@ -116,6 +116,23 @@ def test_fused_layer_at_least_as_accurate_as_reference_bf16(name, c, B, S):
         assert eg <= 1.25 * er + 1e-3, f"{name} {tag}: fused err {eg:.2e} vs reference bf16 err {er:.2e}"
 
 
+def test_weight_gradients_on_side_stream_match_serial_bitwise():
+    """The weight-gradient GEMMs give the same bits whether they run in series
+    with the input-gradient chain (the default) or on a side stream: every
+    kernel is deterministic and the side stream only changes the order."""
+    from femtotron_amd.fused_layer import set_wgrad_side_stream, wgrad_side_stream
+    assert not wgrad_side_stream()
+    serial = _run_layer(CFG3, 1, 256, torch.bfloat16, fused=True)
+    set_wgrad_side_stream(True)
+    try:
+        side = _run_layer(CFG3, 1, 256, torch.bfloat16, fused=True)
+    finally:
+        set_wgrad_side_stream(False)
+    assert torch.equal(serial[0], side[0]) and torch.equal(serial[1], side[1])
+    for k in serial[2]:
+        assert torch.equal(serial[2][k], side[2][k]), k
+
+
 def test_fused_layer_reference_init_bf16():
     """All parameters N(0, 0.02) (norm weights too), the reference's own init."""
     got = _run_layer(CFG1, 2, 128, torch.bfloat16, fused=True, norm_mean=0.0)
