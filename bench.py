@@ -13,16 +13,23 @@ The default workload is the metric's (TinyLlama, every layer checkpointed);
 1 x 32768 tokens) and --ac selective the selective policy (MLP and norms
 checkpointed) instead of whole layers.
 Prints ONE JSON line.  Besides tokens/s it reports:
-  * roofline: the fused memory-bound kernel with the largest share of step time,
-    its algorithmic bytes per launch / its mean launch time (HIP events on the
-    launch stream) against the 8 TB/s HBM peak, and every other fused kernel;
-  * attention kernels and the hand-written weight-gradient GEMM against the 2.5 PFLOP/s dense
-    bf16 MFMA peak;
+  * roofline: this build's dominant kernel, the hand-written kernel with the most
+    time per step (a projection GEMM on fh_gemm_bf16 on the TinyLlama step), its
+    algorithmic FLOPs (or bytes) per launch / its mean launch time (HIP events on
+    the launch stream, the kernel alone at the step's shape) against the 2.5
+    PFLOP/s dense bf16 MFMA peak (or the 8 TB/s HBM peak); roofline_hbm the same
+    for the fused memory-bound kernel with the most time per step;
+  * every fused memory-bound kernel against HBM peak at the step's shapes, and at
+    BASELINE config 2's op-level shapes with the MALL flushed before each launch;
+  * attention kernels and every projection GEMM (hand-written and library, the
+    one the dispatch runs marked) against the MFMA peak; model and hardware FLOPs
+    per token and the step's MFU / HFU;
   * peak activation bytes per token of the fused path and of the reference path
-    (Hugging Face layers under torch.utils.checkpoint, debug=True) on the same GPU;
+    (Hugging Face layers under torch.utils.checkpoint, debug=True as the
+    reference's wrapper calls it, and debug=False) on the same GPU;
   * cpu_baseline: the reference-equivalent path (oracle/torch_llama.py under
-    torch.utils.checkpoint with debug=True, fp32) on the host cores, on a bounded
-    sample of the same model.
+    torch.utils.checkpoint with debug=True and debug=False, fp32) on the host
+    cores, on a bounded sample of the same model, plus BASELINE configs 1 and 2.
 """
 from __future__ import annotations
 
@@ -101,6 +108,8 @@ def parse_args():
     ap.add_argument("--stock-attention", action="store_true",
                     help="under --ac selective keep HF's LlamaAttention outside the checkpoints "
                          "(no fuse_attention)")
+    ap.add_argument("--no-chain", action="store_true",
+                    help="skip the BASELINE config 2 op-level table of the memory-bound chain")
     ap.add_argument("--no-optimizer", action="store_true",
                     help="skip the fused-AdamW timing (reported beside the fwd+bwd metric)")
     ap.add_argument("--profile-kernel", default=None,
@@ -311,6 +320,107 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True,
     return rows, mfma
 
 
+# the decoder layer's memory-bound chain, op-level.
+CHAIN_CFG2 = dict(tokens=4096, hidden=4096, ffn=14336, rope_heads=32, head_dim=128, theta=500000.0)
+MALL_FLUSH_BYTES = 512 << 20
+
+
+def flushed_ms(torch, fn, reps: int, flush) -> float:
+    """Median launch time of fn(i) over `reps` launches, each preceded by a
+    read of a 512 MiB buffer (more than the 256 MiB MALL, so every launch's
+    operands come from HBM); HIP events around each launch alone."""
+    fn(0)
+    stream = torch.cuda.current_stream()
+    ev = []
+    for i in range(reps):
+        flush()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        fn(i)
+        b.record(stream)
+        ev.append((a, b))
+    torch.cuda.synchronize()
+    ms = sorted(a.elapsed_time(b) for a, b in ev)
+    return ms[len(ms) // 2]
+
+
+def chain_table(torch, shape: dict, reps: int) -> list:
+    """The fused memory-bound kernels at BASELINE config 2's shapes (x [1, T, H]
+    bf16, RMSNorm weight 1 + N(0, 0.02), RoPE on rope_heads x head_dim of q,
+    SwiGLU gate/up [1, T, F], residual add; forward, recompute and backward
+    kernels), inputs from CPU generators with seeds 1-5 as the op-level config
+    prescribes, the MALL flushed before every launch."""
+    from femtotron_amd import ops
+    T, H, Fd = shape["tokens"], shape["hidden"], shape["ffn"]
+    nr, hd = shape["rope_heads"], shape["head_dim"]
+    dev, bf = "cuda", torch.bfloat16
+
+    def cpu_randn(seed, *size):
+        return torch.randn(*size, generator=torch.Generator().manual_seed(seed)).to(device=dev, dtype=bf)
+
+    x = cpu_randn(1, T, H)
+    w = (1 + 0.02 * torch.randn(H, generator=torch.Generator().manual_seed(2))).to(device=dev, dtype=bf)
+    g = cpu_randn(3, T, Fd)
+    u = cpu_randn(4, T, Fd)
+    dy = cpu_randn(5, T, H)
+    dp = cpu_randn(5, T, Fd)
+    flush_buf = torch.ones(MALL_FLUSH_BYTES // 4, device=dev, dtype=torch.float32)
+
+    def flush():
+        flush_buf.sum()
+
+    y = torch.empty_like(x)
+    hh = torch.empty_like(x)
+    rs = torch.empty(T, device=dev, dtype=torch.float32)
+    q = x[:, :nr * hd].clone()
+    inv = 1.0 / (shape["theta"] ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
+    ang = torch.arange(T, dtype=torch.float32)[:, None] * inv[None, :]
+    ang = torch.cat((ang, ang), dim=-1)[None]
+    cos, sin = ang.cos().to(device=dev, dtype=bf), ang.sin().to(device=dev, dtype=bf)
+    p = torch.empty(T, Fd, device=dev, dtype=bf)
+    dg, du = torch.empty_like(p), torch.empty_like(p)
+    rows = []
+
+    def row(name, symbol, nbytes, fn):
+        ms = flushed_ms(torch, fn, reps, flush)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        rows.append(dict(kernel=name, symbol=symbol, bytes_per_launch=int(nbytes), ms_per_launch=round(ms, 5),
+                         achieved_gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4)))
+
+    row("rmsnorm_fwd", "k_rmsnorm_fwd", 4 * T * H, lambda i: ops.rmsnorm_fwd(x, w, 1e-5, out=y, rstd=rs))
+    row("add_rmsnorm_fwd", "k_rmsnorm_fwd (ADD)", 8 * T * H,
+        lambda i: ops.add_rmsnorm_fwd(x, dy, w, 1e-5, rstd=rs))
+    row("rmsnorm_bwd", "k_rmsnorm_bwd (+ residual gradient)", 8 * T * H,
+        lambda i: ops.rmsnorm_bwd(dy, x, w, 1e-5, rstd=rs, dres=y))
+    row("rmsnorm_bwd_plain", "k_rmsnorm_bwd", 6 * T * H, lambda i: ops.rmsnorm_bwd(dy, x, w, 1e-5))
+    row("rope_fwd", "k_rope<fwd>", 4 * T * nr * hd, lambda i: ops.rope_fwd_(q, nr, hd, T, cos, sin))
+    row("rope_bwd", "k_rope<bwd>", 4 * T * nr * hd, lambda i: ops.rope_bwd_(q, nr, hd, T, cos, sin))
+    row("swiglu_fwd", "k_swiglu_fwd", 6 * T * Fd, lambda i: ops.swiglu_fwd(g, u, out=p))
+    row("swiglu_bwd", "k_swiglu_bwd", 10 * T * Fd, lambda i: ops.swiglu_bwd(dp, g, u, dg, du))
+    row("residual_add", "k_add", 6 * T * H, lambda i: ops.add(x, dy, out=hh))
+    del flush_buf
+    return rows
+
+
+def step_flops_per_token(c: dict) -> dict:
+    """Algorithmic FLOPs per token of one step: the layer forward (projection
+    GEMMs + causal attention 2 Hq S), counted 3x without recompute (model FLOPs)
+    and 4x with the full-layer recompute (hardware FLOPs, the recompute path
+    re-runs the layer up to SwiGLU, so the down projection is not counted
+    twice), plus the lm_head 3x."""
+    H, Fd, S = c["hidden"], c["ffn"], c["seq"]
+    hd = H // c["heads"]
+    Hq, Hkv = c["heads"] * hd, c["kv"] * hd
+    gemm = 2 * (H * (Hq + 2 * Hkv) + Hq * H + 3 * H * Fd)
+    attn = 2 * Hq * S
+    fwd = gemm + attn
+    head = 2 * H * c["vocab"]
+    L = c["layers"]
+    model = L * 3 * fwd + 3 * head
+    hardware = L * (4 * fwd - 2 * H * Fd) + 3 * head
+    return {"model": model, "hardware": hardware}
+
+
 def projection_gemm_rows(torch, c: dict, iters: int, sel: bool, fused_attention: bool, rnd) -> list:
     """Every projection GEMM of the step at its shape: the hand-written
     fh_gemm_bf16 and the library GEMM timed side by side (HIP events), the one
@@ -505,29 +615,109 @@ def optimizer_timing(torch, model, iters: int) -> dict:
                          "on fp32 masters; param.copy_(master)"}
 
 
+def host_info(threads: int) -> dict:
+    """The host the CPU baseline ran on: logical CPUs, threads used, lscpu's
+    model name, sockets and cores per socket."""
+    import subprocess
+    info = {"cpu_count": os.cpu_count(), "threads": threads}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            if key.strip() in ("Model name", "Socket(s)", "Core(s) per socket", "Thread(s) per core"):
+                info[key.strip()] = val.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return info
+
+
 def cpu_baseline(torch, n_tokens: int) -> dict:
-    """Reference-equivalent path on the host: oracle Llama (HF layer math) with
-    every layer under torch.utils.checkpoint(use_reentrant=False, debug=True), fp32."""
-    from oracle.torch_llama import OracleLlama
-    c = TINYLLAMA
+    """Reference-equivalent path on the host, fp32: the oracle Llama (HF layer
+    math) with every layer under torch.utils.checkpoint(use_reentrant=False,
+    debug=True) as the reference wrapper calls it, and with debug=False (the
+    stock number).  `value` is a bounded sample of the metric's TinyLlama
+    workload; beside it BASELINE config 1 (the whole debug model step) and
+    config 2 (the memory-bound chain, op-level) on the same cores."""
+    import torch.nn.functional as Fn
+    from oracle.torch_llama import OracleLlama, rmsnorm, rope
     cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
     prev = torch.get_num_threads()
     torch.set_num_threads(cores)
+
+    def model_step(orc, ids, debug: bool) -> float:
+        t0 = time.perf_counter()
+        _, loss = orc.forward(ids, ids, checkpoint=True, debug=debug)
+        loss.backward()
+        return time.perf_counter() - t0
+
     try:
+        c = TINYLLAMA
         orc = OracleLlama(vocab=c["vocab"], hidden=c["hidden"], n_layers=c["layers"], n_heads=c["heads"],
                           n_kv=c["kv"], ffn=c["ffn"], theta=c["theta"])
         ids = torch.randint(0, c["vocab"], (1, n_tokens), generator=torch.Generator().manual_seed(2000))
-        t0 = time.perf_counter()
-        _, loss = orc.forward(ids, ids, checkpoint=True, debug=True)
-        loss.backward()
-        dt = time.perf_counter() - t0
+        model_step(orc, ids[:, :16], True)  # one-time initialisation outside the timed sample
+        dt = model_step(orc, ids, True)
+        dt_nd = model_step(orc, ids, False)
+        del orc
+        # config 1: the 2-layer debug model, batch 2 x 128 (median of 3 steps)
+        tiny = OracleLlama(vocab=1024, hidden=256, n_layers=2, n_heads=8, n_kv=4, ffn=688, theta=10000.0)
+        ids1 = torch.randint(0, 1024, (2, 128), generator=torch.Generator().manual_seed(2000))
+        c1 = {d: sorted(model_step(tiny, ids1, d) for _ in range(3))[1] for d in (True, False)}
+        # config 2: RMSNorm -> RoPE (32 x 128) + residual, SwiGLU [4096, 14336];
+        # forward under the checkpoint (recomputed in backward) + backward
+        sh = CHAIN_CFG2
+        T, H, Fd, nr, hd = sh["tokens"], sh["hidden"], sh["ffn"], sh["rope_heads"], sh["head_dim"]
+        gen = [torch.Generator().manual_seed(k) for k in range(1, 6)]
+        x = torch.randn(1, T, H, generator=gen[0]).requires_grad_(True)
+        wn = (1 + 0.02 * torch.randn(H, generator=gen[1])).requires_grad_(True)
+        gt = torch.randn(1, T, Fd, generator=gen[2]).requires_grad_(True)
+        ut = torch.randn(1, T, Fd, generator=gen[3]).requires_grad_(True)
+        dyc = torch.randn(1, T, H, generator=gen[4])
+        dpc = torch.randn(1, T, Fd, generator=gen[4])
+        inv = 1.0 / (sh["theta"] ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
+        ang = torch.arange(T, dtype=torch.float32)[:, None] * inv[None, :]
+        ang = torch.cat((ang, ang), dim=-1)[None]
+        cos, sin = ang.cos(), ang.sin()
+
+        def chain(x_, g_, u_):
+            y = rmsnorm(x_, wn, 1e-5)
+            q = y.view(1, T, nr, hd).transpose(1, 2)
+            qr, _ = rope(q, q, cos, sin)
+            return qr.transpose(1, 2).reshape(1, T, H) + x_, Fn.silu(g_) * u_
+
+        def chain_step(debug: bool) -> float:
+            t0 = time.perf_counter()
+            o1, o2 = torch.utils.checkpoint.checkpoint(chain, x, gt, ut, use_reentrant=False, debug=debug)
+            torch.autograd.backward((o1, o2), (dyc, dpc))
+            return time.perf_counter() - t0
+
+        chain_step(True)  # one-time allocation outside the timed runs
+        runs = {True: [], False: []}
+        for _ in range(3):
+            for d in (True, False):
+                runs[d].append(chain_step(d))
+        c2 = {d: sorted(v)[1] for d, v in runs.items()}
     finally:
         torch.set_num_threads(prev)
     return {"value": round(n_tokens / dt, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"1 fwd+bwd of the full 22-layer TinyLlama-1.1B-shaped model on 1 x {n_tokens} "
                       f"tokens, fp32, oracle/torch_llama.py layers under torch.utils.checkpoint("
                       f"use_reentrant=False, debug=True) as the reference wrapper calls it; "
-                      f"{dt:.1f} s on {cores} threads"}
+                      f"{dt:.1f} s on {cores} threads",
+            "debug_false": {"value": round(n_tokens / dt_nd, 2), "unit": "tokens/s",
+                            "note": "same sample, torch.utils.checkpoint(debug=False)"},
+            "config1": {"debug_true_tokens_per_s": round(256 / c1[True], 1),
+                        "debug_false_tokens_per_s": round(256 / c1[False], 1),
+                        "sample": "BASELINE config 1: the 2-layer debug model (hidden 256, 8 heads, "
+                                  "4 KV heads, ffn 688, vocab 1024), one fwd+bwd of 2 x 128 tokens, "
+                                  "median of 3"},
+            "config2_chain": {"debug_true_ms": round(c2[True] * 1e3, 1),
+                              "debug_false_ms": round(c2[False] * 1e3, 1),
+                              "tokens_per_s": round(T / c2[True], 1),
+                              "sample": "BASELINE config 2 op-level chain, fp32: RMSNorm, RoPE on "
+                                        "32 x 128, residual add, SwiGLU [4096, 14336], forward under "
+                                        "the checkpoint + recompute + backward (median of 3, interleaved)"},
+            "host": host_info(cores)}
 
 
 def main() -> int:
@@ -613,11 +803,28 @@ def main() -> int:
                               fused_attention=bool(attn_fused))
     for r in rows:
         r["ms_per_step"] = round(r["ms_per_launch"] * r["launches_per_step"], 4)
+    for r in mfma:
+        r["ms_per_step"] = round(r["ms_per_launch"] * r["launches_per_step"], 4)
+    timing = (f"mean of {args.kernel_iters} back-to-back launches alone at the step's shape, HIP events "
+              "on the launch stream")
     dom = max(rows, key=lambda r: r["ms_per_step"])
-    roofline = {"bound": "hbm", "kernel": dom["kernel"], "achieved": dom["achieved_gbs"],
-                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["frac"],
-                "traffic": measured_traffic(dom["kernel"]) if args.workload == "tinyllama" else None,
-                "bytes_per_launch": dom["bytes_per_launch"]}
+    roofline_hbm = {"bound": "hbm", "kernel": dom["kernel"], "achieved": dom["achieved_gbs"],
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["frac"],
+                    "traffic": measured_traffic(dom["kernel"]) if args.workload == "tinyllama" else None,
+                    "bytes_per_launch": dom["bytes_per_launch"], "us_per_launch": round(dom["ms_per_launch"] * 1e3, 2),
+                    "duration": timing}
+    # The dominant kernel of this build: the hand-written kernel (fused HBM,
+    # attention or projection GEMM on fh_gemm_bf16) with the most time per step.
+    own = [r for r in mfma if not r.get("path", "fh").startswith("library")]
+    dom_m = max(own, key=lambda r: r["ms_per_step"]) if own else None
+    if dom_m is not None and dom_m["ms_per_step"] > dom["ms_per_step"]:
+        roofline = {"bound": "mfma", "kernel": dom_m["kernel"], "achieved": dom_m["achieved_tflops"],
+                    "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": dom_m["frac"],
+                    "traffic": measured_traffic(dom_m["kernel"]) if args.workload == "tinyllama" else None,
+                    "flop_per_launch": dom_m["flop_per_launch"],
+                    "us_per_launch": round(dom_m["ms_per_launch"] * 1e3, 2), "duration": timing}
+    else:
+        roofline = roofline_hbm
 
     def use(fused: bool):
         remove_activation_checkpointing(model)
@@ -637,8 +844,23 @@ def main() -> int:
         use(False)
         rsec = time_steps(torch, model, ids, args.reference_steps, 1)
         ref = {"tokens_per_s": round(T / rsec, 1), "ms_per_step": round(rsec * 1e3, 2),
-               "speedup_fused_vs_reference": round(rsec / sec, 2)}
+               "speedup_fused_vs_reference": round(rsec / sec, 2),
+               "checkpoint": "torch.utils.checkpoint(use_reentrant=False, debug=True), as the reference's "
+                             "wrapper calls it (femtotron/training/activation_ckpt.py:84)"}
         log(f"reference: {rsec * 1e3:.1f} ms/step")
+        # the stock number: the same path with the checkpoint's debug traces off
+        from torch.utils.checkpoint import checkpoint as torch_checkpoint
+
+        def checkpoint_no_debug(fn, *a, **k):
+            k["debug"] = False
+            return torch_checkpoint(fn, *a, **k)
+
+        remove_activation_checkpointing(model)
+        apply_activation_checkpointing(model, policy, checkpoint_fn=checkpoint_no_debug)
+        rsec_nd = time_steps(torch, model, ids, args.reference_steps, 1)
+        ref["debug_false"] = {"tokens_per_s": round(T / rsec_nd, 1), "ms_per_step": round(rsec_nd * 1e3, 2),
+                              "speedup_fused_vs_reference": round(rsec_nd / sec, 2)}
+        log(f"reference, debug=False: {rsec_nd * 1e3:.1f} ms/step")
     # Activation memory, measured back to back for both paths in the same
     # allocator state (each after one step of its own to allocate gradients).
     use(True)
@@ -655,10 +877,28 @@ def main() -> int:
     del model
     torch.cuda.empty_cache()
 
+    chain = None
+    if not args.no_chain:
+        log("BASELINE config 2: the memory-bound chain op-level, MALL flushed before every launch")
+        chain = {"shape": CHAIN_CFG2, "rows": chain_table(torch, CHAIN_CFG2, max(10, args.kernel_iters)),
+                 "duration": "median of per-launch HIP events, a 512 MiB read before each launch"}
+        torch.cuda.empty_cache()
+
     cpu = None
     if args.cpu_sample_tokens > 0 and args.workload == "tinyllama":
         log(f"cpu baseline: {args.cpu_sample_tokens} tokens on the host")
         cpu = cpu_baseline(torch, args.cpu_sample_tokens)
+
+    step_flops = None
+    if args.ac == "full":
+        fl = step_flops_per_token(c)
+        step_flops = {"model_gflop_per_token": round(fl["model"] / 1e9, 3),
+                      "hardware_gflop_per_token": round(fl["hardware"] / 1e9, 3),
+                      "mfu": round(fl["model"] * tok_s / (MFMA_BF16_PEAK_TFLOPS * 1e12), 4),
+                      "hfu": round(fl["hardware"] * tok_s / (MFMA_BF16_PEAK_TFLOPS * 1e12), 4),
+                      "note": "layer forward (projection GEMMs + causal attention 2 Hq S per token) x3 "
+                              "(model) or x4 less the down projection (hardware: the recompute stops at "
+                              "SwiGLU), lm_head x3, against 2.5 PFLOP/s dense bf16"}
 
     metric = METRIC if args.workload == "tinyllama" else f"ckpt'd fwd+bwd tokens/s @1 GPU ({model_name})"
     out = {
@@ -677,7 +917,10 @@ def main() -> int:
                            else "checkpoints as HF's LlamaAttention"),
                    "parallelism": "single GPU (TP=PP=DP=1)"},
         "roofline": roofline,
+        "roofline_hbm": roofline_hbm,
+        "step_flops": step_flops,
         "fused_kernels_hbm": rows,
+        "op_level_chain_cfg2": chain,
         "mfma_kernels": mfma,
         "gemms": {"policy": args.gemm,
                   "projection_gemms_per_step": gemm_counts,
