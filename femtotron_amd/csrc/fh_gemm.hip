@@ -459,14 +459,13 @@ extern "C" int fh_gemm_bf16(int op, const void* a, int64_t lda, const void* b, i
   // Extents each operand's leading dimension must cover.
   const int64_t a_cols = op == FH_GEMM_TN ? m : k;
   const int64_t b_cols = op == FH_GEMM_NT ? k : n;
-  FH_REQUIRE(lda >= a_cols && ldb >= b_cols && ldc >= n && lda % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0,
-             "gemm_bf16: leading dims must cover the rows (a, b multiples of 8, c of 4)");
+  FH_REQUIRE(lda >= a_cols && ldb >= b_cols && ldc >= n && lda % 8 == 0 && ldb % 8 == 0 && ldc % 8 == 0,
+             "gemm_bf16: leading dims must cover the rows and be multiples of 8");
   FH_REQUIRE(a && b && c, "gemm_bf16: null pointer");
-  FH_REQUIRE(aligned16(a) && aligned16(b) && (reinterpret_cast<uintptr_t>(c) & 7u) == 0,
-             "gemm_bf16: a and b must be 16-byte aligned, c 8-byte aligned");
+  FH_REQUIRE(aligned16(a) && aligned16(b) && aligned16(c), "gemm_bf16: a, b and c must be 16-byte aligned");
   if (residual) {
-    FH_REQUIRE(ldr >= n && ldr % 4 == 0 && (reinterpret_cast<uintptr_t>(residual) & 7u) == 0,
-               "gemm_bf16: residual must be 8-byte aligned with ldr >= n, a multiple of 4");
+    FH_REQUIRE(ldr >= n && ldr % 8 == 0 && aligned16(residual),
+               "gemm_bf16: residual must be 16-byte aligned with ldr >= n, a multiple of 8");
     FH_REQUIRE(residual == c ? ldr == ldc : true, "gemm_bf16: residual aliasing c must share its ldc");
   }
   const int slices = gemm_slices(m, n, k);

@@ -367,8 +367,8 @@ def gemm(op: str, a: torch.Tensor, b: torch.Tensor, *, residual: torch.Tensor | 
             continue
         if t.dtype != torch.bfloat16 or tuple(t.shape) != (m, n) or t.stride(1) != 1:
             raise ValueError(f"gemm({op}): {name} must be a bf16 [{m}, {n}] row-major view")
-        if t.stride(0) % 4 or t.data_ptr() % 8:
-            raise ValueError(f"gemm({op}): {name} must be 8-byte aligned with a row stride % 4 == 0")
+        if t.stride(0) % 8 or t.data_ptr() % 16:
+            raise ValueError(f"gemm({op}): {name} must be 16-byte aligned with a row stride % 8 == 0")
     code = _GEMM_OPS[op]
     nbytes = _lib.lib().fh_gemm_bf16_workspace_size(code, m, n, k)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device) if nbytes else None

@@ -296,9 +296,9 @@ int fh_embedding_bwd(fh_dtype dt, const void* dy, const int64_t* ids, void* dwei
  * hidden_states` of modeling_llama.py:323 fused into the epilogue with its own
  * rounding.  `residual` may be C itself (same ldc), any other overlap is not
  * allowed.
- * Requirements: k % 64 == 0; n % 8 == 0 (and m % 8 == 0 for FH_GEMM_TN); lda,
- * ldb multiples of 8, ldc and ldr of 4; A and B 16-byte aligned, C and the
- * residual 8-byte aligned; m, n, k < 2^30.
+ * Requirements: k % 64 == 0; n % 8 == 0 (and m % 8 == 0 for FH_GEMM_TN);
+ * lda, ldb, ldc and ldr multiples of 8 (< 2^26 for lda, ldb); A, B, C and the
+ * residual 16-byte aligned; m, n, k < 2^30.
  * When the output has few 256 x 256 tiles the k range is split into slices
  * whose fp32 partial sums go to `workspace` (fh_gemm_bf16_workspace_size bytes;
  * 0 = none needed) and are added in slice order, so results are bitwise

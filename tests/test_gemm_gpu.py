@@ -136,3 +136,13 @@ def test_gemm_rejects_unsupported_operands():
     st = _lib.lib().fh_gemm_bf16(_lib.FH_GEMM_NT, x.data_ptr(), 128, x.data_ptr(), 128, x.data_ptr(),
                                  128, None, 0, 128, 128, 96, None, None)
     assert st == 1 and b"multiple of 64" in _lib.lib().fh_last_error()
+    # the output tile is written in 16-byte rows: C and the residual need ldc % 8 and 16-byte alignment
+    st = _lib.lib().fh_gemm_bf16(_lib.FH_GEMM_NT, x.data_ptr(), 128, x.data_ptr(), 128, x.data_ptr(),
+                                 132, None, 0, 128, 128, 128, None, None)
+    assert st == 1 and b"multiples of 8" in _lib.lib().fh_last_error()
+    st = _lib.lib().fh_gemm_bf16(_lib.FH_GEMM_NT, x.data_ptr(), 128, x.data_ptr(), 128, x.data_ptr() + 8,
+                                 128, None, 0, 64, 128, 128, None, None)
+    assert st == 1 and b"16-byte aligned" in _lib.lib().fh_last_error()
+    wide = torch.empty(128, 132, device=DEV, dtype=BF)
+    with pytest.raises(ValueError):
+        ops.gemm("nt", x, x, out=wide[:, :128])
