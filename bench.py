@@ -263,8 +263,7 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True,
     if attn:
         ms = event_ms(torch, lambda i=0: ops.rope_fwd_(qkvs[i % 6], nh + nkv, hd, c["seq"], cos, sin), iters)
         add_row("rope_fwd", "k_rope<fwd>", n_fwd, 4 * T * (Hq + Hkv), ms)
-        ms = event_ms(torch, lambda i=0: ops.rope_bwd_(qkvs[i % 6], nh + nkv, hd, c["seq"], cos, sin), iters)
-        add_row("rope_bwd", "k_rope<bwd>", L, 4 * T * (Hq + Hkv), ms)
+        # the RoPE backward runs inside the attention backward's dQ / dK stores
     # SwiGLU: g,u -> p (6TF);  dp,g,u -> dg,du (10TF)
     gus = sets(3, lambda: rnd(T, 2 * F))
     ps = sets(3, lambda: torch.empty(T, F, device=dev, dtype=bf))
@@ -302,7 +301,8 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True,
     do = rnd(T, Hq)
     dqkv = torch.empty_like(qkv)
     ms_b = event_ms(torch, lambda i=0: ops.attn_bwd(q, k, v, o, do, lse, dqkv[:, :Hq], dqkv[:, Hq:Hq + Hkv],
-                                                      dqkv[:, Hq + Hkv:], B, S, nh, nkv, hd, hd ** -0.5),
+                                                      dqkv[:, Hq + Hkv:], B, S, nh, nkv, hd, hd ** -0.5,
+                                                      rope=(cos, sin)),
                     max(3, iters // 4))
     # backward: dK/dV kernel 4 products + dQ kernel 3 products (the dQ kernel
     # recomputes S and dP); algorithmic = the 5 products of attention backward
@@ -312,7 +312,8 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True,
                  achieved_tflops=round(fwd_flop / ms_f / 1e9, 1),
                  frac=round(fwd_flop / ms_f / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)),
             dict(kernel="attn_bwd", symbol=f"k_attn_bwd_dq<{hd}> + k_attn_bwd_dkdv"
-                                           f"{'_fused' if hd <= 64 else ''}<{hd}>",
+                                           f"{'_fused' if hd <= 64 else ''}<{hd}>, RoPE backward in the "
+                                           "dQ / dK stores (fh_attn_bwd_rope)",
                  launches_per_step=L, flop_per_launch=bwd_flop, ms_per_launch=round(ms_b, 4),
                  achieved_tflops=round(bwd_flop / ms_b / 1e9, 1),
                  frac=round(bwd_flop / ms_b / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4))]
@@ -515,8 +516,11 @@ def profile_kernel(torch, name: str, c: dict, launches: int = 10) -> dict:
         if name == "attn_fwd":
             fn = lambda i: ops.attn_fwd(q, k, v, c["batch"], c["seq"], nh, nkv, hd, hd ** -0.5)
         else:
+            cos = rnd(1, c["seq"], hd)
+            sin = rnd(1, c["seq"], hd)
             fn = lambda i: ops.attn_bwd(q, k, v, o, do, lse, dqkv[:, :Hq], dqkv[:, Hq:Hq + Hkv],
-                                        dqkv[:, Hq + Hkv:], c["batch"], c["seq"], nh, nkv, hd, hd ** -0.5)
+                                        dqkv[:, Hq + Hkv:], c["batch"], c["seq"], nh, nkv, hd, hd ** -0.5,
+                                        rope=(cos, sin))
         nbytes = None
     elif name in ("embedding_fwd", "embedding_bwd"):
         V = c["vocab"]

@@ -54,6 +54,9 @@ SIGNATURES: dict[str, tuple] = {
     "fh_attn_bwd": (c_int, [c_int, _V, _I64, _V, _I64, _V, _I64, _V, _I64, _V, _I64,
                             POINTER(c_float), _V, _I64, _V, _I64, _V, _I64, _V,
                             _I64, _I64, _I64, _I64, _I64, _F, _V]),
+    "fh_attn_bwd_rope": (c_int, [c_int, _V, _I64, _V, _I64, _V, _I64, _V, _I64, _V, _I64,
+                                 POINTER(c_float), _V, _I64, _V, _I64, _V, _I64, _V,
+                                 _I64, _I64, _I64, _I64, _I64, _F, _V, _V, c_int, _V]),
     "fh_ce_fwd_bwd": (c_int, [c_int, _V, _I64, _V, _I64, _I64, _I64, _V, POINTER(c_float), _V]),
     "fh_adamw_workspace_size": (c_size_t, [_I64]),
     "fh_gemm_bf16_workspace_size": (c_size_t, [c_int, _I64, _I64, _I64]),

@@ -111,6 +111,69 @@ __device__ __forceinline__ void store_rows_T(uint16_t* out_row, const f32x16 (&a
     }
 }
 
+// Rotary tables of the RoPE backward fused into the dQ and dK stores:
+// cos / sin rows of head_dim elements in the gradients' dtype, one row per
+// position (per_token == 0) or per token; cos == null means plain stores.
+template <typename T>
+struct RopeRows {
+  const T* cos;
+  const T* sin;
+  int per_token;
+  // Row of position `pos` of the sequence whose first token is row tok0.
+  __device__ __forceinline__ int64_t row(int64_t tok0, int pos) const { return per_token ? tok0 + pos : pos; }
+};
+
+__device__ __forceinline__ void unpack4_bf16(uint2 w, float (&v)[4]) {
+  v[0] = __uint_as_float(w.x << 16);
+  v[1] = __uint_as_float(w.x & 0xffff0000u);
+  v[2] = __uint_as_float(w.y << 16);
+  v[3] = __uint_as_float(w.y & 0xffff0000u);
+}
+
+// store_rows_T followed by the RoPE backward of the stored row: with
+// x = bf16(acc * mul) it writes rope_pair<bf16, backward> of (x[d], x[d+HD/2])
+// -- bit for bit what the plain store and a separate rope backward over the row
+// give.  cs / sn point at this token's cos / sin row.  A lane holds dims
+// dt*32 + 8g + 4hl + (0..3) of its token, so both halves of every pair are in
+// the lane: the partner of (dt, g) is (dt + ND/2, g) for HD >= 64 and
+// (dt, g + 2) for HD == 32.
+template <int HD>
+__device__ __forceinline__ void store_rows_T_rope(uint16_t* out_row, const f32x16 (&acc)[HD / 32], float mul,
+                                                  int hl, const uint16_t* cs, const uint16_t* sn) {
+  constexpr int ND = HD / 32, H2 = HD / 2;
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      if (dt * 32 + 8 * g >= H2) continue;  // upper half: written with its partner
+      const int dt2 = HD == 32 ? dt : dt + ND / 2, g2 = HD == 32 ? g + 2 : g;
+      const int d0 = dt * 32 + 8 * g + 4 * hl, d1 = d0 + H2;
+      float c0[4], c1[4], s0[4], s1[4], o0[4], o1[4];
+      unpack4_bf16(*reinterpret_cast<const uint2*>(cs + d0), c0);
+      unpack4_bf16(*reinterpret_cast<const uint2*>(cs + d1), c1);
+      unpack4_bf16(*reinterpret_cast<const uint2*>(sn + d0), s0);
+      unpack4_bf16(*reinterpret_cast<const uint2*>(sn + d1), s1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        rope_pair<uint16_t, true>(round_bf(acc[dt][4 * g + i] * mul), round_bf(acc[dt2][4 * g2 + i] * mul), c0[i],
+                                  c1[i], s0[i], s1[i], o0[i], o1[i]);
+      *reinterpret_cast<uint2*>(out_row + d0) = make_uint2(pk_bf16(o0[0], o0[1]), pk_bf16(o0[2], o0[3]));
+      *reinterpret_cast<uint2*>(out_row + d1) = make_uint2(pk_bf16(o1[0], o1[1]), pk_bf16(o1[2], o1[3]));
+    }
+}
+
+// The dQ / dK store of token `pos` (row tok0 + pos), rotated when rope.cos is set.
+template <int HD>
+__device__ __forceinline__ void store_grad_row(uint16_t* out_row, const f32x16 (&acc)[HD / 32], float mul, int hl,
+                                               const RopeRows<uint16_t>& rope, int64_t tok0, int pos) {
+  if (rope.cos) {
+    const int64_t r = rope.row(tok0, pos) * HD;
+    store_rows_T_rope<HD>(out_row, acc, mul, hl, rope.cos + r, rope.sin + r);
+  } else {
+    store_rows_T<HD>(out_row, acc, mul, hl);
+  }
+}
+
 // ------------------------------------------------------------ forward (bf16)
 // Block = 4 waves x (32*QT) queries of one (batch, head); loop over 64-key
 // blocks, double-buffered in LDS: the next block's K/V are loaded straight
@@ -367,7 +430,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const uint16_t* __restrict__ v, int64_t ldv, const uint16_t* __restrict__ o, int64_t ldo,
     const uint16_t* __restrict__ dO, int64_t lddo, const float* __restrict__ lse,
     float* __restrict__ delta, uint16_t* __restrict__ dq, int64_t lddq, int S, int nh, int group,
-    float scale_log2, float scale) {
+    float scale_log2, float scale, RopeRows<uint16_t> rope) {
   constexpr int BM = 128, BN = 64, NS = HD / 16, ND = HD / 32, TILE = BN * 2 * HD;
   __shared__ __align__(16) char sk0[TILE], sk1[TILE], sv0[TILE], sv1[TILE];
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
@@ -426,7 +489,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                             dq_block<HD>(K, V, qf, gf, dqacc, nlse2, dl, a_off, b0, b8, k0, qw, qi, hl, S,
                                          scale_log2);
                         });
-  if (qi < S) store_rows_T<HD>(dq + (tok0 + qi) * lddq + static_cast<int64_t>(h) * HD, dqacc, scale, hl);
+  if (qi < S) store_grad_row<HD>(dq + (tok0 + qi) * lddq + static_cast<int64_t>(h) * HD, dqacc, scale, hl, rope, tok0, qi);
 }
 
 // Load stage of the dK/dV kernels: the Q and dO tiles, lse and delta of one
@@ -560,7 +623,7 @@ __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves
     const uint16_t* __restrict__ v, int64_t ldv, const uint16_t* __restrict__ dO, int64_t lddo,
     const float* __restrict__ lse, const float* __restrict__ delta, uint16_t* __restrict__ dk,
     int64_t lddk, uint16_t* __restrict__ dv, int64_t lddv, int S, int nh, int nkv, int group,
-    float scale_log2, float scale) {
+    float scale_log2, float scale, RopeRows<uint16_t> rope) {
   constexpr int NWH = DkdvFusedTiles<HD>::NWH, NT = DkdvFusedTiles<HD>::NT;
   constexpr int BKN = NWH * 32, BQ = DkdvFusedTiles<HD>::BQ, NS = HD / 16, ND = HD / 32;
   constexpr int TILE = BQ * 2 * HD;
@@ -659,7 +722,7 @@ __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves
       for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
         for (int j = 0; j < 16; ++j) dkacc[dt][j] = dkacc[dt][j] + other[dt * 16 + j][lane];
-      if (ki < S) store_rows_T<HD>(dk + (tok0 + ki) * lddk + static_cast<int64_t>(kvh) * HD, dkacc, scale, hl);
+      if (ki < S) store_grad_row<HD>(dk + (tok0 + ki) * lddk + static_cast<int64_t>(kvh) * HD, dkacc, scale, hl, rope, tok0, ki);
     } else {
 #pragma unroll
       for (int dt = 0; dt < ND; ++dt)
@@ -699,7 +762,7 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) __attribute__((amdgpu_waves_per_
     const uint16_t* __restrict__ v, int64_t ldv, const uint16_t* __restrict__ dO, int64_t lddo,
     const float* __restrict__ lse, const float* __restrict__ delta, uint16_t* __restrict__ dk,
     int64_t lddk, uint16_t* __restrict__ dv, int64_t lddv, int S, int nh, int nkv, int group,
-    float scale_log2, float scale) {
+    float scale_log2, float scale, RopeRows<uint16_t> rope) {
   constexpr int NKS = DkdvTiles<HD>::NKS, NT = DkdvTiles<HD>::NT, BQ = DkdvTiles<HD>::BQ;
   constexpr int BKN = NKS * 32, NS = HD / 16, ND = HD / 32, NQT = BQ / 32, TILE = BQ * 2 * HD;
   // Two LDS stages as separate arrays (the loop below is unrolled by two),
@@ -834,13 +897,34 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) __attribute__((amdgpu_waves_per_
     if (role_a)
       store_rows_T<HD>(dv + (tok0 + ki) * lddv + static_cast<int64_t>(kvh) * HD, acc, 1.f, hl);
     else
-      store_rows_T<HD>(dk + (tok0 + ki) * lddk + static_cast<int64_t>(kvh) * HD, acc, scale, hl);
+      store_grad_row<HD>(dk + (tok0 + ki) * lddk + static_cast<int64_t>(kvh) * HD, acc, scale, hl, rope, tok0, ki);
   }
 }
 
 // --------------------------------------------------------- fp32 reference-precision kernels
 // Plain fp32 FMA kernels (one thread per output row) for fp32 models; the same
 // algorithm (online softmax forward with lse, delta-based backward) as above.
+
+// out[d] = acc[d] * mul, followed by the RoPE backward of the row when
+// rope.cos is set (the fp32 counterpart of store_grad_row).
+template <int HD>
+__device__ __forceinline__ void store_row_f32(float* out, const float (&acc)[HD], float mul,
+                                              const RopeRows<float>& rope, int64_t tok0, int pos) {
+  if (!rope.cos) {
+    for (int d = 0; d < HD; ++d) out[d] = acc[d] * mul;
+    return;
+  }
+  const int64_t r = rope.row(tok0, pos) * HD;
+  const float* cs = rope.cos + r;
+  const float* sn = rope.sin + r;
+  for (int d = 0; d < HD / 2; ++d) {
+    float o0, o1;
+    rope_pair<float, true>(acc[d] * mul, acc[d + HD / 2] * mul, cs[d], cs[d + HD / 2], sn[d], sn[d + HD / 2],
+                           o0, o1);
+    out[d] = o0;
+    out[d + HD / 2] = o1;
+  }
+}
 template <int HD>
 __global__ __launch_bounds__(128) void k_attn_fwd_f32(
     const float* __restrict__ q, int64_t ldq, const float* __restrict__ k, int64_t ldk,
@@ -879,7 +963,7 @@ __global__ __launch_bounds__(128) void k_attn_bwd_dq_f32(
     const float* __restrict__ q, int64_t ldq, const float* __restrict__ k, int64_t ldk,
     const float* __restrict__ v, int64_t ldv, const float* __restrict__ dO, int64_t lddo,
     const float* __restrict__ lse, const float* __restrict__ delta, float* __restrict__ dq,
-    int64_t lddq, int S, int nh, int group, float scale, int64_t rows) {
+    int64_t lddq, int S, int nh, int group, float scale, int64_t rows, RopeRows<float> rope) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= rows) return;
   const int s = static_cast<int>(idx % S);
@@ -904,7 +988,7 @@ __global__ __launch_bounds__(128) void k_attn_bwd_dq_f32(
     for (int d = 0; d < HD; ++d) acc[d] = fmaf(ds, kr[d], acc[d]);
   }
   float* out = dq + (b * S + s) * lddq + static_cast<int64_t>(h) * HD;
-  for (int d = 0; d < HD; ++d) out[d] = acc[d] * scale;
+  store_row_f32<HD>(out, acc, scale, rope, b * S, s);
 }
 
 template <int HD>
@@ -913,7 +997,7 @@ __global__ __launch_bounds__(128) void k_attn_bwd_dkdv_f32(
     const float* __restrict__ v, int64_t ldv, const float* __restrict__ dO, int64_t lddo,
     const float* __restrict__ lse, const float* __restrict__ delta, float* __restrict__ dk,
     int64_t lddk, float* __restrict__ dv, int64_t lddv, int S, int nh, int nkv, int group,
-    float scale, int64_t rows) {
+    float scale, int64_t rows, RopeRows<float> rope) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= rows) return;  // rows = B*nkv*S, idx = (b*nkv + kvh)*S + j
   const int j = static_cast<int>(idx % S);
@@ -945,7 +1029,8 @@ __global__ __launch_bounds__(128) void k_attn_bwd_dkdv_f32(
   }
   float* ok = dk + (b * S + j) * lddk + static_cast<int64_t>(kvh) * HD;
   float* ov = dv + (b * S + j) * lddv + static_cast<int64_t>(kvh) * HD;
-  for (int d = 0; d < HD; ++d) { ok[d] = ak[d] * scale; ov[d] = av[d]; }
+  for (int d = 0; d < HD; ++d) ov[d] = av[d];
+  store_row_f32<HD>(ok, ak, scale, rope, b * S, j);
 }
 
 // ------------------------------------------------------------------- host
@@ -1028,12 +1113,20 @@ extern "C" int fh_attn_fwd(fh_dtype dt, const void* q, int64_t ldq, const void* 
   return check_launch("fh_attn_fwd");
 }
 
-extern "C" int fh_attn_bwd(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t ldk,
-                           const void* v, int64_t ldv, const void* o, int64_t ldo,
-                           const void* dout, int64_t lddo, const float* lse, void* dq,
-                           int64_t lddq, void* dk, int64_t lddk, void* dv, int64_t lddv,
-                           void* workspace, int64_t batch, int64_t seq_len, int64_t n_heads,
-                           int64_t n_kv_heads, int64_t head_dim, float scale, hipStream_t stream) {
+namespace {
+
+// Rotary tables of fh_attn_bwd_rope as passed in (cos == null: no rotation).
+struct RopeArgs {
+  const void* cos;
+  const void* sin;
+  int per_token;
+};
+
+int attn_bwd_impl(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
+                  int64_t ldv, const void* o, int64_t ldo, const void* dout, int64_t lddo, const float* lse,
+                  void* dq, int64_t lddq, void* dk, int64_t lddk, void* dv, int64_t lddv, void* workspace,
+                  int64_t batch, int64_t seq_len, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                  float scale, const RopeArgs& rp, hipStream_t stream) {
   const Dims d{batch, seq_len, n_heads, n_kv_heads, head_dim};
   if (int e = check_dims(dt, d)) return e;
   if (batch == 0 || seq_len == 0) return FH_OK;
@@ -1054,6 +1147,9 @@ extern "C" int fh_attn_bwd(fh_dtype dt, const void* q, int64_t ldq, const void* 
   const int S = static_cast<int>(seq_len), nh = static_cast<int>(n_heads);
   const int nkv = static_cast<int>(n_kv_heads), group = static_cast<int>(n_heads / n_kv_heads);
   float* delta = static_cast<float*>(workspace);
+  const RopeRows<uint16_t> rb{static_cast<const uint16_t*>(rp.cos), static_cast<const uint16_t*>(rp.sin),
+                              rp.per_token};
+  const RopeRows<float> rf{static_cast<const float*>(rp.cos), static_cast<const float*>(rp.sin), rp.per_token};
   if (dt == FH_BF16) {
     // dQ first: its prologue writes delta = rowsum(dO*O), which dK/dV reads.
     const dim3 gq(static_cast<unsigned>((seq_len + 127) / 128), static_cast<unsigned>(batch * n_heads));
@@ -1063,7 +1159,7 @@ extern "C" int fh_attn_bwd(fh_dtype dt, const void* q, int64_t ldq, const void* 
                          static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(k), ldk,
                          static_cast<const uint16_t*>(v), ldv, static_cast<const uint16_t*>(o), ldo,
                          static_cast<const uint16_t*>(dout), lddo, lse, delta,
-                         static_cast<uint16_t*>(dq), lddq, S, nh, group, scale * kLog2e, scale);
+                         static_cast<uint16_t*>(dq), lddq, S, nh, group, scale * kLog2e, scale, rb);
       const auto kq = static_cast<const uint16_t*>(q);
       const auto kk = static_cast<const uint16_t*>(k);
       const auto kvp = static_cast<const uint16_t*>(v);
@@ -1076,14 +1172,14 @@ extern "C" int fh_attn_bwd(fh_dtype dt, const void* q, int64_t ldq, const void* 
         const dim3 gk(static_cast<unsigned>((nkb + 1) / 2), static_cast<unsigned>(batch * n_kv_heads));
         hipLaunchKernelGGL((k_attn_bwd_dkdv_fused<HD>), gk, dim3(DT::NT), 0, stream, kq, ldq, kk,
                            ldk, kvp, ldv, kg, lddo, lse, delta, kdk, lddk, kdv, lddv, S, nh, nkv,
-                           group, scale * kLog2e, scale);
+                           group, scale * kLog2e, scale, rb);
       } else {
         using DT = DkdvTiles<HD>;
         const int64_t nkb = (seq_len + DT::NKS * 32 - 1) / (DT::NKS * 32);
         const dim3 gk(static_cast<unsigned>(nkb), static_cast<unsigned>(batch * n_kv_heads));
         hipLaunchKernelGGL((k_attn_bwd_dkdv<HD>), gk, dim3(DT::NT), 0, stream, kq, ldq, kk, ldk,
                            kvp, ldv, kg, lddo, lse, delta, kdk, lddk, kdv, lddv, S, nh, nkv, group,
-                           scale * kLog2e, scale);
+                           scale * kLog2e, scale, rb);
       }
       return 0;
     });
@@ -1099,15 +1195,42 @@ extern "C" int fh_attn_bwd(fh_dtype dt, const void* q, int64_t ldq, const void* 
                          dim3(128), 0, stream, static_cast<const float*>(q), ldq,
                          static_cast<const float*>(k), ldk, static_cast<const float*>(v), ldv,
                          static_cast<const float*>(dout), lddo, lse, delta, static_cast<float*>(dq),
-                         lddq, S, nh, group, scale, qrows);
+                         lddq, S, nh, group, scale, qrows, rf);
       hipLaunchKernelGGL((k_attn_bwd_dkdv_f32<hdc()>), dim3(static_cast<unsigned>((krows + 127) / 128)),
                          dim3(128), 0, stream, static_cast<const float*>(q), ldq,
                          static_cast<const float*>(k), ldk, static_cast<const float*>(v), ldv,
                          static_cast<const float*>(dout), lddo, lse, delta,
                          static_cast<float*>(dk), lddk, static_cast<float*>(dv), lddv, S, nh, nkv,
-                         group, scale, krows);
+                         group, scale, krows, rf);
       return 0;
     });
   }
-  return check_launch("fh_attn_bwd");
+  return check_launch(rp.cos ? "fh_attn_bwd_rope" : "fh_attn_bwd");
+}
+
+}  // namespace
+
+extern "C" int fh_attn_bwd(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t ldk,
+                           const void* v, int64_t ldv, const void* o, int64_t ldo,
+                           const void* dout, int64_t lddo, const float* lse, void* dq,
+                           int64_t lddq, void* dk, int64_t lddk, void* dv, int64_t lddv,
+                           void* workspace, int64_t batch, int64_t seq_len, int64_t n_heads,
+                           int64_t n_kv_heads, int64_t head_dim, float scale, hipStream_t stream) {
+  return attn_bwd_impl(dt, q, ldq, k, ldk, v, ldv, o, ldo, dout, lddo, lse, dq, lddq, dk, lddk, dv, lddv,
+                       workspace, batch, seq_len, n_heads, n_kv_heads, head_dim, scale,
+                       RopeArgs{nullptr, nullptr, 0}, stream);
+}
+
+extern "C" int fh_attn_bwd_rope(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t ldk,
+                                const void* v, int64_t ldv, const void* o, int64_t ldo,
+                                const void* dout, int64_t lddo, const float* lse, void* dq,
+                                int64_t lddq, void* dk, int64_t lddk, void* dv, int64_t lddv,
+                                void* workspace, int64_t batch, int64_t seq_len, int64_t n_heads,
+                                int64_t n_kv_heads, int64_t head_dim, float scale, const void* cos,
+                                const void* sin, int cos_per_token, hipStream_t stream) {
+  FH_REQUIRE(cos && sin, "attn_bwd_rope: null cos/sin");
+  FH_REQUIRE(aligned16(cos) && aligned16(sin), "attn_bwd_rope: cos/sin must be 16-byte aligned");
+  return attn_bwd_impl(dt, q, ldq, k, ldk, v, ldv, o, ldo, dout, lddo, lse, dq, lddq, dk, lddk, dv, lddv,
+                       workspace, batch, seq_len, n_heads, n_kv_heads, head_dim, scale,
+                       RopeArgs{cos, sin, cos_per_token ? 1 : 0}, stream);
 }

@@ -136,6 +136,30 @@ struct Elem<float> {
   __device__ __forceinline__ static void st1(float* p, float f) { *p = f; }
 };
 
+// ------------------------------------------------------------ RoPE pair
+// Rotate-half rotary embedding of one pair (x0 at dim i, x1 at dim
+// i + head_dim/2; cos c0, c1 and sin s0, s1 at those dims), rounded with
+// Elem<T>::rnd wherever the reference materialises a tensor -- each product,
+// then the sum (q*cos + rotate_half(q)*sin, modeling_llama.py:130-160):
+//   forward:   o0 = x0*c0 - x1*s0,  o1 = x1*c1 + x0*s1
+//   backward (the transposed rotation, grad*cos + rotate_half^T(grad*sin)):
+//              o0 = x0*c0 + x1*s1,  o1 = x1*c1 - x0*s0
+// Multiply-add contraction is off, so the fp32 path also rounds each product
+// separately, as torch's elementwise ops do.
+template <typename T, bool BWD>
+__device__ __forceinline__ void rope_pair(float x0, float x1, float c0, float c1, float s0, float s1,
+                                          float& o0, float& o1) {
+#pragma clang fp contract(off)
+  using E = Elem<T>;
+  if constexpr (!BWD) {
+    o0 = E::rnd(E::rnd(x0 * c0) - E::rnd(x1 * s0));
+    o1 = E::rnd(E::rnd(x1 * c1) + E::rnd(x0 * s1));
+  } else {
+    o0 = E::rnd(E::rnd(x0 * c0) + E::rnd(x1 * s1));
+    o1 = E::rnd(E::rnd(x1 * c1) - E::rnd(x0 * s0));
+  }
+}
+
 // ------------------------------------------------------- wave reductions
 // DPP (data-parallel primitive) lane moves: VALU ops with no LDS round trip.
 template <int CTRL, int ROW_MASK = 0xf>

@@ -120,17 +120,7 @@ __global__ __launch_bounds__(256) void k_rope(T* __restrict__ qk, int64_t ld, in
     Elem<T>::unpack(r0[k], x0);
     Elem<T>::unpack(r1[k], x1);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if constexpr (!BWD) {
-        // q*cos + rotate_half(q)*sin, rotate_half(q) = cat(-q[d/2:], q[:d/2])
-        o0[j] = Elem<T>::rnd(Elem<T>::rnd(x0[j] * c0[j]) - Elem<T>::rnd(x1[j] * s0[j]));
-        o1[j] = Elem<T>::rnd(Elem<T>::rnd(x1[j] * c1[j]) + Elem<T>::rnd(x0[j] * s1[j]));
-      } else {
-        // transpose of the rotation: grad*cos + rotate_half^T(grad*sin)
-        o0[j] = Elem<T>::rnd(Elem<T>::rnd(x0[j] * c0[j]) + Elem<T>::rnd(x1[j] * s1[j]));
-        o1[j] = Elem<T>::rnd(Elem<T>::rnd(x1[j] * c1[j]) - Elem<T>::rnd(x0[j] * s0[j]));
-      }
-    }
+    for (int j = 0; j < 8; ++j) rope_pair<T, BWD>(x0[j], x1[j], c0[j], c1[j], s0[j], s1[j], o0[j], o1[j]);
     Elem<T>::store8(base + k * head_dim, o0);
     Elem<T>::store8(base + k * head_dim + half, o1);
   }

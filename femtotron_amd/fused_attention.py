@@ -21,7 +21,7 @@ It saves y, the rotated qkv, o and lse for backward, as the stock path saves
 the projections' input and SDPA's q, k, v, output and log-sum-exp.  The
 backward takes the same steps as the attention half of the fused layer: the o
 and q/k/v weight gradients run on the side stream, beside the input-gradient
-chain o-projection -> fh_attn_bwd -> fh_rope_bwd -> q/k/v projection.
+chain o-projection -> fh_attn_bwd_rope (RoPE backward in the dq/dk stores) -> q/k/v projection.
 
 A call the kernels do not cover runs the module's own forward: off a HIP
 device, another dtype, autocast, an attention mask, a KV cache, attention
@@ -89,9 +89,8 @@ class FusedAttentionFunction(torch.autograd.Function):
             side = _WgradStream(da2.device)
             dwo = side.mm_tn(da2, o)
             do = linear_dgrad(da2, wo)
-            dqkv = attn_bwd(do, qkv, o, lse, B, S, shp)
+            dqkv = attn_bwd(do, qkv, o, lse, B, S, shp, cos, sin)
             del do
-            ops.rope_bwd_(dqkv, shp.n_heads + shp.n_kv_heads, shp.head_dim, S, cos, sin)
             dwqkv = side.mm_tn(dqkv, y.reshape(B * S, H))
             dy = linear_dgrad(dqkv, _cat_rows(wq, wk, wv))
             side.join()

@@ -78,13 +78,14 @@ def attn_fwd(qkv: torch.Tensor, batch: int, seq: int, shp: "LayerShape", *, need
 
 
 def attn_bwd(do: torch.Tensor, qkv: torch.Tensor, o: torch.Tensor, lse: torch.Tensor, batch: int,
-             seq: int, shp: "LayerShape") -> torch.Tensor:
-    """dqkv [T, Hq+2Hkv] of attn_fwd (fh_attn_bwd)."""
+             seq: int, shp: "LayerShape", cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """dqkv [T, Hq+2Hkv] of RoPE then attn_fwd: the attention backward with the
+    RoPE backward of dq and dk fused into their stores (fh_attn_bwd_rope)."""
     q, k, v = _qkv_split(qkv, shp)
     dqkv = torch.empty_like(qkv)
     dq, dk, dv = _qkv_split(dqkv, shp)
     ops.attn_bwd(q, k, v, o, do, lse, dq, dk, dv, batch, seq, shp.n_heads, shp.n_kv_heads,
-                 shp.head_dim, shp.scale)
+                 shp.head_dim, shp.scale, rope=(cos, sin))
     return dqkv
 
 
@@ -204,10 +205,9 @@ def layer_backward(dout2: torch.Tensor, x2: torch.Tensor, cos: torch.Tensor, sin
     # attention output projection
     dwo = wg_stream.mm_tn(dh, acts.o)
     do = linear_dgrad(dh, wo)
-    dqkv = attn_bwd(do, acts.qkv, acts.o, acts.lse, batch, seq, shp)
+    dqkv = attn_bwd(do, acts.qkv, acts.o, acts.lse, batch, seq, shp, cos, sin)
     del do
     acts.o = acts.lse = acts.qkv = None
-    ops.rope_bwd_(dqkv, shp.n_heads + shp.n_kv_heads, shp.head_dim, seq, cos, sin)
     dwqkv = wg_stream.mm_tn(dqkv, acts.y1)
     dy1 = linear_dgrad(dqkv, _cat_rows(wq, wk, wv))
     del dqkv

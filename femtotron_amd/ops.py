@@ -138,21 +138,27 @@ def _rope(name: str, qk: torch.Tensor, n_heads: int, head_dim: int, seq_len: int
     ld = _rowmajor(qk, name)
     if qk.size(1) < n_heads * head_dim:
         raise ValueError(f"{name}: buffer narrower than n_heads*head_dim")
+    tokens = qk.size(0)
+    cos2, sin2, per_token = _rope_tables(name, cos, sin, head_dim, seq_len, tokens)
+    _lib.call(name, _dtype_code(qk), _ptr(qk), ld, tokens, seq_len, n_heads, head_dim, _ptr(cos2),
+              _ptr(sin2), per_token, _stream(qk))
+
+
+def _rope_tables(name: str, cos: torch.Tensor, sin: torch.Tensor, head_dim: int, seq_len: int,
+                 tokens: int):
+    """cos/sin as [rows, head_dim] views and the cos_per_token flag of the C ABI:
+    rows == seq_len (one row per position) or rows == tokens (one per token)."""
     cos2 = cos.reshape(-1, head_dim)
     sin2 = sin.reshape(-1, head_dim)
     if not (cos2.is_contiguous() and sin2.is_contiguous()) or cos2.shape != sin2.shape:
         raise ValueError(f"{name}: cos/sin must be contiguous and of equal shape")
-    tokens = qk.size(0)
     if cos2.size(0) == seq_len:
-        per_token = 0
         if tokens % seq_len:
             raise ValueError(f"{name}: tokens not a multiple of seq_len")
-    elif cos2.size(0) == tokens:
-        per_token = 1
-    else:
-        raise ValueError(f"{name}: cos/sin rows ({cos2.size(0)}) match neither seq_len nor tokens")
-    _lib.call(name, _dtype_code(qk), _ptr(qk), ld, tokens, seq_len, n_heads, head_dim, _ptr(cos2),
-              _ptr(sin2), per_token, _stream(qk))
+        return cos2, sin2, 0
+    if cos2.size(0) == tokens:
+        return cos2, sin2, 1
+    raise ValueError(f"{name}: cos/sin rows ({cos2.size(0)}) match neither seq_len nor tokens")
 
 
 def rope_fwd_(qk: torch.Tensor, n_heads: int, head_dim: int, seq_len: int, cos: torch.Tensor,
@@ -232,19 +238,29 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, batch: int, seq_
 def attn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
              dout: torch.Tensor, lse: torch.Tensor, dq: torch.Tensor, dk: torch.Tensor,
              dv: torch.Tensor, batch: int, seq_len: int, n_heads: int, n_kv_heads: int,
-             head_dim: int, scale: float) -> None:
-    """Writes dq, dk, dv (token-major views, may be column ranges of one buffer)."""
+             head_dim: int, scale: float, rope: tuple | None = None) -> None:
+    """Writes dq, dk, dv (token-major views, may be column ranges of one buffer).
+    rope=(cos, sin): dq and dk come out passed through the RoPE backward as well
+    (fh_attn_bwd_rope), the gradients before the rotation of q and k."""
     _require_gpu(q, k, v, o, dout, lse, dq, dk, dv)
     _same_dtype(q, k, v, o, dout, dq, dk, dv)
     if lse.dtype != torch.float32 or not lse.is_contiguous() or lse.numel() != batch * n_heads * seq_len:
         raise ValueError("attn_bwd: lse must be contiguous fp32 [batch, n_heads, seq_len]")
     ws_bytes = _lib.lib().fh_attn_bwd_workspace_size(batch, seq_len, n_heads)
     ws = torch.empty(max(ws_bytes, 4) // 4, dtype=torch.float32, device=q.device)
-    _lib.call("fh_attn_bwd", _dtype_code(q), _ptr(q), _rowmajor(q, "q"), _ptr(k), _rowmajor(k, "k"),
-              _ptr(v), _rowmajor(v, "v"), _ptr(o), _rowmajor(o, "o"), _ptr(dout),
-              _rowmajor(dout, "dout"), _fptr(lse), _ptr(dq), _rowmajor(dq, "dq"), _ptr(dk),
-              _rowmajor(dk, "dk"), _ptr(dv), _rowmajor(dv, "dv"), _ptr(ws), batch, seq_len,
-              n_heads, n_kv_heads, head_dim, float(scale), _stream(q))
+    args = (_dtype_code(q), _ptr(q), _rowmajor(q, "q"), _ptr(k), _rowmajor(k, "k"),
+            _ptr(v), _rowmajor(v, "v"), _ptr(o), _rowmajor(o, "o"), _ptr(dout),
+            _rowmajor(dout, "dout"), _fptr(lse), _ptr(dq), _rowmajor(dq, "dq"), _ptr(dk),
+            _rowmajor(dk, "dk"), _ptr(dv), _rowmajor(dv, "dv"), _ptr(ws), batch, seq_len,
+            n_heads, n_kv_heads, head_dim, float(scale))
+    if rope is None:
+        _lib.call("fh_attn_bwd", *args, _stream(q))
+        return
+    cos, sin = rope
+    _require_gpu(cos, sin)
+    _same_dtype(q, cos, sin)
+    cos2, sin2, per_token = _rope_tables("attn_bwd_rope", cos, sin, head_dim, seq_len, batch * seq_len)
+    _lib.call("fh_attn_bwd_rope", *args, _ptr(cos2), _ptr(sin2), per_token, _stream(q))
 
 
 # ------------------------------------------------------------- loss head

@@ -190,6 +190,22 @@ int fh_attn_bwd(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t 
                 void* workspace, int64_t batch, int64_t seq_len, int64_t n_heads,
                 int64_t n_kv_heads, int64_t head_dim, float scale, hipStream_t stream);
 
+/* fh_attn_bwd with the RoPE backward fused into the dq and dk stores: the
+ * result equals, bit for bit, fh_attn_bwd followed by fh_rope_bwd over dq's
+ * n_heads heads and over dk's n_kv_heads heads, i.e. the gradients with
+ * respect to the projections' outputs before apply_rotary_pos_emb
+ * (modeling_llama.py:130-160, 256).  cos/sin as in fh_rope_fwd (same dtype as
+ * the gradients, [seq_len, head_dim] or, with cos_per_token != 0,
+ * [batch*seq_len, head_dim]), 16-byte aligned.
+ */
+int fh_attn_bwd_rope(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t ldk,
+                     const void* v, int64_t ldv, const void* o, int64_t ldo,
+                     const void* dout, int64_t lddo, const float* lse, void* dq,
+                     int64_t lddq, void* dk, int64_t lddk, void* dv, int64_t lddv,
+                     void* workspace, int64_t batch, int64_t seq_len, int64_t n_heads,
+                     int64_t n_kv_heads, int64_t head_dim, float scale, const void* cos,
+                     const void* sin, int cos_per_token, hipStream_t stream);
+
 /* ------------------------------------------------------------------------
  * Causal-LM cross-entropy, forward and gradient in one pass, in place.
  * Replaces, for one chunk of rows of the logits, the loss head of

@@ -178,3 +178,52 @@ def test_attention_rejects_bad_head_dim():
     x = torch.zeros(16, 3 * 48, dtype=torch.bfloat16, device=DEV)
     with pytest.raises(FemtoHipError, match="head_dim"):
         _ops().attn_fwd(x[:, :48], x[:, 48:96], x[:, 96:], 1, 16, 1, 1, 48, 0.1)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("B,S,nh,nkv,hd,per_token", [
+    (2, 200, 8, 2, 64, False),    # GQA, ragged S, the TinyLlama head_dim
+    (1, 77, 4, 4, 32, True),      # MHA, per-token tables
+    (2, 131, 4, 1, 128, False),   # MQA, head_dim 128 (split-role dK/dV kernel)
+    (3, 64, 32, 4, 64, True),     # TinyLlama heads, per-token tables over 3 sequences
+])
+def test_attention_bwd_rope_equals_bwd_then_rope_bwd(dtype, B, S, nh, nkv, hd, per_token):
+    """fh_attn_bwd_rope == fh_attn_bwd followed by fh_rope_bwd over the dq and dk
+    heads, bit for bit (dv untouched).  The tables are random rather than real
+    cos/sin, so cos[i] != cos[i + hd/2] and sin[i] != sin[i + hd/2]: a rotation
+    that took the pair's own sin in place of its partner's, or rotated by the
+    wrong row, would differ."""
+    ops = _ops()
+    buf, do = _inputs(B, S, nh, nkv, hd, dtype, 21)
+    rows = B * S if per_token else S
+    cos = randn((rows, hd), 22).to(dtype).to(DEV)
+    sin = randn((rows, hd), 23).to(dtype).to(DEV)
+    g, d = buf.to(DEV), do.to(DEV)
+    hq, hkv = nh * hd, nkv * hd
+    q, k, v = g[:, :hq], g[:, hq:hq + hkv], g[:, hq + hkv:]
+    args = (B, S, nh, nkv, hd, hd ** -0.5)
+    o, lse = ops.attn_fwd(q, k, v, *args)
+    ref = torch.empty_like(g)
+    ops.attn_bwd(q, k, v, o, d, lse, ref[:, :hq], ref[:, hq:hq + hkv], ref[:, hq + hkv:], *args)
+    plain_dv = ref[:, hq + hkv:].clone()
+    ops.rope_bwd_(ref, nh + nkv, hd, S, cos, sin)
+    assert torch.equal(ref[:, hq + hkv:], plain_dv)
+    got = torch.full_like(g, float("nan"))
+    ops.attn_bwd(q, k, v, o, d, lse, got[:, :hq], got[:, hq:hq + hkv], got[:, hq + hkv:], *args,
+                 rope=(cos, sin))
+    torch.cuda.synchronize()
+    assert torch.isfinite(got).all()
+    assert torch.equal(got, ref)
+
+
+def test_attention_bwd_rope_rejects_bad_tables():
+    ops = _ops()
+    B, S, nh, nkv, hd = 1, 16, 2, 1, 32
+    g = torch.zeros(B * S, (nh + 2 * nkv) * hd, dtype=torch.bfloat16, device=DEV)
+    hq, hkv = nh * hd, nkv * hd
+    o, lse = ops.attn_fwd(g[:, :hq], g[:, hq:hq + hkv], g[:, hq + hkv:], B, S, nh, nkv, hd, 0.1)
+    dg = torch.empty_like(g)
+    cos = torch.zeros(S + 1, hd, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="neither seq_len nor tokens"):
+        ops.attn_bwd(g[:, :hq], g[:, hq:hq + hkv], g[:, hq + hkv:], o, g[:, :hq], lse, dg[:, :hq],
+                     dg[:, hq:hq + hkv], dg[:, hq + hkv:], B, S, nh, nkv, hd, 0.1, rope=(cos, cos))
