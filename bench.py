@@ -743,7 +743,7 @@ def main() -> int:
     from femtotron_amd import projections
     if args.tune_gemm_dispatch:
         wls = {name: (w["batch"] * w["seq"], w["hidden"], w["hidden"], w["kv"] * w["hidden"] // w["heads"],
-                      w["ffn"]) for name, (w, _, _) in WORKLOADS.items()}
+                      w["ffn"], w["hidden"] // w["heads"], w["seq"]) for name, (w, _, _) in WORKLOADS.items()}
         path = projections.measure_dispatch(wls, log=log)
         print(json.dumps({"gemm_dispatch": str(path)}), flush=True)
         return 0

@@ -12,7 +12,7 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_size_t, c_void_
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libfemtohip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 FH_BF16 = 0
 FH_F32 = 1
@@ -61,6 +61,8 @@ SIGNATURES: dict[str, tuple] = {
     "fh_adamw_workspace_size": (c_size_t, [_I64]),
     "fh_gemm_bf16_workspace_size": (c_size_t, [c_int, _I64, _I64, _I64]),
     "fh_gemm_bf16": (c_int, [c_int, _V, _I64, _V, _I64, _V, _I64, _V, _I64, _I64, _I64, _I64, _V, _V]),
+    "fh_gemm_bf16_rope": (c_int, [_V, _I64, _V, _I64, _V, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+                                  _V, _V, c_int, _V]),
     "fh_embedding_fwd": (c_int, [c_int, _V, _V, _V, _I64, _I64, _I64, _V]),
     "fh_embedding_bwd_workspace_size": (c_size_t, [_I64, _I64]),
     "fh_embedding_bwd": (c_int, [c_int, _V, _V, _V, _I64, _I64, _I64, _I64, _V, _V]),
@@ -88,13 +90,16 @@ def lib() -> ctypes.CDLL:
                 f"{LIB_PATH} is missing: build it with `python -m femtotron_amd.csrc.build` "
                 "(or __graft_entry__.build()) before using the fused path")
         handle = ctypes.CDLL(str(LIB_PATH))
+        # the version first: a stale library may lack entry points bound below
+        handle.fh_abi_version.restype = c_int
+        handle.fh_abi_version.argtypes = []
+        got = handle.fh_abi_version()
+        if got != ABI_VERSION:
+            raise FemtoHipError(f"libfemtohip ABI {got} != expected {ABI_VERSION}: rebuild it")
         for name, (restype, argtypes) in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.restype = restype
             fn.argtypes = argtypes
-        got = handle.fh_abi_version()
-        if got != ABI_VERSION:
-            raise FemtoHipError(f"libfemtohip ABI {got} != expected {ABI_VERSION}: rebuild it")
         _lib = handle
         return handle
 

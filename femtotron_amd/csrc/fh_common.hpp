@@ -160,6 +160,19 @@ __device__ __forceinline__ void rope_pair(float x0, float x1, float c0, float c1
   }
 }
 
+// One output of the forward rotation for a caller that holds its own element
+// x, the pair partner p, and cos c / sin s at its own dim: the lower half's
+// o0 = x*c - p*s and the upper half's o1 = x*c + p*s, rounded as rope_pair
+// rounds.  Round-to-nearest-even is symmetric, so rnd(p*s) negated equals
+// rnd(p*(-s)) and the caller passes s_signed = -s (lower) or s (upper): one
+// form covers both halves bit for bit.
+template <typename T>
+__device__ __forceinline__ float rope_fwd_one(float x, float p, float c, float s_signed) {
+#pragma clang fp contract(off)
+  using E = Elem<T>;
+  return E::rnd(E::rnd(x * c) + E::rnd(p * s_signed));
+}
+
 // ------------------------------------------------------- wave reductions
 // DPP (data-parallel primitive) lane moves: VALU ops with no LDS round trip.
 template <int CTRL, int ROW_MASK = 0xf>

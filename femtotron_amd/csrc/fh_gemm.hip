@@ -47,7 +47,19 @@ namespace {
 constexpr int kTm = 256, kTn = 256, kTk = 64;  // block tile and stage depth
 constexpr int kSubBytes = kTk * 128;           // KO sub-tile: [64 k x 64] bf16
 
-enum Epi { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_PARTIAL = 2 };
+enum Epi { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_PARTIAL = 2, EPI_ROPE = 3 };
+
+// The rotary embedding of EPI_ROPE: columns [0, rot_cols) of C are heads of
+// hd columns (hd a power of two dividing the 256-column tile, so no head
+// straddles a tile); row t of C is a token at position t % seq_len
+// (per_token == 0: cos/sin rows are positions) or t (per_token: rows are
+// tokens).
+struct GemmRope {
+  const uint16_t* cos;
+  const uint16_t* sin;
+  int rot_cols, hd, per_token, seq_len;
+  FastDiv seq;
+};
 
 struct GemmArgs {
   const uint16_t* a;
@@ -60,7 +72,22 @@ struct GemmArgs {
   int tiles_m, tiles_n, tiles;
   int steps_per_slice, total_steps;
   int grid;  // logical blocks (tiles * slices)
+  GemmRope rope;
 };
+
+// 8 outputs of the forward rotation (rope_fwd_one) from this chunk x, its
+// partner chunk p (hd/2 columns away in the head), and the cos / signed sin
+// chunks of its own columns.
+__device__ __forceinline__ uint4 rope_fwd_chunk(uint4 x, uint4 p, uint4 c, uint4 s) {
+  float xf[8], pf[8], cf[8], sf[8], o[8];
+  Elem<uint16_t>::unpack(x, xf);
+  Elem<uint16_t>::unpack(p, pf);
+  Elem<uint16_t>::unpack(c, cf);
+  Elem<uint16_t>::unpack(s, sf);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = rope_fwd_one<uint16_t>(xf[e], pf[e], cf[e], sf[e]);
+  return Elem<uint16_t>::pack(o);
+}
 
 // Lane offset of a transposing fragment read with K in natural order: lane i
 // gets rows 8*(i/32) + plus4 + 0..3 of column i%32 of a 32-wide column block
@@ -335,6 +362,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     bar();
     const int chunk = lane & 31;
     const int col = n0 + 8 * chunk;
+    if constexpr (EPI == EPI_ROPE) {
+      // Rotated columns read their partner chunk (hd/2 columns away, same
+      // head, same row) from the staged tile and the cos / sin chunks of
+      // their own columns; eight rows' loads are issued before their math.
+      const GemmRope& rp = g.rope;
+      const bool rot = col < rp.rot_cols;
+      const int hc = rp.hd >> 4, pc = chunk ^ hc, cofs = col & (rp.hd - 1);
+      const uint32_t sflip = (chunk & hc) ? 0u : 0x80008000u;  // lower half of a head: -sin
+#pragma unroll 1
+      for (int q0 = 0; q0 < 32; q0 += 8) {
+        uint4 v[8], pv[8], cv[8], sv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int r = 64 * wave + 2 * (q0 + u) + hl;
+          v[u] = *reinterpret_cast<const uint4*>(ring + r * 512 + ((chunk ^ (r & 15)) << 4));
+          if (rot) {
+            pv[u] = *reinterpret_cast<const uint4*>(ring + r * 512 + ((pc ^ (r & 15)) << 4));
+            const int t = min(m0 + r, g.m - 1);  // rows past m: an in-bounds read, never stored
+            const int pos = rp.per_token ? t : t - static_cast<int>(rp.seq.div(static_cast<uint32_t>(t))) * rp.seq_len;
+            const int64_t tb = static_cast<int64_t>(pos) * rp.hd + cofs;
+            cv[u] = *reinterpret_cast<const uint4*>(rp.cos + tb);
+            sv[u] = *reinterpret_cast<const uint4*>(rp.sin + tb);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int mrow = m0 + 64 * wave + 2 * (q0 + u) + hl;
+          uint4 o = v[u];
+          if (rot)
+            o = rope_fwd_chunk(v[u], pv[u], cv[u],
+                               make_uint4(sv[u].x ^ sflip, sv[u].y ^ sflip, sv[u].z ^ sflip, sv[u].w ^ sflip));
+          if (mrow < g.m && col < g.n) *reinterpret_cast<uint4*>(g.c + mrow * g.ldc + col) = o;
+        }
+      }
+      return;
+    }
 #pragma unroll 4
     for (int q2 = 0; q2 < 32; ++q2) {
       const int r = 64 * wave + 2 * q2 + hl;
@@ -424,6 +487,12 @@ int gemm_slices(int64_t m, int64_t n, int64_t k) {
 
 template <bool A_KO, bool B_KO>
 void launch(const GemmArgs& g, unsigned blocks, bool partial, bool resid, hipStream_t stream) {
+  if constexpr (!A_KO && !B_KO) {  // the rotated forward projection is NT only
+    if (g.rope.cos) {
+      hipLaunchKernelGGL((k_gemm<false, false, EPI_ROPE>), dim3(blocks), dim3(256), 0, stream, g);
+      return;
+    }
+  }
   if (partial)
     hipLaunchKernelGGL((k_gemm<A_KO, B_KO, EPI_PARTIAL>), dim3(blocks), dim3(256), 0, stream, g);
   else if (resid)
@@ -445,9 +514,11 @@ extern "C" size_t fh_gemm_bf16_workspace_size(int op, int64_t m, int64_t n, int6
   return s > 1 ? static_cast<size_t>(s) * m * n * sizeof(float) : 0;
 }
 
-extern "C" int fh_gemm_bf16(int op, const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
-                            int64_t ldc, const void* residual, int64_t ldr, int64_t m, int64_t n,
-                            int64_t k, void* workspace, hipStream_t stream) {
+namespace {
+
+// Checks the operands of one GEMM and fills g (tiling for `slices` K slices).
+int gemm_setup(int op, const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc,
+               const void* residual, int64_t ldr, int64_t m, int64_t n, int64_t k, GemmArgs& g) {
   FH_REQUIRE(valid_op(op), "gemm_bf16: op must be FH_GEMM_NT, FH_GEMM_NN or FH_GEMM_TN");
   FH_REQUIRE(m > 0 && n > 0 && k > 0, "gemm_bf16: sizes must be positive");
   FH_REQUIRE(k % 64 == 0, "gemm_bf16: k must be a multiple of 64");
@@ -468,16 +539,11 @@ extern "C" int fh_gemm_bf16(int op, const void* a, int64_t lda, const void* b, i
                "gemm_bf16: residual must be 16-byte aligned with ldr >= n, a multiple of 8");
     FH_REQUIRE(residual == c ? ldr == ldc : true, "gemm_bf16: residual aliasing c must share its ldc");
   }
-  const int slices = gemm_slices(m, n, k);
-  FH_REQUIRE(slices == 1 || (workspace && aligned16(workspace)),
-             "gemm_bf16: workspace (fh_gemm_bf16_workspace_size bytes) required");
-
-  GemmArgs g;
+  g = GemmArgs{};
   g.a = static_cast<const uint16_t*>(a);
   g.b = static_cast<const uint16_t*>(b);
   g.c = static_cast<uint16_t*>(c);
   g.r = static_cast<const uint16_t*>(residual);
-  g.part = static_cast<float*>(workspace);
   g.lda = lda;
   g.ldb = ldb;
   g.ldc = ldc;
@@ -488,27 +554,70 @@ extern "C" int fh_gemm_bf16(int op, const void* a, int64_t lda, const void* b, i
   g.tiles_n = static_cast<int>((n + kTn - 1) / kTn);
   g.tiles = g.tiles_m * g.tiles_n;
   g.total_steps = static_cast<int>(k / kTk);
+  return FH_OK;
+}
+
+// Launches the GEMM of g over `slices` K slices (partials in `workspace`,
+// summed by k_gemm_reduce, when slices > 1).
+int gemm_run(int op, GemmArgs& g, int slices, void* workspace, hipStream_t stream) {
+  g.part = static_cast<float*>(workspace);
   g.steps_per_slice = (g.total_steps + slices - 1) / slices;
   const int64_t logical = static_cast<int64_t>(g.tiles) * slices;
   FH_REQUIRE(logical <= 0x7ffffff0, "gemm_bf16: grid too large");
   g.grid = static_cast<int>(logical);
   const unsigned blocks = static_cast<unsigned>((logical + 7) / 8 * 8);
-  const bool partial = slices > 1, resid = residual != nullptr;
+  const bool partial = slices > 1, resid = g.r != nullptr;
   switch (op) {
     case FH_GEMM_NT: launch<false, false>(g, blocks, partial, resid, stream); break;
     case FH_GEMM_NN: launch<false, true>(g, blocks, partial, resid, stream); break;
     default: launch<true, true>(g, blocks, partial, resid, stream); break;
   }
   if (partial) {
-    const int64_t mn = m * n;
+    const int64_t mn = static_cast<int64_t>(g.m) * g.n;
     const unsigned rb = static_cast<unsigned>((mn / 4 + 255) / 256);
     if (resid)
       hipLaunchKernelGGL(k_gemm_reduce<true>, dim3(rb), dim3(256), 0, stream, g.part, slices, g.m, g.n, g.c,
-                         ldc, g.r, ldr);
+                         g.ldc, g.r, g.ldr);
     else
       hipLaunchKernelGGL(k_gemm_reduce<false>, dim3(rb), dim3(256), 0, stream, g.part, slices, g.m, g.n,
-                         g.c, ldc, nullptr, int64_t(0));
+                         g.c, g.ldc, nullptr, int64_t(0));
   }
+  return FH_OK;
+}
+
+}  // namespace
+
+extern "C" int fh_gemm_bf16(int op, const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
+                            int64_t ldc, const void* residual, int64_t ldr, int64_t m, int64_t n,
+                            int64_t k, void* workspace, hipStream_t stream) {
+  GemmArgs g;
+  if (int e = gemm_setup(op, a, lda, b, ldb, c, ldc, residual, ldr, m, n, k, g)) return e;
+  const int slices = gemm_slices(m, n, k);
+  FH_REQUIRE(slices == 1 || (workspace && aligned16(workspace)),
+             "gemm_bf16: workspace (fh_gemm_bf16_workspace_size bytes) required");
+  if (int e = gemm_run(op, g, slices, workspace, stream)) return e;
   return check_launch("fh_gemm_bf16");
 }
 
+extern "C" int fh_gemm_bf16_rope(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc,
+                                 int64_t m, int64_t n, int64_t k, int64_t rot_cols, int64_t head_dim,
+                                 int64_t seq_len, const void* cos, const void* sin, int cos_per_token,
+                                 hipStream_t stream) {
+  GemmArgs g;
+  if (int e = gemm_setup(FH_GEMM_NT, a, lda, b, ldb, c, ldc, nullptr, 0, m, n, k, g)) return e;
+  FH_REQUIRE(head_dim == 32 || head_dim == 64 || head_dim == 128, "gemm_bf16_rope: head_dim must be 32, 64 or 128");
+  FH_REQUIRE(rot_cols > 0 && rot_cols <= n && rot_cols % head_dim == 0,
+             "gemm_bf16_rope: rot_cols must be a positive multiple of head_dim, at most n");
+  FH_REQUIRE(seq_len > 0 && seq_len < (int64_t(1) << 30), "gemm_bf16_rope: seq_len out of range");
+  FH_REQUIRE(cos_per_token || m % seq_len == 0, "gemm_bf16_rope: m must be a multiple of seq_len");
+  FH_REQUIRE(cos && sin && aligned16(cos) && aligned16(sin), "gemm_bf16_rope: cos/sin null or not 16-byte aligned");
+  g.rope.cos = static_cast<const uint16_t*>(cos);
+  g.rope.sin = static_cast<const uint16_t*>(sin);
+  g.rope.rot_cols = static_cast<int>(rot_cols);
+  g.rope.hd = static_cast<int>(head_dim);
+  g.rope.per_token = cos_per_token ? 1 : 0;
+  g.rope.seq_len = static_cast<int>(seq_len);
+  g.rope.seq = FastDiv(static_cast<uint32_t>(seq_len));
+  if (int e = gemm_run(FH_GEMM_NT, g, 1, nullptr, stream)) return e;  // whole K: the epilogue sees final sums
+  return check_launch("fh_gemm_bf16_rope");
+}

@@ -13,15 +13,16 @@ o projection) with its activations stored for backward.
 kernels.  The module, its parameters and its state-dict keys stay as they are:
 
     qkv    = y [Wq;Wk;Wv]^T      one GEMM over the packed weights
-    q, k   = RoPE(q, k)          fh_rope_fwd, in place
+    q, k   = RoPE(q, k)          in the q/k/v GEMM's epilogue (or fh_rope_fwd after a library GEMM)
     o, lse = attention(qkv)      fh_attn_fwd, causal GQA
     a      = o Wo^T
 
 It saves y, the rotated qkv, o and lse for backward, as the stock path saves
 the projections' input and SDPA's q, k, v, output and log-sum-exp.  The
 backward takes the same steps as the attention half of the fused layer: the o
-and q/k/v weight gradients run on the side stream, beside the input-gradient
-chain o-projection -> fh_attn_bwd_rope (RoPE backward in the dq/dk stores) -> q/k/v projection.
+and q/k/v weight gradients (in series, or on the optional side stream), and the
+input-gradient chain o-projection -> fh_attn_bwd_rope (RoPE backward in the
+dq/dk stores) -> q/k/v projection.
 
 A call the kernels do not cover runs the module's own forward: off a HIP
 device, another dtype, autocast, an attention mask, a KV cache, attention
@@ -40,7 +41,7 @@ import torch
 from . import _lib, ops
 from .fused_checkpoint import _aligned, _check_params, _linear_weight
 from .fused_layer import LayerShape, _WgradStream, _cat_rows, attn_bwd, attn_fwd
-from .projections import linear, linear_dgrad
+from .projections import linear, linear_dgrad, linear_rope
 
 _ACCEPTED_KWARGS = {"position_ids", "use_cache", "cache_position"}
 _counts_lock = threading.Lock()
@@ -71,8 +72,8 @@ class FusedAttentionFunction(torch.autograd.Function):
     def forward(ctx, y, cos, sin, shp, wq, wk, wv, wo):
         B, S, H = y.shape
         y2 = y.reshape(B * S, H)
-        qkv = linear(y2, _cat_rows(wq, wk, wv))
-        ops.rope_fwd_(qkv, shp.n_heads + shp.n_kv_heads, shp.head_dim, S, cos, sin)
+        qkv = linear_rope(y2, _cat_rows(wq, wk, wv), shp.n_heads + shp.n_kv_heads, shp.head_dim, S, cos,
+                          sin)
         o, lse = attn_fwd(qkv, B, S, shp, need_lse=True)
         a = linear(o, wo)
         ctx.save_for_backward(y, cos, sin, qkv, o, lse, wq, wk, wv, wo)

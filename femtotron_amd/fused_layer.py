@@ -11,7 +11,8 @@ backward.
 Layer arithmetic (transformers 5.15.0, models/llama/modeling_llama.py:284-325):
     y1 = RMSNorm1(x)
     q,k,v = y1 Wq^T, y1 Wk^T, y1 Wv^T          -> one GEMM over [Wq;Wk;Wv]
-    q,k   = RoPE(q,k)                            (in place, fh_rope_fwd)
+    q,k   = RoPE(q,k)                            (in the GEMM's epilogue, fh_gemm_bf16_rope,
+                                                  or fh_rope_fwd after a library GEMM)
     o     = causal GQA attention(q,k,v)
     h     = x + o Wo^T;  z = RMSNorm2(h)         (fh_add_rmsnorm_fwd)
     g,u   = z Wg^T, z Wu^T                       -> one GEMM over [Wg;Wu]
@@ -34,7 +35,7 @@ from dataclasses import dataclass
 import torch
 
 from . import ops
-from .projections import linear, linear_dgrad, linear_residual, linear_wgrad
+from .projections import linear, linear_dgrad, linear_residual, linear_rope, linear_wgrad
 from .weight_packing import packed
 
 
@@ -108,8 +109,7 @@ def layer_forward(x2: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, shp: L
     y1 = ops.rmsnorm_fwd(x2, w1, shp.eps1, rstd=rstd1)
 
     wqkv = _cat_rows(wq, wk, wv)
-    qkv = linear(y1, wqkv)
-    ops.rope_fwd_(qkv, shp.n_heads + shp.n_kv_heads, shp.head_dim, seq, cos, sin)
+    qkv = linear_rope(y1, wqkv, shp.n_heads + shp.n_kv_heads, shp.head_dim, seq, cos, sin)
     o, lse = attn_fwd(qkv, batch, seq, shp, need_lse=keep)
     a = linear(o, wo)
     rstd2 = torch.empty(T, dtype=torch.float32, device=dev) if keep else None

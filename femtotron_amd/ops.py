@@ -394,3 +394,22 @@ def gemm(op: str, a: torch.Tensor, b: torch.Tensor, *, residual: torch.Tensor | 
     return c
 
 
+def gemm_rope(a: torch.Tensor, b: torch.Tensor, n_rot_heads: int, head_dim: int, seq_len: int,
+              cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """a [m,k] @ b[n,k]^T (the q/k/v projection) with the rotary embedding of
+    rope_fwd_ applied to heads 0..n_rot_heads-1 of the output in the GEMM's
+    epilogue (fh_gemm_bf16_rope); rows of a are tokens."""
+    _require_gpu(a, b, cos, sin)
+    if not gemm_supported("nt", a, b):
+        raise ValueError(f"gemm_rope: unsupported operands {tuple(a.shape)} {a.stride()} x "
+                         f"{tuple(b.shape)} {b.stride()} ({a.dtype}, {b.dtype})")
+    _same_dtype(a, cos, sin)
+    m, n, k = gemm_dims("nt", a, b)
+    cos2, sin2, per_token = _rope_tables("gemm_rope", cos, sin, head_dim, seq_len, m)
+    c = torch.empty(m, n, dtype=a.dtype, device=a.device)
+    _lib.call("fh_gemm_bf16_rope", _ptr(a), a.stride(0), _ptr(b), b.stride(0), _ptr(c), c.stride(0),
+              m, n, k, n_rot_heads * head_dim, head_dim, seq_len, _ptr(cos2), _ptr(sin2), per_token,
+              _stream(a))
+    return c
+
+

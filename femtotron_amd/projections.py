@@ -10,15 +10,19 @@ i.e. ``F.linear(x, W)`` with W [out, in] and no bias.  Its three GEMMs are:
 
 plus ``residual + x W^T`` with the residual add fused into the forward GEMM's
 epilogue (linear_residual; modeling_llama.py:323 rounds the projection output
-to bf16, then the sum).
+to bf16, then the sum), and the q/k/v projection with the rotary embedding of
+q and k in its epilogue (linear_rope, fh_gemm_bf16_rope) or, on the library
+path, the GEMM followed by the separate rotation (fh_rope_fwd).
 
 Each call runs either the hand-written gfx950 kernel or the tuned library
 GEMM (``torch.mm`` on hipBLASLt/rocBLAS), by policy:
 
 * ``"auto"`` (default): the shipped per-shape table
   ``tuned/gemm_dispatch_gfx950.json`` names the shapes measured on an MI355X
-  where the library was faster than the hand-written kernel; those run on the
-  library, every other supported shape on the hand-written kernel;
+  where the library was faster than the hand-written kernel (for linear_rope:
+  the library GEMM plus the separate rotation against the rotating kernel);
+  those run on the library, every other supported shape on the hand-written
+  kernel;
 * ``"hand"``: the hand-written kernel wherever it supports the operands;
 * ``"library"``: always the library.
 
@@ -69,7 +73,7 @@ def reset_gemm_dispatch_counts() -> None:
 def _library_shapes() -> dict[str, set]:
     global _table
     if _table is None:
-        shapes: dict[str, set] = {"nt": set(), "nn": set(), "tn": set()}
+        shapes: dict[str, set] = {"nt": set(), "nn": set(), "tn": set(), "nt_rope": set()}
         if TABLE_FILE.is_file():
             data = json.loads(TABLE_FILE.read_text())
             for op in shapes:
@@ -78,11 +82,11 @@ def _library_shapes() -> dict[str, set]:
     return _table
 
 
-def _use_hand(op: str, a: torch.Tensor, b: torch.Tensor) -> bool:
+def _use_hand(op: str, a: torch.Tensor, b: torch.Tensor, table: str | None = None) -> bool:
     pol = _policy[0]
     use = pol != "library" and ops.gemm_supported(op, a, b)
     if use and pol == "auto":
-        use = ops.gemm_dims(op, a, b) not in _library_shapes()[op]
+        use = ops.gemm_dims(op, a, b) not in _library_shapes()[table or op]
     with _lock:
         _counts["hand" if use else "library"] += 1
     return use
@@ -93,6 +97,16 @@ def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     if _use_hand("nt", x, w):
         return ops.gemm("nt", x, w)
     return torch.mm(x, w.t())
+
+
+def linear_rope(x: torch.Tensor, w: torch.Tensor, n_rot_heads: int, head_dim: int, seq_len: int,
+                cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """x [T, in] @ w[out, in]^T with heads 0..n_rot_heads-1 of the output (q and
+    k of the packed q/k/v projection) rotated by RoPE (rope_fwd_'s arithmetic)."""
+    if head_dim in (32, 64, 128) and _use_hand("nt", x, w, "nt_rope"):
+        return ops.gemm_rope(x, w, n_rot_heads, head_dim, seq_len, cos, sin)
+    y = linear(x, w)
+    return ops.rope_fwd_(y, n_rot_heads, head_dim, seq_len, cos, sin)
 
 
 def linear_residual(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
@@ -131,8 +145,10 @@ def measure_dispatch(workloads: dict, path: str | Path = TABLE_FILE, *, iters: i
                      log=print) -> Path:
     """Time the hand-written kernel against the library GEMM (with whatever
     library solutions the process has enabled) for every layer GEMM of
-    `workloads` ({name: (tokens, hidden, q width, kv width, ffn)}) and write
-    the shapes where the library was faster.  Needs a HIP device."""
+    `workloads` ({name: (tokens, hidden, q width, kv width, ffn, head_dim,
+    seq_len)}) and write the shapes where the library was faster; for the
+    q/k/v projection also the rotating kernel (fh_gemm_bf16_rope) against the
+    library GEMM + fh_rope_fwd.  Needs a HIP device."""
     dev, bf = "cuda", torch.bfloat16
     g = torch.Generator(device=dev).manual_seed(0)
     lib_faster: dict[str, list] = {"nt": [], "nn": [], "tn": []}
@@ -149,7 +165,25 @@ def measure_dispatch(workloads: dict, path: str | Path = TABLE_FILE, *, iters: i
         e.synchronize()
         return s.elapsed_time(e) / iters * 1e3
 
-    for name, (T, H, hq, hkv, F) in workloads.items():
+    lib_faster["nt_rope"] = []
+    for name, (T, H, hq, hkv, F, hd, S) in workloads.items():
+        # the q/k/v projection with its rotation: fused kernel against the
+        # library GEMM + fh_rope_fwd
+        m, n, k = T, hq + 2 * hkv, H
+        a = torch.randn(m, k, device=dev, generator=g).to(bf)
+        b = torch.randn(n, k, device=dev, generator=g).to(bf)
+        cos = torch.randn(S, hd, device=dev, generator=g).to(bf)
+        sin = torch.randn(S, hd, device=dev, generator=g).to(bf)
+        nr = (hq + hkv) // hd
+        t_hand = timed(lambda: ops.gemm_rope(a, b, nr, hd, S, cos, sin))
+        t_lib = timed(lambda: ops.rope_fwd_(torch.mm(a, b.t()), nr, hd, S, cos, sin))
+        rows.append(dict(workload=name, op="nt_rope", m=m, n=n, k=k, hand_us=round(t_hand, 1),
+                         library_us=round(t_lib, 1)))
+        if t_lib < t_hand and [m, n, k] not in lib_faster["nt_rope"]:
+            lib_faster["nt_rope"].append([m, n, k])
+        log(f"[gemm-dispatch] {name} nt_rope m={m} n={n} k={k}: hand {t_hand:.1f} us, "
+            f"library + rope {t_lib:.1f} us")
+        del a, b
         for op, m, n, k in layer_gemm_forms(T, H, hq, hkv, F):
             a_shape = (k, m) if op == "tn" else (m, k)
             b_shape = (n, k) if op == "nt" else (k, n)
@@ -167,7 +201,8 @@ def measure_dispatch(workloads: dict, path: str | Path = TABLE_FILE, *, iters: i
                 f"library {t_lib:.1f} us")
             del a, b
     data = {"note": "shapes (m, n, k of fh_gemm_bf16) where the tuned library GEMM measured faster "
-                    "than the hand-written kernel on an MI355X; everything else runs hand-written",
+                    "than the hand-written kernel on an MI355X (nt_rope: the library GEMM followed by "
+                    "fh_rope_fwd against fh_gemm_bf16_rope); everything else runs hand-written",
             "library": lib_faster, "measurements": rows}
     Path(path).write_text(json.dumps(data, indent=1) + "\n")
     global _table

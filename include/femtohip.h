@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define FH_ABI_VERSION 2
+#define FH_ABI_VERSION 3
 
 typedef enum fh_dtype {
   FH_BF16 = 0, /* bfloat16 storage, fp32 arithmetic */
@@ -330,6 +330,22 @@ size_t fh_gemm_bf16_workspace_size(int op, int64_t m, int64_t n, int64_t k);
 int fh_gemm_bf16(int op, const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
                  int64_t ldc, const void* residual, int64_t ldr, int64_t m, int64_t n,
                  int64_t k, void* workspace, hipStream_t stream);
+
+/* The q/k/v projection with the rotary embedding in its epilogue: C = A B^T
+ * (FH_GEMM_NT, no residual) and then, on columns [0, rot_cols) of C (the q and
+ * k heads of head_dim columns each), the rotation of fh_rope_fwd -- bit for
+ * bit fh_gemm_bf16 followed by fh_rope_fwd(FH_BF16, c, ldc, m, seq_len,
+ * rot_cols / head_dim, head_dim, cos, sin, cos_per_token), i.e.
+ * apply_rotary_pos_emb(q_proj(x), k_proj(x)) of modeling_llama.py:130-160,
+ * 253-256.  Rows of C are tokens (row t at position t % seq_len; m a multiple
+ * of seq_len unless cos_per_token).  head_dim in {32, 64, 128}; rot_cols a
+ * multiple of head_dim, at most n; cos/sin bf16 [seq_len or m, head_dim],
+ * 16-byte aligned.  K is never split: no workspace.
+ */
+int fh_gemm_bf16_rope(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
+                      int64_t ldc, int64_t m, int64_t n, int64_t k, int64_t rot_cols,
+                      int64_t head_dim, int64_t seq_len, const void* cos, const void* sin,
+                      int cos_per_token, hipStream_t stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

@@ -146,3 +146,45 @@ def test_gemm_rejects_unsupported_operands():
     wide = torch.empty(128, 132, device=DEV, dtype=BF)
     with pytest.raises(ValueError):
         ops.gemm("nt", x, x, out=wide[:, :128])
+
+
+@pytest.mark.parametrize("m,seq,nh,nkv,hd,k,per_token", [
+    (16384, 2048, 32, 4, 64, 2048, False),  # the TinyLlama q/k/v projection
+    (600, 200, 8, 2, 64, 256, False),       # ragged m (not a multiple of the 256-row tile), 3 sequences
+    (333, 111, 4, 4, 32, 128, True),        # per-token tables, MHA, head_dim 32
+    (512, 256, 4, 1, 128, 192, False),      # head_dim 128, MQA
+])
+def test_gemm_rope_equals_gemm_then_rope_fwd(m, seq, nh, nkv, hd, k, per_token):
+    """fh_gemm_bf16_rope == fh_gemm_bf16 (NT) followed by fh_rope_fwd over the q and
+    k heads, bit for bit; the v heads are the plain product.  Random tables
+    (cos[i] != cos[i + hd/2]) so that a partner or sign mix-up shows."""
+    g = torch.Generator(device=DEV).manual_seed(m + hd)
+    n = (nh + 2 * nkv) * hd
+    a, b = _operands("nt", m, n, k, g)
+    rows = m if per_token else seq
+    cos = torch.randn(rows, hd, device=DEV, generator=g).to(BF)
+    sin = torch.randn(rows, hd, device=DEV, generator=g).to(BF)
+    assert _lib.lib().fh_gemm_bf16_workspace_size(_lib.FH_GEMM_NT, m, n, k) == 0  # one K slice
+    ref = ops.gemm("nt", a, b)
+    plain_v = ref[:, (nh + nkv) * hd:].clone()
+    ops.rope_fwd_(ref, nh + nkv, hd, seq, cos, sin)
+    assert torch.equal(ref[:, (nh + nkv) * hd:], plain_v)
+    got = ops.gemm_rope(a, b, nh + nkv, hd, seq, cos, sin)
+    assert torch.equal(got, ref)
+
+
+def test_gemm_rope_rejects_bad_arguments():
+    from femtotron_amd._lib import FemtoHipError
+    x = torch.randn(256, 128, device=DEV).to(BF)
+    cos = torch.randn(256, 48, device=DEV).to(BF)
+    with pytest.raises(FemtoHipError, match="head_dim"):
+        ops.gemm_rope(x, x, 2, 48, 256, cos, cos)
+    c64 = torch.randn(256, 64, device=DEV).to(BF)
+    lib = _lib.lib()
+    # rot_cols beyond n, and m not a multiple of seq_len with per-position tables
+    st = lib.fh_gemm_bf16_rope(x.data_ptr(), 128, x.data_ptr(), 128, x.data_ptr(), 128, 256, 128, 128,
+                               192, 64, 256, c64.data_ptr(), c64.data_ptr(), 0, None)
+    assert st == 1 and b"rot_cols" in lib.fh_last_error()
+    st = lib.fh_gemm_bf16_rope(x.data_ptr(), 128, x.data_ptr(), 128, x.data_ptr(), 128, 256, 128, 128,
+                               128, 64, 100, c64.data_ptr(), c64.data_ptr(), 0, None)
+    assert st == 1 and b"multiple of seq_len" in lib.fh_last_error()
