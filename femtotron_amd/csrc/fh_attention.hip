@@ -194,19 +194,32 @@ struct FwdTiles {
 // arrays and the loop is unrolled by two, so every access names its stage
 // and the compiler can tell that the loads into one stage do not alias the
 // reads of the other (it would otherwise wait for them before every read).
-template <int BN, int HD, class Body>
+// FAST: per-lane load addresses computed once (TileDma: no vector address
+// arithmetic per load, 4-8 more registers); the dQ kernel, at the edge of an
+// occupancy step, computes them per load instead (dma_tile).
+template <int BN, int HD, bool FAST, class Body>
 __device__ __forceinline__ void kv_block_loop(const uint16_t* kb_ptr, int64_t ldk, const uint16_t* vb_ptr,
                                               int64_t ldv, int nkb, int S, char* sk0, char* sk1, char* sv0,
                                               char* sv1, int wave, int lane, Body&& body) {
-  dma_tile<BN, HD, 4>(kb_ptr, ldk, 0, S - 1, sk0, wave, lane);
-  dma_tile<BN, HD, 4>(vb_ptr, ldv, 0, S - 1, sv0, wave, lane);
+  TileDma<BN, HD, 4> dk, dv;
+  if constexpr (FAST) {
+    dk.init(ldk, wave, lane);
+    dv.init(ldv, wave, lane);
+  }
+  auto load = [&](int r0, char* KN, char* VN) __attribute__((always_inline)) {
+    if constexpr (FAST) {
+      dk.load(kb_ptr, ldk, r0, S - 1, KN, wave, lane);
+      dv.load(vb_ptr, ldv, r0, S - 1, VN, wave, lane);
+    } else {
+      dma_tile<BN, HD, 4>(kb_ptr, ldk, r0, S - 1, KN, wave, lane);
+      dma_tile<BN, HD, 4>(vb_ptr, ldv, r0, S - 1, VN, wave, lane);
+    }
+  };
+  load(0, sk0, sv0);
   wait_loads();
   __syncthreads();
   auto step = [&](int kb, const char* K, const char* V, char* KN, char* VN) __attribute__((always_inline)) {
-    if (kb + 1 < nkb) {
-      dma_tile<BN, HD, 4>(kb_ptr, ldk, (kb + 1) * BN, S - 1, KN, wave, lane);
-      dma_tile<BN, HD, 4>(vb_ptr, ldv, (kb + 1) * BN, S - 1, VN, wave, lane);
-    }
+    if (kb + 1 < nkb) load((kb + 1) * BN, KN, VN);
     if (kb < nkb) body(kb, K, V);
     wait_loads();
     __syncthreads();
@@ -244,12 +257,14 @@ __device__ __forceinline__ void fwd_block(const char* K, const char* V, const bf
     const int qi = qw + 32 * u + l32;
     float mloc = -INFINITY;
     if (need_mask) {  // diagonal or ragged block
+      // key = k0 + 32t + acc_row(j, hl) is masked when key > qi or key >= S,
+      // i.e. when its compile-time part 32t + acc_row(j, 0) exceeds lim.
+      const int lim = min(qi, S - 1) - k0 - 4 * hl;
 #pragma unroll
       for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-          const int key = k0 + 32 * t + acc_row(j, hl);
-          x[t][u][j] = ((key > qi) | (key >= S)) ? -INFINITY : x[t][u][j];
+          x[t][u][j] = 32 * t + acc_row(j, 0) > lim ? -INFINITY : x[t][u][j];
           mloc = fmaxf(mloc, x[t][u][j]);
         }
     } else {
@@ -270,22 +285,24 @@ __device__ __forceinline__ void fwd_block(const char* K, const char* V, const bf
         for (int j = 0; j < 16; ++j) oacc[u][dt][j] *= alpha;
     }
     const float nm = -m[u];
-    float lsum = 0.f;
 #pragma unroll
     for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const float p = fast_exp2(fmaf(x[t][u][j], scale_log2, nm));
-        x[t][u][j] = p;
-        lsum += p;
-      }
-    l[u] += lsum;
+      for (int j = 0; j < 16; ++j) x[t][u][j] = fast_exp2(fmaf(x[t][u][j], scale_log2, nm));
   }
+  // The row sums add the bf16 weights that P V multiplies (v_dot2 on the
+  // packed fragments), so the normalisation matches the weights used.
+  float lsum[QT];
+#pragma unroll
+  for (int u = 0; u < QT; ++u) lsum[u] = 0.f;
 #pragma unroll
   for (int s = 0; s < BN / 16; ++s) {
     bf16x8 pf[QT];
 #pragma unroll
-    for (int u = 0; u < QT; ++u) pf[u] = pack_frag(x[s >> 1][u], 8 * (s & 1));
+    for (int u = 0; u < QT; ++u) {
+      pf[u] = pack_frag(x[s >> 1][u], 8 * (s & 1));
+      lsum[u] = sum_bf16x8(pf[u], lsum[u]);
+    }
 #pragma unroll
     for (int dt = 0; dt < ND; ++dt) {
       const bf16x8 a = lds_frag_tr<HD>(V, b0, b8, 16 * s, dt);
@@ -293,6 +310,8 @@ __device__ __forceinline__ void fwd_block(const char* K, const char* V, const bf
       for (int u = 0; u < QT; ++u) oacc[u][dt] = mfma(a, pf[u], oacc[u][dt]);
     }
   }
+#pragma unroll
+  for (int u = 0; u < QT; ++u) l[u] += lsum[u];
 }
 
 template <int HD>
@@ -336,7 +355,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   const int nkb = (kend + BN - 1) / BN;
   const uint16_t* kb_ptr = k + tok0 * ldk + static_cast<int64_t>(kvh) * HD;
   const uint16_t* vb_ptr = v + tok0 * ldv + static_cast<int64_t>(kvh) * HD;
-  kv_block_loop<BN, HD>(kb_ptr, ldk, vb_ptr, ldv, nkb, S, sk0, sk1, sv0, sv1, wave, lane,
+  kv_block_loop<BN, HD, true>(kb_ptr, ldk, vb_ptr, ldv, nkb, S, sk0, sk1, sv0, sv1, wave, lane,
                         [&](int kb, const char* K, const char* V) __attribute__((always_inline)) {
                           refresh_offsets(a_off, b0, b8);
                           const int k0 = kb * BN;
@@ -404,11 +423,12 @@ __device__ __forceinline__ void dq_block(const char* K, const char* V, const bf1
       y = mfma(lds_frag<HD>(V, a_off, 32 * t, s), gf[s], y);
     }
     if (need_mask) {
+      // key = k0 + 32t + acc_row(j, hl) is dead when key > qi or key >= S.
+      const int lim = min(qi, S - 1) - k0 - 32 * t - 4 * hl;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const int key = k0 + 32 * t + acc_row(j, hl);
         const float p = fast_exp2(fmaf(x[j], scale_log2, nlse2));
-        x[j] = ((key > qi) | (key >= S)) ? 0.f : p * (y[j] - dl);  // dS^T
+        x[j] = acc_row(j, 0) > lim ? 0.f : p * (y[j] - dl);  // dS^T
       }
     } else {
 #pragma unroll
@@ -429,8 +449,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
     const uint16_t* __restrict__ v, int64_t ldv, const uint16_t* __restrict__ o, int64_t ldo,
     const uint16_t* __restrict__ dO, int64_t lddo, const float* __restrict__ lse,
-    float* __restrict__ delta, uint16_t* __restrict__ dq, int64_t lddq, int S, int nh, int group,
-    float scale_log2, float scale, RopeRows<uint16_t> rope) {
+    float* __restrict__ delta, float* __restrict__ nl2, uint16_t* __restrict__ dq, int64_t lddq, int S,
+    int nh, int group, float scale_log2, float scale, RopeRows<uint16_t> rope) {
   constexpr int BM = 128, BN = 64, NS = HD / 16, ND = HD / 32, TILE = BN * 2 * HD;
   __shared__ __align__(16) char sk0[TILE], sk1[TILE], sv0[TILE], sv1[TILE];
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
@@ -470,7 +490,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     dl = xor32_sum(part);
     if (qi < S) {
       nlse2 = -lse[static_cast<int64_t>(bh) * S + qi] * kLog2e;
-      if (hl == 0) delta[static_cast<int64_t>(bh) * S + qi] = dl;
+      if (hl == 0) {
+        delta[static_cast<int64_t>(bh) * S + qi] = dl;
+        nl2[static_cast<int64_t>(bh) * S + qi] = nlse2;
+      }
     }
   }
   f32x16 dqacc[ND];
@@ -481,7 +504,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   const int nkb = (kend + BN - 1) / BN;
   const uint16_t* kb_ptr = k + tok0 * ldk + static_cast<int64_t>(kvh) * HD;
   const uint16_t* vb_ptr = v + tok0 * ldv + static_cast<int64_t>(kvh) * HD;
-  kv_block_loop<BN, HD>(kb_ptr, ldk, vb_ptr, ldv, nkb, S, sk0, sk1, sv0, sv1, wave, lane,
+  kv_block_loop<BN, HD, false>(kb_ptr, ldk, vb_ptr, ldv, nkb, S, sk0, sk1, sv0, sv1, wave, lane,
                         [&](int kb, const char* K, const char* V) __attribute__((always_inline)) {
                           refresh_offsets(a_off, b0, b8);
                           const int k0 = kb * BN;
@@ -492,14 +515,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   if (qi < S) store_grad_row<HD>(dq + (tok0 + qi) * lddq + static_cast<int64_t>(h) * HD, dqacc, scale, hl, rope, tok0, qi);
 }
 
-// Load stage of the dK/dV kernels: the Q and dO tiles, lse and delta of one
+// Load stage of the dK/dV kernels: the Q and dO tiles, -lse*log2(e) and delta of one
 // (query tile, query head) item of the loop, loaded straight into an LDS
 // stage.  Items run from the last query tile down to the key block's first
 // (qt0), and over the group's query heads within a tile: all blocks of one kv
 // head start at the same tile and move down together, so a tile loaded by one
-// block is found in L2 by the others.  q, dO, lse, delta point at the group's
-// first query head; lse/delta rows are [head][S].  The tiles go through
-// dma_tile; the last wave loads the raw lse and delta of 64 rows from the
+// block is found in L2 by the others.  q, dO, nl2, delta point at the group's
+// first query head; nl2/delta rows are [head][S].  The tiles go through
+// TileDma; the last wave loads -lse*log2(e) and delta of 64 rows from the
 // tile's first (sl and sd hold 64 floats; rows from BQ on are unused).  Rows
 // past S re-read row S - 1: the kernels mask their weights to zero.  No
 // registers hold the tiles; the caller waits for its own loads (vmcnt) before
@@ -507,9 +530,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 template <int HD, int BQ, int NT>
 struct QTileDma {
   int qt = 0, hh = 0;  // the item to fetch next
-  __device__ __forceinline__ void start(int qt_end) {
+  TileDma<BQ, HD, NT / 64> tq, tg;  // per-lane load offsets of the Q and dO tiles
+  __device__ __forceinline__ void start(int qt_end, int64_t ldq, int64_t lddo, int wave, int lane) {
     qt = qt_end - 1;
     hh = 0;
+    tq.init(ldq, wave, lane);
+    tg.init(lddo, wave, lane);
   }
   __device__ __forceinline__ void advance(int group) {
     if (++hh == group) {
@@ -518,7 +544,7 @@ struct QTileDma {
     }
   }
   __device__ __forceinline__ void fetch(const uint16_t* q, int64_t ldq, const uint16_t* dO,
-                                        int64_t lddo, const float* lse, const float* delta,
+                                        int64_t lddo, const float* nl2, const float* delta,
                                         int S, int qt0, int group, char* sq, char* sg, float* sl,
                                         float* sd, int wave, int lane) {
     typedef __attribute__((address_space(1))) const void* gptr;
@@ -527,11 +553,11 @@ struct QTileDma {
     static_assert(BQ <= 64, "one lse/delta load covers the tile's rows");
     const int qs = max(qt, qt0) * BQ;
     const int64_t hcol = static_cast<int64_t>(hh) * HD;
-    dma_tile<BQ, HD, NW>(q + hcol, ldq, qs, S - 1, sq, wave, lane);
-    dma_tile<BQ, HD, NW>(dO + hcol, lddo, qs, S - 1, sg, wave, lane);
+    tq.load(q + hcol, ldq, qs, S - 1, sq, wave, lane);
+    tg.load(dO + hcol, lddo, qs, S - 1, sg, wave, lane);
     if (wave == NW - 1) {
       const int64_t row = static_cast<int64_t>(hh) * S + min(qs + lane, S - 1);
-      __builtin_amdgcn_global_load_lds((gptr)(lse + row), (lptr)sl, 4, 0, 0);
+      __builtin_amdgcn_global_load_lds((gptr)(nl2 + row), (lptr)sl, 4, 0, 0);
       __builtin_amdgcn_global_load_lds((gptr)(delta + row), (lptr)sd, 4, 0, 0);
     }
     advance(group);
@@ -586,7 +612,7 @@ __device__ __forceinline__ void dkdv_tile(const char* Q, const char* G, const fl
   for (int g = 0; g < 4; ++g) {
     const float4 L4 = *reinterpret_cast<const float4*>(&sl[hrow + 8 * g + 4 * hl]);
     const float4 D4 = *reinterpret_cast<const float4*>(&sd[hrow + 8 * g + 4 * hl]);
-    const float Lv[4] = {-L4.x * kLog2e, -L4.y * kLog2e, -L4.z * kLog2e, -L4.w * kLog2e};
+    const float Lv[4] = {L4.x, L4.y, L4.z, L4.w};  // -lse * log2(e)
     const float Dv[4] = {D4.x, D4.y, D4.z, D4.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -597,10 +623,13 @@ __device__ __forceinline__ void dkdv_tile(const char* Q, const char* G, const fl
     }
   }
   if (need_mask) {
+    // query qa = qh + acc_row(j, hl) is dead for this lane's key ki when
+    // qa < ki, qa >= S or ki >= S: its compile-time part acc_row(j, 0) lies
+    // outside [lo, hi) (an empty range when ki >= S).
+    const int lo = ki - qh - 4 * hl, hi = ki < S ? S - qh - 4 * hl : lo;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const int qa = qh + acc_row(j, hl);
-      const bool dead = (ki > qa) | (qa >= S) | (ki >= S);
+      const bool dead = (acc_row(j, 0) < lo) | (acc_row(j, 0) >= hi);
       x[j] = dead ? 0.f : x[j];
       y[j] = dead ? 0.f : y[j];
     }
@@ -621,7 +650,7 @@ template <int HD>
 __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_bwd_dkdv_fused(
     const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
     const uint16_t* __restrict__ v, int64_t ldv, const uint16_t* __restrict__ dO, int64_t lddo,
-    const float* __restrict__ lse, const float* __restrict__ delta, uint16_t* __restrict__ dk,
+    const float* __restrict__ nl2, const float* __restrict__ delta, uint16_t* __restrict__ dk,
     int64_t lddk, uint16_t* __restrict__ dv, int64_t lddv, int S, int nh, int nkv, int group,
     float scale_log2, float scale, RopeRows<uint16_t> rope) {
   constexpr int NWH = DkdvFusedTiles<HD>::NWH, NT = DkdvFusedTiles<HD>::NT;
@@ -632,7 +661,7 @@ __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves
   // access names its stage statically and the compiler can tell that the
   // direct-to-LDS loads into one stage do not alias the reads of the other.
   __shared__ __align__(16) char sq0[TILE], sq1[TILE], sg0[TILE], sg1[TILE];
-  __shared__ __align__(16) float sl0[BQ], sl1[BQ], sd0[BQ], sd1[BQ];  // raw lse and delta
+  __shared__ __align__(16) float sl0[BQ], sl1[BQ], sd0[BQ], sd1[BQ];  // -lse*log2(e) and delta
   __shared__ __align__(16) float xchg[2][NWH][ND * 16][64];  // [0]: dV of half 0, [1]: dK of half 1
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
@@ -647,7 +676,7 @@ __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves
   const int64_t h0 = static_cast<int64_t>(kvh) * group;
   const uint16_t* qg = q + tok0 * ldq + h0 * HD;
   const uint16_t* gg = dO + tok0 * lddo + h0 * HD;
-  const float* lg = lse + (static_cast<int64_t>(b) * nh + h0) * S;
+  const float* lg = nl2 + (static_cast<int64_t>(b) * nh + h0) * S;
   const float* dg = delta + (static_cast<int64_t>(b) * nh + h0) * S;
   const int qt_end = (S + BQ - 1) / BQ;
   const int hrow = 32 * half;  // this wave's first query row within a tile
@@ -681,7 +710,7 @@ __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves
     const int qt0 = (jb * BKN) / BQ;
     const int n_it = group * (qt_end - qt0);
     QTileDma<HD, BQ, NT> pre;
-    pre.start(qt_end);
+    pre.start(qt_end, ldq, lddo, wave, lane);
     pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, sq0, sg0, sl0, sd0, wave, lane);
     wait_loads();
     __syncthreads();
@@ -760,7 +789,7 @@ template <int HD>
 __global__ __launch_bounds__(DkdvTiles<HD>::NT) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_bwd_dkdv(
     const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
     const uint16_t* __restrict__ v, int64_t ldv, const uint16_t* __restrict__ dO, int64_t lddo,
-    const float* __restrict__ lse, const float* __restrict__ delta, uint16_t* __restrict__ dk,
+    const float* __restrict__ nl2, const float* __restrict__ delta, uint16_t* __restrict__ dk,
     int64_t lddk, uint16_t* __restrict__ dv, int64_t lddv, int S, int nh, int nkv, int group,
     float scale_log2, float scale, RopeRows<uint16_t> rope) {
   constexpr int NKS = DkdvTiles<HD>::NKS, NT = DkdvTiles<HD>::NT, BQ = DkdvTiles<HD>::BQ;
@@ -772,7 +801,7 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) __attribute__((amdgpu_waves_per_
   // every load in flight first).  lse and delta rows are loaded 64 at a time;
   // rows from BQ on are unused.
   __shared__ __align__(16) char st0[2 * TILE], st1[2 * TILE];
-  __shared__ __align__(16) float sl0[64], sl1[64], sd0[64], sd1[64];  // raw lse and delta
+  __shared__ __align__(16) float sl0[64], sl1[64], sd0[64], sd1[64];  // -lse*log2(e) and delta
   __shared__ __align__(16) float sp[NKS][NQT][16 * 64];  // P of each sub-tile, [j/4][lane][4]
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
@@ -803,10 +832,10 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) __attribute__((amdgpu_waves_per_
   const int64_t h0 = static_cast<int64_t>(kvh) * group;
   const uint16_t* qg = q + tok0 * ldq + h0 * HD;
   const uint16_t* gg = dO + tok0 * lddo + h0 * HD;
-  const float* lg = lse + (static_cast<int64_t>(b) * nh + h0) * S;
+  const float* lg = nl2 + (static_cast<int64_t>(b) * nh + h0) * S;
   const float* dg = delta + (static_cast<int64_t>(b) * nh + h0) * S;
   QTileDma<HD, BQ, NT> pre;
-  pre.start(qt_end);
+  pre.start(qt_end, ldq, lddo, wave, lane);
   if (n_it > 0) pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, st0, st0 + TILE, sl0, sd0, wave, lane);
   wait_loads();
   __syncthreads();
@@ -837,16 +866,17 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) __attribute__((amdgpu_waves_per_
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             const float4 L4 = *reinterpret_cast<const float4*>(&L[32 * u + 8 * g + 4 * hl]);
-            const float Lv[4] = {-L4.x * kLog2e, -L4.y * kLog2e, -L4.z * kLog2e, -L4.w * kLog2e};
+            const float Lv[4] = {L4.x, L4.y, L4.z, L4.w};  // -lse * log2(e)
 #pragma unroll
             for (int e = 0; e < 4; ++e) x[u][4 * g + e] = fast_exp2(fmaf(x[u][4 * g + e], scale_log2, Lv[e]));
           }
           if (need_mask) {  // also zeroes the rows past S (their Q/dO rows repeat row S - 1)
+            // query qa = q0 + 32u + acc_row(j, hl) is dead when qa < ki, qa >= S
+            // or ki >= S: acc_row(j, 0) outside [lo, hi) (empty when ki >= S).
+            const int lo = ki - q0 - 32 * u - 4 * hl, hi = ki < S ? S - q0 - 32 * u - 4 * hl : lo;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-              const int qa = q0 + 32 * u + acc_row(j, hl);
-              x[u][j] = ((ki > qa) | (qa >= S) | (ki >= S)) ? 0.f : x[u][j];
-            }
+            for (int j = 0; j < 16; ++j)
+              x[u][j] = ((acc_row(j, 0) < lo) | (acc_row(j, 0) >= hi)) ? 0.f : x[u][j];
           }
 #pragma unroll
           for (int g = 0; g < 4; ++g)
@@ -1050,9 +1080,10 @@ int check_dims(fh_dtype dt, const Dims& d) {
 }
 
 int check_ld(int64_t ld, int64_t heads, int64_t hd, const char* what) {
-  if (ld < heads * hd || ld % 8 != 0)
+  // < 2^24: the kernels' per-lane tile load offsets (up to 64 rows) are 32-bit
+  if (ld < heads * hd || ld % 8 != 0 || ld >= (int64_t(1) << 24))
     return fail(FH_ERR_INVALID, std::string("attention: ") + what +
-                                    " row stride must be >= heads*head_dim and a multiple of 8");
+                                    " row stride must be >= heads*head_dim, a multiple of 8 and < 2^24");
   return FH_OK;
 }
 
@@ -1070,7 +1101,7 @@ using namespace fh;
 
 extern "C" size_t fh_attn_bwd_workspace_size(int64_t batch, int64_t seq_len, int64_t n_heads) {
   if (batch <= 0 || seq_len <= 0 || n_heads <= 0) return 0;
-  return static_cast<size_t>(batch * seq_len * n_heads) * sizeof(float);
+  return 2 * static_cast<size_t>(batch * seq_len * n_heads) * sizeof(float);
 }
 
 extern "C" int fh_attn_fwd(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t ldk,
@@ -1146,7 +1177,10 @@ int attn_bwd_impl(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_
              "attn_bwd: pointers must be 16-byte aligned");
   const int S = static_cast<int>(seq_len), nh = static_cast<int>(n_heads);
   const int nkv = static_cast<int>(n_kv_heads), group = static_cast<int>(n_heads / n_kv_heads);
+  // workspace: delta = rowsum(dO*O) and nl2 = -lse*log2(e) per query, both
+  // written by the dQ kernel (its prologue), read by the dK/dV kernel.
   float* delta = static_cast<float*>(workspace);
+  float* nl2 = delta + batch * n_heads * seq_len;
   const RopeRows<uint16_t> rb{static_cast<const uint16_t*>(rp.cos), static_cast<const uint16_t*>(rp.sin),
                               rp.per_token};
   const RopeRows<float> rf{static_cast<const float*>(rp.cos), static_cast<const float*>(rp.sin), rp.per_token};
@@ -1158,7 +1192,7 @@ int attn_bwd_impl(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_
       hipLaunchKernelGGL((k_attn_bwd_dq<HD>), gq, dim3(256), 0, stream,
                          static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(k), ldk,
                          static_cast<const uint16_t*>(v), ldv, static_cast<const uint16_t*>(o), ldo,
-                         static_cast<const uint16_t*>(dout), lddo, lse, delta,
+                         static_cast<const uint16_t*>(dout), lddo, lse, delta, nl2,
                          static_cast<uint16_t*>(dq), lddq, S, nh, group, scale * kLog2e, scale, rb);
       const auto kq = static_cast<const uint16_t*>(q);
       const auto kk = static_cast<const uint16_t*>(k);
@@ -1171,14 +1205,14 @@ int attn_bwd_impl(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_
         const int64_t nkb = (seq_len + DT::NWH * 32 - 1) / (DT::NWH * 32);
         const dim3 gk(static_cast<unsigned>((nkb + 1) / 2), static_cast<unsigned>(batch * n_kv_heads));
         hipLaunchKernelGGL((k_attn_bwd_dkdv_fused<HD>), gk, dim3(DT::NT), 0, stream, kq, ldq, kk,
-                           ldk, kvp, ldv, kg, lddo, lse, delta, kdk, lddk, kdv, lddv, S, nh, nkv,
+                           ldk, kvp, ldv, kg, lddo, nl2, delta, kdk, lddk, kdv, lddv, S, nh, nkv,
                            group, scale * kLog2e, scale, rb);
       } else {
         using DT = DkdvTiles<HD>;
         const int64_t nkb = (seq_len + DT::NKS * 32 - 1) / (DT::NKS * 32);
         const dim3 gk(static_cast<unsigned>(nkb), static_cast<unsigned>(batch * n_kv_heads));
         hipLaunchKernelGGL((k_attn_bwd_dkdv<HD>), gk, dim3(DT::NT), 0, stream, kq, ldq, kk, ldk,
-                           kvp, ldv, kg, lddo, lse, delta, kdk, lddk, kdv, lddv, S, nh, nkv, group,
+                           kvp, ldv, kg, lddo, nl2, delta, kdk, lddk, kdv, lddv, S, nh, nkv, group,
                            scale * kLog2e, scale, rb);
       }
       return 0;

@@ -167,7 +167,8 @@ int fh_add(fh_dtype dt, const void* a, const void* b, void* out, int64_t n,
  * Token-major layouts: row t = b*seq_len + s; query head h occupies columns
  * h*head_dim.. of q/o/dout/dq (row strides ldq, ldo, ...), kv head j columns
  * j*head_dim.. of k/v/dk/dv; q head h reads kv head h / (n_heads/n_kv_heads).
- * head_dim in {32, 64, 128}; strides multiples of 8; 16-byte aligned bases.
+ * head_dim in {32, 64, 128}; strides multiples of 8 and < 2^24; 16-byte
+ * aligned bases.
  * FH_BF16 runs on MFMA (fp32 softmax/accumulation); FH_F32 in fp32 FMA.
  * lse: fp32 [batch, n_heads, seq_len], natural-log row log-sum-exp of the
  * scaled scores (nullable in the forward).
@@ -177,7 +178,8 @@ int fh_attn_fwd(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t 
                 int64_t batch, int64_t seq_len, int64_t n_heads, int64_t n_kv_heads,
                 int64_t head_dim, float scale, hipStream_t stream);
 
-/* Bytes of workspace fh_attn_bwd needs (the fp32 rowsum(dO*O) per query). */
+/* Bytes of workspace fh_attn_bwd needs (per query, fp32: rowsum(dO*O) and the
+ * lse in log2 units). */
 size_t fh_attn_bwd_workspace_size(int64_t batch, int64_t seq_len, int64_t n_heads);
 
 /* Gradients of fh_attn_fwd given o, lse and dout: writes dq, dk, dv (each
