@@ -257,8 +257,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   for (int jj = 0; jj < 6; ++jj) dma(OpB(), 1, 3, jj);
   wait_vm_n<14>();
   bar();
+  // In the order the loop's tail issues them, so that the loop's first MFMAs
+  // wait for their own fragments only (a different order here would make the
+  // compiler wait for all eight reads at the top of every stage).
 #pragma unroll
-  for (int r = 0; r < 8; ++r) rd1(0, 1, 0, 0, r);
+  for (int r = 0; r < 8; ++r) {
+    rd1(0, 1, 0, 0, r);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   // Stage x: 64 MFMAs (k16 steps 0..3 x 16) on fragments read one step
   // ahead.  Loads issued during stage x (slot s = 2x % 5):
@@ -284,11 +290,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    wait_lds();
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int nn = 0; nn < 8; ++nn) mf1(1, nn);
     __builtin_amdgcn_sched_barrier(0);
+    // This stage's fragment reads finish before the barrier after which its
+    // slots are refilled.
+    wait_lds();
     wait_vm_n<8>();
     bar();
 #pragma unroll
