@@ -256,14 +256,15 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True,
         ms = event_ms(torch, lambda i=0: ops.add(xs[i % 8], ys[i % 8], out=ys[(i + 1) % 8]), iters)
         add_row("residual_add", "k_add", L, 6 * T * H, ms)
     del xs, ys
-    # rope on q and k of the qkv buffer   (4T(Hq+Hkv))
+    # rope on the k heads of the qkv buffer   (4T Hkv)
     qkvs = sets(6, lambda: rnd(T, Hq + 2 * Hkv))
     cos = torch.cos(torch.arange(c["seq"] * hd, device=dev, dtype=torch.float32)).to(bf).view(1, c["seq"], hd)
     sin = torch.sin(torch.arange(c["seq"] * hd, device=dev, dtype=torch.float32)).to(bf).view(1, c["seq"], hd)
     if attn:
-        ms = event_ms(torch, lambda i=0: ops.rope_fwd_(qkvs[i % 6], nh + nkv, hd, c["seq"], cos, sin), iters)
-        add_row("rope_fwd", "k_rope<fwd>", n_fwd, 4 * T * (Hq + Hkv), ms)
-        # the RoPE backward runs inside the attention backward's dQ / dK stores
+        # k heads only: q is rotated as the attention forward loads it, and the
+        # RoPE backward runs inside the attention backward's dQ / dK stores
+        ms = event_ms(torch, lambda i=0: ops.rope_fwd_(qkvs[i % 6][:, Hq:], nkv, hd, c["seq"], cos, sin), iters)
+        add_row("rope_fwd", "k_rope<fwd> (k heads)", n_fwd, 4 * T * Hkv, ms)
     # SwiGLU: g,u -> p (6TF);  dp,g,u -> dg,du (10TF)
     gus = sets(3, lambda: rnd(T, 2 * F))
     ps = sets(3, lambda: torch.empty(T, F, device=dev, dtype=bf))
@@ -297,7 +298,10 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True,
     q, k, v = qkv[:, :Hq], qkv[:, Hq:Hq + Hkv], qkv[:, Hq + Hkv:]
     fwd_flop = 4 * B * nh * S * S * hd / 2
     o, lse = ops.attn_fwd(q, k, v, B, S, nh, nkv, hd, hd ** -0.5)
-    ms_f = event_ms(torch, lambda i=0: ops.attn_fwd(q, k, v, B, S, nh, nkv, hd, hd ** -0.5), iters)
+    # the recompute's form: q rotated on load and written out rotated for the backward
+    q_rot = torch.empty_like(q)
+    ms_f = event_ms(torch, lambda i=0: ops.attn_fwd(q, k, v, B, S, nh, nkv, hd, hd ** -0.5, rope=(cos, sin),
+                                                      q_out=q_rot), iters)
     do = rnd(T, Hq)
     dqkv = torch.empty_like(qkv)
     ms_b = event_ms(torch, lambda i=0: ops.attn_bwd(q, k, v, o, do, lse, dqkv[:, :Hq], dqkv[:, Hq:Hq + Hkv],
@@ -307,7 +311,8 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True,
     # backward: dK/dV kernel 4 products + dQ kernel 3 products (the dQ kernel
     # recomputes S and dP); algorithmic = the 5 products of attention backward
     bwd_flop = 2.5 * fwd_flop
-    mfma = [dict(kernel="attn_fwd", symbol=f"k_attn_fwd<{hd}>", launches_per_step=n_fwd,
+    mfma = [dict(kernel="attn_fwd", symbol=f"k_attn_fwd<{hd}>, q rotated on load and written out "
+                                           "(fh_attn_fwd_rope)", launches_per_step=n_fwd,
                  flop_per_launch=fwd_flop, ms_per_launch=round(ms_f, 4),
                  achieved_tflops=round(fwd_flop / ms_f / 1e9, 1),
                  frac=round(fwd_flop / ms_f / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)),
@@ -501,12 +506,12 @@ def profile_kernel(torch, name: str, c: dict, launches: int = 10) -> dict:
               "rmsnorm_bwd": lambda i: ops.rmsnorm_bwd(as_[i], xs[i], w, 1e-5, dres=as_[(i + 1) % n]),
               "residual_add": lambda i: ops.add(xs[i], as_[i])}[name]
         nbytes = {"rmsnorm_fwd": 4, "add_rmsnorm_fwd": 8, "rmsnorm_bwd": 8, "residual_add": 6}[name] * T * H
-    elif name == "rope_fwd":
+    elif name == "rope_fwd":  # the k heads (q is rotated by the attention forward)
         qkvs = [rnd(T, Hq + 2 * Hkv) for _ in range(n)]
         cos = rnd(1, c["seq"], hd)
         sin = rnd(1, c["seq"], hd)
-        fn = lambda i: ops.rope_fwd_(qkvs[i], nh + nkv, hd, c["seq"], cos, sin)
-        nbytes = 4 * T * (Hq + Hkv)
+        fn = lambda i: ops.rope_fwd_(qkvs[i][:, Hq:], nkv, hd, c["seq"], cos, sin)
+        nbytes = 4 * T * Hkv
     elif name in ("attn_fwd", "attn_bwd"):
         qkv = rnd(T, Hq + 2 * Hkv)
         q, k, v = qkv[:, :Hq], qkv[:, Hq:Hq + Hkv], qkv[:, Hq + Hkv:]
@@ -514,7 +519,11 @@ def profile_kernel(torch, name: str, c: dict, launches: int = 10) -> dict:
         do = rnd(T, Hq)
         dqkv = torch.empty_like(qkv)
         if name == "attn_fwd":
-            fn = lambda i: ops.attn_fwd(q, k, v, c["batch"], c["seq"], nh, nkv, hd, hd ** -0.5)
+            cos = rnd(1, c["seq"], hd)
+            sin = rnd(1, c["seq"], hd)
+            q_rot = torch.empty_like(q)
+            fn = lambda i: ops.attn_fwd(q, k, v, c["batch"], c["seq"], nh, nkv, hd, hd ** -0.5, rope=(cos, sin),
+                                        q_out=q_rot)
         else:
             cos = rnd(1, c["seq"], hd)
             sin = rnd(1, c["seq"], hd)

@@ -50,6 +50,8 @@ SIGNATURES: dict[str, tuple] = {
     "fh_add": (c_int, [c_int, _V, _V, _V, _I64, _V]),
     "fh_attn_fwd": (c_int, [c_int, _V, _I64, _V, _I64, _V, _I64, _V, _I64, POINTER(c_float),
                             _I64, _I64, _I64, _I64, _I64, _F, _V]),
+    "fh_attn_fwd_rope": (c_int, [c_int, _V, _I64, _V, _I64, _V, _I64, _V, _I64, POINTER(c_float), _V,
+                                 _I64, _I64, _I64, _I64, _I64, _I64, _F, _V, _V, c_int, _V]),
     "fh_attn_bwd_workspace_size": (c_size_t, [_I64, _I64, _I64]),
     "fh_attn_bwd": (c_int, [c_int, _V, _I64, _V, _I64, _V, _I64, _V, _I64, _V, _I64,
                             POINTER(c_float), _V, _I64, _V, _I64, _V, _I64, _V,

@@ -174,6 +174,36 @@ __device__ __forceinline__ void store_grad_row(uint16_t* out_row, const f32x16 (
   }
 }
 
+// The forward rotation of one query row's fragments as ld_frag loads them
+// (fragment s of the lane holds dims 16s + 8hl .. +7, so the pair partner of
+// fragment s is fragment s + HD/32, in the same lane), with the arithmetic of
+// the standalone rope kernel; out_row (nullable) receives the rotated row.
+template <int HD>
+__device__ __forceinline__ void rope_q_frags(bf16x8 (&qf)[HD / 16], const uint16_t* cs, const uint16_t* sn,
+                                             int hl, uint16_t* out_row) {
+  constexpr int H2 = HD / 32;
+#pragma unroll
+  for (int s = 0; s < H2; ++s) {
+    const int d0 = 16 * s + 8 * hl, d1 = d0 + HD / 2;
+    float x0[8], x1[8], c0[8], c1[8], s0[8], s1[8], o0[8], o1[8];
+    Elem<uint16_t>::unpack(__builtin_bit_cast(uint4, qf[s]), x0);
+    Elem<uint16_t>::unpack(__builtin_bit_cast(uint4, qf[s + H2]), x1);
+    Elem<uint16_t>::load8(cs + d0, c0);
+    Elem<uint16_t>::load8(cs + d1, c1);
+    Elem<uint16_t>::load8(sn + d0, s0);
+    Elem<uint16_t>::load8(sn + d1, s1);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) rope_pair<uint16_t, false>(x0[e], x1[e], c0[e], c1[e], s0[e], s1[e], o0[e], o1[e]);
+    const uint4 p0 = Elem<uint16_t>::pack(o0), p1 = Elem<uint16_t>::pack(o1);
+    qf[s] = as_bf16x8(p0);
+    qf[s + H2] = as_bf16x8(p1);
+    if (out_row) {
+      *reinterpret_cast<uint4*>(out_row + d0) = p0;
+      *reinterpret_cast<uint4*>(out_row + d1) = p1;
+    }
+  }
+}
+
 // ------------------------------------------------------------ forward (bf16)
 // Block = 4 waves x (32*QT) queries of one (batch, head); loop over 64-key
 // blocks, double-buffered in LDS: the next block's K/V are loaded straight
@@ -197,10 +227,12 @@ struct FwdTiles {
 // FAST: per-lane load addresses computed once (TileDma: no vector address
 // arithmetic per load, 4-8 more registers); the dQ kernel, at the edge of an
 // occupancy step, computes them per load instead (dma_tile).
-template <int BN, int HD, bool FAST, class Body>
+// pre() runs once after block 0's loads are issued, before they are waited
+// for (the kernel's own loads then overlap them).
+template <int BN, int HD, bool FAST, class Body, class Pre>
 __device__ __forceinline__ void kv_block_loop(const uint16_t* kb_ptr, int64_t ldk, const uint16_t* vb_ptr,
                                               int64_t ldv, int nkb, int S, char* sk0, char* sk1, char* sv0,
-                                              char* sv1, int wave, int lane, Body&& body) {
+                                              char* sv1, int wave, int lane, Body&& body, Pre&& pre) {
   TileDma<BN, HD, 4> dk, dv;
   if constexpr (FAST) {
     dk.init(ldk, wave, lane);
@@ -216,6 +248,7 @@ __device__ __forceinline__ void kv_block_loop(const uint16_t* kb_ptr, int64_t ld
     }
   };
   load(0, sk0, sv0);
+  pre();
   wait_loads();
   __syncthreads();
   auto step = [&](int kb, const char* K, const char* V, char* KN, char* VN) __attribute__((always_inline)) {
@@ -318,7 +351,8 @@ template <int HD>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_fwd(
     const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
     const uint16_t* __restrict__ v, int64_t ldv, uint16_t* __restrict__ o, int64_t ldo,
-    float* __restrict__ lse, int S, int nh, int group, float scale_log2) {
+    float* __restrict__ lse, int S, int nh, int group, float scale_log2, RopeRows<uint16_t> rope,
+    uint16_t* __restrict__ qout, int64_t ldqo) {
   constexpr int QT = FwdTiles<HD>::QT;
   constexpr int BM = 4 * 32 * QT, BN = 64, NS = HD / 16, ND = HD / 32, TILE = BN * 2 * HD;
   __shared__ __align__(16) char sk0[TILE], sk1[TILE], sv0[TILE], sv1[TILE];
@@ -332,15 +366,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   int a_off = lane_off_a<HD>(lane);
   int b0 = lane_off_b<HD>(lane, 0), b8 = lane_off_b<HD>(lane, 8);
 
+  // Q fragments: loaded (and rotated) while the first K/V block is in flight.
   bf16x8 qf[QT][NS];
+  auto load_q = [&]() __attribute__((always_inline)) {
 #pragma unroll
-  for (int u = 0; u < QT; ++u) {
-    const int qi = qw + 32 * u + l32;
-    const uint16_t* qrow = q + (tok0 + qi) * ldq + static_cast<int64_t>(h) * HD + 8 * hl;
+    for (int u = 0; u < QT; ++u) {
+      const int qi = qw + 32 * u + l32;
+      const uint16_t* qrow = q + (tok0 + qi) * ldq + static_cast<int64_t>(h) * HD + 8 * hl;
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
-      qf[u][s] = qi < S ? ld_frag(qrow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
-  }
+      for (int s = 0; s < NS; ++s)
+        qf[u][s] = qi < S ? ld_frag(qrow + 16 * s) : as_bf16x8(make_uint4(0, 0, 0, 0));
+      if (rope.cos && qi < S) {  // q rotated on load (RoPE forward), optionally written back
+        const int64_t r = rope.row(tok0, qi) * HD;
+        rope_q_frags<HD>(qf[u], rope.cos + r, rope.sin + r, hl,
+                         qout ? qout + (tok0 + qi) * ldqo + static_cast<int64_t>(h) * HD : nullptr);
+      }
+    }
+  };
   f32x16 oacc[QT][ND];
   float m[QT], l[QT];  // running max (log2 units) and sum of weights per query tile
 #pragma unroll
@@ -362,7 +404,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                           if (k0 <= qw + 32 * QT - 1)  // some key of the block precedes some query of the wave
                             fwd_block<HD, QT>(K, V, qf, oacc, m, l, a_off, b0, b8, k0, qw, l32, hl, S,
                                               scale_log2);
-                        });
+                        },
+                        load_q);
 #pragma unroll
   for (int u = 0; u < QT; ++u) {
     const int qi = qw + 32 * u + l32;
@@ -511,7 +554,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                           if (k0 <= qw + 31)
                             dq_block<HD>(K, V, qf, gf, dqacc, nlse2, dl, a_off, b0, b8, k0, qw, qi, hl, S,
                                          scale_log2);
-                        });
+                        },
+                        [] {});
   if (qi < S) store_grad_row<HD>(dq + (tok0 + qi) * lddq + static_cast<int64_t>(h) * HD, dqacc, scale, hl, rope, tok0, qi);
 }
 
@@ -959,7 +1003,8 @@ template <int HD>
 __global__ __launch_bounds__(128) void k_attn_fwd_f32(
     const float* __restrict__ q, int64_t ldq, const float* __restrict__ k, int64_t ldk,
     const float* __restrict__ v, int64_t ldv, float* __restrict__ o, int64_t ldo,
-    float* __restrict__ lse, int S, int nh, int group, float scale, int64_t rows) {
+    float* __restrict__ lse, int S, int nh, int group, float scale, int64_t rows, RopeRows<float> rope,
+    float* __restrict__ qout, int64_t ldqo) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= rows) return;  // rows = B*nh*S, idx = (b*nh + h)*S + s
   const int s = static_cast<int>(idx % S);
@@ -970,6 +1015,21 @@ __global__ __launch_bounds__(128) void k_attn_fwd_f32(
   const float* qr = q + (b * S + s) * ldq + static_cast<int64_t>(h) * HD;
   float qv[HD], acc[HD];
   for (int d = 0; d < HD; ++d) { qv[d] = qr[d]; acc[d] = 0.f; }
+  if (rope.cos) {  // q rotated on load (RoPE forward), optionally written back
+    const int64_t r = rope.row(b * S, s) * HD;
+    float* qo = qout ? qout + (b * S + s) * ldqo + static_cast<int64_t>(h) * HD : nullptr;
+    for (int d = 0; d < HD / 2; ++d) {
+      float o0, o1;
+      rope_pair<float, false>(qv[d], qv[d + HD / 2], rope.cos[r + d], rope.cos[r + d + HD / 2], rope.sin[r + d],
+                              rope.sin[r + d + HD / 2], o0, o1);
+      qv[d] = o0;
+      qv[d + HD / 2] = o1;
+      if (qo) {
+        qo[d] = o0;
+        qo[d + HD / 2] = o1;
+      }
+    }
+  }
   float m = -INFINITY, l = 0.f;
   for (int j = 0; j <= s; ++j) {
     const float* kr = k + (b * S + j) * ldk + static_cast<int64_t>(kvh) * HD;
@@ -1104,10 +1164,19 @@ extern "C" size_t fh_attn_bwd_workspace_size(int64_t batch, int64_t seq_len, int
   return 2 * static_cast<size_t>(batch * seq_len * n_heads) * sizeof(float);
 }
 
-extern "C" int fh_attn_fwd(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t ldk,
-                           const void* v, int64_t ldv, void* o, int64_t ldo, float* lse,
-                           int64_t batch, int64_t seq_len, int64_t n_heads, int64_t n_kv_heads,
-                           int64_t head_dim, float scale, hipStream_t stream) {
+namespace {
+
+// Rotary tables as passed to the *_rope entry points (cos == null: no rotation).
+struct RopeArgs {
+  const void* cos;
+  const void* sin;
+  int per_token;
+};
+
+int attn_fwd_impl(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
+                  int64_t ldv, void* o, int64_t ldo, float* lse, void* qout, int64_t ldqo, int64_t batch,
+                  int64_t seq_len, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, float scale,
+                  const RopeArgs& rp, hipStream_t stream) {
   const Dims d{batch, seq_len, n_heads, n_kv_heads, head_dim};
   if (int e = check_dims(dt, d)) return e;
   if (batch == 0 || seq_len == 0) return FH_OK;
@@ -1118,9 +1187,15 @@ extern "C" int fh_attn_fwd(fh_dtype dt, const void* q, int64_t ldq, const void* 
   FH_REQUIRE(q && k && v && o, "attn_fwd: null pointer");
   FH_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o),
              "attn_fwd: pointers must be 16-byte aligned");
+  if (qout) {
+    if (int e = check_ld(ldqo, n_heads, head_dim, "q_out")) return e;
+    FH_REQUIRE(aligned16(qout), "attn_fwd_rope: q_out must be 16-byte aligned");
+  }
   const int S = static_cast<int>(seq_len), nh = static_cast<int>(n_heads);
   const int group = static_cast<int>(n_heads / n_kv_heads);
   if (dt == FH_BF16) {
+    const RopeRows<uint16_t> rb{static_cast<const uint16_t*>(rp.cos), static_cast<const uint16_t*>(rp.sin),
+                                rp.per_token};
     dispatch_hd(head_dim, [&](auto hdc) {
       constexpr int BM = 4 * 32 * FwdTiles<decltype(hdc)::value>::QT;
       const dim3 grid(static_cast<unsigned>((seq_len + BM - 1) / BM),
@@ -1128,30 +1203,46 @@ extern "C" int fh_attn_fwd(fh_dtype dt, const void* q, int64_t ldq, const void* 
       hipLaunchKernelGGL((k_attn_fwd<hdc()>), grid, dim3(256), 0, stream,
                          static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(k), ldk,
                          static_cast<const uint16_t*>(v), ldv, static_cast<uint16_t*>(o), ldo, lse,
-                         S, nh, group, scale * kLog2e);
+                         S, nh, group, scale * kLog2e, rb, static_cast<uint16_t*>(qout), ldqo);
       return 0;
     });
   } else {
+    const RopeRows<float> rf{static_cast<const float*>(rp.cos), static_cast<const float*>(rp.sin), rp.per_token};
     const int64_t rows = batch * n_heads * seq_len;
     dispatch_hd(head_dim, [&](auto hdc) {
       hipLaunchKernelGGL((k_attn_fwd_f32<hdc()>), dim3(static_cast<unsigned>((rows + 127) / 128)),
                          dim3(128), 0, stream, static_cast<const float*>(q), ldq,
                          static_cast<const float*>(k), ldk, static_cast<const float*>(v), ldv,
-                         static_cast<float*>(o), ldo, lse, S, nh, group, scale, rows);
+                         static_cast<float*>(o), ldo, lse, S, nh, group, scale, rows, rf,
+                         static_cast<float*>(qout), ldqo);
       return 0;
     });
   }
-  return check_launch("fh_attn_fwd");
+  return check_launch(rp.cos ? "fh_attn_fwd_rope" : "fh_attn_fwd");
+}
+
+}  // namespace
+
+extern "C" int fh_attn_fwd(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t ldk,
+                           const void* v, int64_t ldv, void* o, int64_t ldo, float* lse,
+                           int64_t batch, int64_t seq_len, int64_t n_heads, int64_t n_kv_heads,
+                           int64_t head_dim, float scale, hipStream_t stream) {
+  return attn_fwd_impl(dt, q, ldq, k, ldk, v, ldv, o, ldo, lse, nullptr, 0, batch, seq_len, n_heads, n_kv_heads,
+                       head_dim, scale, RopeArgs{nullptr, nullptr, 0}, stream);
+}
+
+extern "C" int fh_attn_fwd_rope(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t ldk,
+                                const void* v, int64_t ldv, void* o, int64_t ldo, float* lse, void* q_out,
+                                int64_t ldqo, int64_t batch, int64_t seq_len, int64_t n_heads,
+                                int64_t n_kv_heads, int64_t head_dim, float scale, const void* cos,
+                                const void* sin, int cos_per_token, hipStream_t stream) {
+  FH_REQUIRE(cos && sin, "attn_fwd_rope: null cos/sin");
+  FH_REQUIRE(aligned16(cos) && aligned16(sin), "attn_fwd_rope: cos/sin must be 16-byte aligned");
+  return attn_fwd_impl(dt, q, ldq, k, ldk, v, ldv, o, ldo, lse, q_out, ldqo, batch, seq_len, n_heads,
+                       n_kv_heads, head_dim, scale, RopeArgs{cos, sin, cos_per_token ? 1 : 0}, stream);
 }
 
 namespace {
-
-// Rotary tables of fh_attn_bwd_rope as passed in (cos == null: no rotation).
-struct RopeArgs {
-  const void* cos;
-  const void* sin;
-  int per_token;
-};
 
 int attn_bwd_impl(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
                   int64_t ldv, const void* o, int64_t ldo, const void* dout, int64_t lddo, const float* lse,

@@ -13,8 +13,8 @@ o projection) with its activations stored for backward.
 kernels.  The module, its parameters and its state-dict keys stay as they are:
 
     qkv    = y [Wq;Wk;Wv]^T      one GEMM over the packed weights
-    q, k   = RoPE(q, k)          in the q/k/v GEMM's epilogue (or fh_rope_fwd after a library GEMM)
-    o, lse = attention(qkv)      fh_attn_fwd, causal GQA
+    q, k   = RoPE(q, k)          k: fh_rope_fwd; q: as attention loads it (or both in the GEMM)
+    o, lse = attention(qkv)      fh_attn_fwd_rope, causal GQA
     a      = o Wo^T
 
 It saves y, the rotated qkv, o and lse for backward, as the stock path saves
@@ -40,8 +40,8 @@ import torch
 
 from . import _lib, ops
 from .fused_checkpoint import _aligned, _check_params, _linear_weight
-from .fused_layer import LayerShape, _WgradStream, _cat_rows, attn_bwd, attn_fwd
-from .projections import linear, linear_dgrad, linear_rope
+from .fused_layer import LayerShape, _WgradStream, _cat_rows, attn_bwd, qkv_attention
+from .projections import linear, linear_dgrad
 
 _ACCEPTED_KWARGS = {"position_ids", "use_cache", "cache_position"}
 _counts_lock = threading.Lock()
@@ -72,9 +72,7 @@ class FusedAttentionFunction(torch.autograd.Function):
     def forward(ctx, y, cos, sin, shp, wq, wk, wv, wo):
         B, S, H = y.shape
         y2 = y.reshape(B * S, H)
-        qkv = linear_rope(y2, _cat_rows(wq, wk, wv), shp.n_heads + shp.n_kv_heads, shp.head_dim, S, cos,
-                          sin)
-        o, lse = attn_fwd(qkv, B, S, shp, need_lse=True)
+        qkv, o, lse = qkv_attention(y2, _cat_rows(wq, wk, wv), B, S, shp, cos, sin, keep=True)
         a = linear(o, wo)
         ctx.save_for_backward(y, cos, sin, qkv, o, lse, wq, wk, wv, wo)
         ctx.shp = shp

@@ -11,8 +11,9 @@ backward.
 Layer arithmetic (transformers 5.15.0, models/llama/modeling_llama.py:284-325):
     y1 = RMSNorm1(x)
     q,k,v = y1 Wq^T, y1 Wk^T, y1 Wv^T          -> one GEMM over [Wq;Wk;Wv]
-    q,k   = RoPE(q,k)                            (in the GEMM's epilogue, fh_gemm_bf16_rope,
-                                                  or fh_rope_fwd after a library GEMM)
+    q,k   = RoPE(q,k)                            (k: fh_rope_fwd over the kv heads; q: as the
+                                                  attention forward loads it, fh_attn_fwd_rope;
+                                                  or both in the GEMM's epilogue, fh_gemm_bf16_rope)
     o     = causal GQA attention(q,k,v)
     h     = x + o Wo^T;  z = RMSNorm2(h)         (fh_add_rmsnorm_fwd)
     g,u   = z Wg^T, z Wu^T                       -> one GEMM over [Wg;Wu]
@@ -71,11 +72,27 @@ def _qkv_split(buf: torch.Tensor, shp: "LayerShape"):
     return buf[:, :hq], buf[:, hq:hq + hkv], buf[:, hq + hkv:hq + 2 * hkv]
 
 
-def attn_fwd(qkv: torch.Tensor, batch: int, seq: int, shp: "LayerShape", *, need_lse: bool):
-    """Causal GQA attention over the [T, Hq+2Hkv] qkv buffer (fh_attn_fwd)."""
+def attn_fwd(qkv: torch.Tensor, batch: int, seq: int, shp: "LayerShape", *, need_lse: bool,
+             rope: tuple | None = None, write_q: bool = False):
+    """Causal GQA attention over the [T, Hq+2Hkv] qkv buffer (fh_attn_fwd).  With
+    rope=(cos, sin) q is rotated as it is loaded (fh_attn_fwd_rope) and, with
+    write_q, written back rotated into qkv for the backward."""
     q, k, v = _qkv_split(qkv, shp)
     return ops.attn_fwd(q, k, v, batch, seq, shp.n_heads, shp.n_kv_heads, shp.head_dim, shp.scale,
-                        need_lse=need_lse)
+                        need_lse=need_lse, rope=rope, q_out=q if rope is not None and write_q else None)
+
+
+def qkv_attention(y: torch.Tensor, wqkv: torch.Tensor, batch: int, seq: int, shp: "LayerShape",
+                  cos: torch.Tensor, sin: torch.Tensor, *, keep: bool):
+    """q/k/v projection, RoPE and causal attention: (qkv, o, lse).  qkv holds the
+    rotated q and k when keep (what the backward reads).  k is rotated by a pass
+    over the kv heads, q as the attention forward loads it, unless the dispatch
+    runs the rotating GEMM (fh_gemm_bf16_rope), which rotates both."""
+    qkv, rotated = linear_rope(y, wqkv, shp.n_heads + shp.n_kv_heads, shp.head_dim, seq, cos, sin,
+                               defer_heads=shp.n_heads)
+    o, lse = attn_fwd(qkv, batch, seq, shp, need_lse=keep, rope=None if rotated else (cos, sin),
+                      write_q=keep)
+    return qkv, o, lse
 
 
 def attn_bwd(do: torch.Tensor, qkv: torch.Tensor, o: torch.Tensor, lse: torch.Tensor, batch: int,
@@ -108,9 +125,7 @@ def layer_forward(x2: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, shp: L
     rstd1 = torch.empty(T, dtype=torch.float32, device=dev) if keep else None
     y1 = ops.rmsnorm_fwd(x2, w1, shp.eps1, rstd=rstd1)
 
-    wqkv = _cat_rows(wq, wk, wv)
-    qkv = linear_rope(y1, wqkv, shp.n_heads + shp.n_kv_heads, shp.head_dim, seq, cos, sin)
-    o, lse = attn_fwd(qkv, batch, seq, shp, need_lse=keep)
+    qkv, o, lse = qkv_attention(y1, _cat_rows(wq, wk, wv), batch, seq, shp, cos, sin, keep=keep)
     a = linear(o, wo)
     rstd2 = torch.empty(T, dtype=torch.float32, device=dev) if keep else None
     h, z = ops.add_rmsnorm_fwd(x2, a, w2, shp.eps2, rstd=rstd2)

@@ -217,10 +217,13 @@ def add(a: torch.Tensor, b: torch.Tensor, *, out: torch.Tensor | None = None) ->
 # ---------------------------------------------------------------- attention
 def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, batch: int, seq_len: int,
              n_heads: int, n_kv_heads: int, head_dim: int, scale: float, *,
-             need_lse: bool = True) -> tuple[torch.Tensor, torch.Tensor | None]:
+             need_lse: bool = True, rope: tuple | None = None,
+             q_out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor | None]:
     """Causal GQA attention on token-major [T, *] views (head h at columns h*head_dim).
-    Returns (o [T, n_heads*head_dim], lse fp32 [batch, n_heads, seq_len] or None)."""
-    _require_gpu(q, k, v)
+    Returns (o [T, n_heads*head_dim], lse fp32 [batch, n_heads, seq_len] or None).
+    rope=(cos, sin): q is read unrotated and rotated on load (fh_attn_fwd_rope; k
+    must already be rotated); q_out (may be q itself) then receives the rotated q."""
+    _require_gpu(q, k, v, q_out)
     _same_dtype(q, k, v)
     T = batch * seq_len
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
@@ -229,9 +232,24 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, batch: int, seq_
     o = torch.empty(T, n_heads * head_dim, dtype=q.dtype, device=q.device)
     lse = (torch.empty(batch, n_heads, seq_len, dtype=torch.float32, device=q.device)
            if need_lse else None)
-    _lib.call("fh_attn_fwd", _dtype_code(q), _ptr(q), _rowmajor(q, "q"), _ptr(k), _rowmajor(k, "k"),
-              _ptr(v), _rowmajor(v, "v"), _ptr(o), o.stride(0), _fptr(lse), batch, seq_len,
-              n_heads, n_kv_heads, head_dim, float(scale), _stream(q))
+    head = (_dtype_code(q), _ptr(q), _rowmajor(q, "q"), _ptr(k), _rowmajor(k, "k"),
+            _ptr(v), _rowmajor(v, "v"), _ptr(o), o.stride(0), _fptr(lse))
+    tail = (batch, seq_len, n_heads, n_kv_heads, head_dim, float(scale))
+    if rope is None:
+        if q_out is not None:
+            raise ValueError("attn_fwd: q_out needs rope")
+        _lib.call("fh_attn_fwd", *head, *tail, _stream(q))
+        return o, lse
+    cos, sin = rope
+    _require_gpu(cos, sin)
+    _same_dtype(q, cos, sin)
+    if q_out is not None:
+        _same_dtype(q, q_out)
+        if tuple(q_out.shape) != tuple(q.shape):
+            raise ValueError("attn_fwd: q_out must have q's shape")
+    cos2, sin2, per_token = _rope_tables("attn_fwd_rope", cos, sin, head_dim, seq_len, T)
+    _lib.call("fh_attn_fwd_rope", *head, _ptr(q_out), 0 if q_out is None else _rowmajor(q_out, "q_out"),
+              *tail, _ptr(cos2), _ptr(sin2), per_token, _stream(q))
     return o, lse
 
 

@@ -105,13 +105,19 @@ def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
 
 
 def linear_rope(x: torch.Tensor, w: torch.Tensor, n_rot_heads: int, head_dim: int, seq_len: int,
-                cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+                cos: torch.Tensor, sin: torch.Tensor, *, defer_heads: int = 0) -> tuple[torch.Tensor, bool]:
     """x [T, in] @ w[out, in]^T with heads 0..n_rot_heads-1 of the output (q and
-    k of the packed q/k/v projection) rotated by RoPE (rope_fwd_'s arithmetic)."""
+    k of the packed q/k/v projection) rotated by RoPE (rope_fwd_'s arithmetic).
+    Returns (y, all rotated).  Where the GEMM is the library's (or the hand-written
+    one without the rotation), the rotation is a separate pass that leaves heads
+    0..defer_heads-1 (q) unrotated for the caller to rotate as it reads them
+    (the attention forward's q load); all rotated is then False."""
     if head_dim in (32, 64, 128) and _use_hand("nt", x, w, "nt_rope"):
-        return ops.gemm_rope(x, w, n_rot_heads, head_dim, seq_len, cos, sin)
+        return ops.gemm_rope(x, w, n_rot_heads, head_dim, seq_len, cos, sin), True
     y = linear(x, w)
-    return ops.rope_fwd_(y, n_rot_heads, head_dim, seq_len, cos, sin)
+    if n_rot_heads > defer_heads:
+        ops.rope_fwd_(y[:, defer_heads * head_dim:], n_rot_heads - defer_heads, head_dim, seq_len, cos, sin)
+    return y, defer_heads == 0
 
 
 def linear_residual(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:

@@ -178,6 +178,21 @@ int fh_attn_fwd(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t 
                 int64_t batch, int64_t seq_len, int64_t n_heads, int64_t n_kv_heads,
                 int64_t head_dim, float scale, hipStream_t stream);
 
+/* fh_attn_fwd with the RoPE forward applied to q as it is loaded: the result
+ * equals, bit for bit, fh_rope_fwd over q's n_heads heads followed by
+ * fh_attn_fwd (apply_rotary_pos_emb then SDPA, modeling_llama.py:130-160,
+ * 256-271).  k must arrive rotated (fh_rope_fwd over the kv heads); q is read
+ * unrotated.  q_out (nullable; may be q itself with ldqo == ldq) receives the
+ * rotated q, which the backward reads.  cos/sin as in fh_rope_fwd (same dtype,
+ * [seq_len, head_dim] or, with cos_per_token != 0, [batch*seq_len, head_dim]),
+ * 16-byte aligned.
+ */
+int fh_attn_fwd_rope(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_t ldk,
+                     const void* v, int64_t ldv, void* o, int64_t ldo, float* lse, void* q_out,
+                     int64_t ldqo, int64_t batch, int64_t seq_len, int64_t n_heads,
+                     int64_t n_kv_heads, int64_t head_dim, float scale, const void* cos,
+                     const void* sin, int cos_per_token, hipStream_t stream);
+
 /* Bytes of workspace fh_attn_bwd needs (per query, fp32: rowsum(dO*O) and the
  * lse in log2 units). */
 size_t fh_attn_bwd_workspace_size(int64_t batch, int64_t seq_len, int64_t n_heads);

@@ -227,3 +227,34 @@ def test_attention_bwd_rope_rejects_bad_tables():
     with pytest.raises(ValueError, match="neither seq_len nor tokens"):
         ops.attn_bwd(g[:, :hq], g[:, hq:hq + hkv], g[:, hq + hkv:], o, g[:, :hq], lse, dg[:, :hq],
                      dg[:, hq:hq + hkv], dg[:, hq + hkv:], B, S, nh, nkv, hd, 0.1, rope=(cos, cos))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("B,S,nh,nkv,hd,per_token", [
+    (2, 200, 8, 2, 64, False),
+    (1, 77, 4, 4, 32, True),
+    (2, 131, 4, 1, 128, False),
+])
+def test_attention_fwd_rope_equals_rope_then_fwd(dtype, B, S, nh, nkv, hd, per_token):
+    """fh_attn_fwd_rope (q rotated on load, k already rotated) == fh_rope_fwd over
+    q's heads followed by fh_attn_fwd, bit for bit: output, lse and the rotated q
+    it writes out (also in place over q itself)."""
+    ops = _ops()
+    buf, _ = _inputs(B, S, nh, nkv, hd, dtype, 31)
+    rows = B * S if per_token else S
+    cos = randn((rows, hd), 32).to(dtype).to(DEV)
+    sin = randn((rows, hd), 33).to(dtype).to(DEV)
+    hq, hkv = nh * hd, nkv * hd
+    args = (B, S, nh, nkv, hd, hd ** -0.5)
+    ref = buf.to(DEV)
+    ops.rope_fwd_(ref, nh + nkv, hd, S, cos, sin)  # q and k rotated
+    o_ref, l_ref = ops.attn_fwd(ref[:, :hq], ref[:, hq:hq + hkv], ref[:, hq + hkv:], *args)
+    g = buf.to(DEV)
+    ops.rope_fwd_(g[:, hq:], nkv, hd, S, cos, sin)  # k only
+    q_rot = torch.full_like(g[:, :hq], float("nan"))
+    o, lse = ops.attn_fwd(g[:, :hq], g[:, hq:hq + hkv], g[:, hq + hkv:], *args, rope=(cos, sin), q_out=q_rot)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o_ref) and torch.equal(lse, l_ref)
+    assert torch.equal(q_rot, ref[:, :hq])
+    o2, _ = ops.attn_fwd(g[:, :hq], g[:, hq:hq + hkv], g[:, hq + hkv:], *args, rope=(cos, sin), q_out=g[:, :hq])
+    assert torch.equal(o2, o_ref) and torch.equal(g, ref)
