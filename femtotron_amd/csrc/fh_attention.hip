@@ -1190,6 +1190,7 @@ int attn_fwd_impl(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_
   if (qout) {
     if (int e = check_ld(ldqo, n_heads, head_dim, "q_out")) return e;
     FH_REQUIRE(aligned16(qout), "attn_fwd_rope: q_out must be 16-byte aligned");
+    FH_REQUIRE(qout != q || ldqo == ldq, "attn_fwd_rope: q_out aliasing q must share its row stride");
   }
   const int S = static_cast<int>(seq_len), nh = static_cast<int>(n_heads);
   const int group = static_cast<int>(n_heads / n_kv_heads);
