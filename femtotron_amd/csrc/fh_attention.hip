@@ -234,17 +234,15 @@ __device__ __forceinline__ void kv_block_loop(const uint16_t* kb_ptr, int64_t ld
                                               int64_t ldv, int nkb, int S, char* sk0, char* sk1, char* sv0,
                                               char* sv1, int wave, int lane, Body&& body, Pre&& pre) {
   TileDma<BN, HD, 4> dk, dv;
-  if constexpr (FAST) {
-    dk.init(ldk, wave, lane);
-    dv.init(ldv, wave, lane);
-  }
+  dk.init(ldk, wave, lane);
+  dv.init(ldv, wave, lane);
   auto load = [&](int r0, char* KN, char* VN) __attribute__((always_inline)) {
     if constexpr (FAST) {
       dk.load(kb_ptr, ldk, r0, S - 1, KN, wave, lane);
       dv.load(vb_ptr, ldv, r0, S - 1, VN, wave, lane);
     } else {
-      dma_tile<BN, HD, 4>(kb_ptr, ldk, r0, S - 1, KN, wave, lane);
-      dma_tile<BN, HD, 4>(vb_ptr, ldv, r0, S - 1, VN, wave, lane);
+      dk.load_asm(kb_ptr, ldk, r0, S - 1, KN, wave, lane);
+      dv.load_asm(vb_ptr, ldv, r0, S - 1, VN, wave, lane);
     }
   };
   load(0, sk0, sv0);

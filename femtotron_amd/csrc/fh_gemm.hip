@@ -115,20 +115,10 @@ __device__ __forceinline__ bf16x8 frag_ko(const char* tile, int t0, int t4, int 
   return as_bf16x8(make_uint4(ulo.x, ulo.y, uhi.x, uhi.y));
 }
 
-// One 1 KB direct-to-LDS copy: lane i loads the 16 bytes at sbase + voff into
-// LDS at lds + 16 i.  Issued as inline asm so that the compiler does not track
-// it (it would otherwise wait for every load in flight before any LDS read):
-// the kernel waits for its loads itself (s_waitcnt vmcnt) before the barrier
-// that hands a stage to the other waves.  M0 carries the LDS address; nothing
-// else in these kernels uses M0, which the compiler reserves (hence the
-// diagnostic it would print for the clobber).
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
-               : "memory", "m0");
-}
-#pragma clang diagnostic pop
+// The loads go through dma16 (fh_mfma.hpp): inline asm, so that the compiler
+// does not track them (it would otherwise wait for every load in flight before
+// any LDS read); the kernel waits for its loads itself (s_waitcnt vmcnt) before
+// the barrier that hands a stage to the other waves.
 
 // Run jj (0..7) of wave q's quarter of an operand's stage, into its 1 KB slot
 // (8q + jj) of the stage's tile at `dst`.  KC: tile rows 64q + 8jj .. +7

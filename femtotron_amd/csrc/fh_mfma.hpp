@@ -131,6 +131,18 @@ __device__ __forceinline__ void dma_tile(const uint16_t* src, int64_t ld, int r0
   }
 }
 
+// One 1 KB direct-to-LDS copy as inline asm: lane i loads the 16 bytes at
+// sbase + voff into LDS at lds + 16 i.  M0 carries the LDS address, set in the
+// same statement; nothing else in these kernels uses M0, which the compiler
+// reserves (hence the diagnostic it would print for the clobber).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 // dma_tile with the per-lane part of every load address computed once (init,
 // outside the loop): a tile at row r0 is read at src + r0*ld, wave-uniform,
 // plus this lane's fixed byte offset of each of the wave's runs, so a load
@@ -159,6 +171,26 @@ struct TileDma {
         const int j = i * NW + wave;  // wave-uniform
         if (RUNS % NW == 0 || j < RUNS)
           __builtin_amdgcn_global_load_lds((gptr)(base + off[i]), (lptr)(dst + j * 1024), 16, 0, 0);
+      }
+    } else {
+      dma_tile<ROWS, HD, NW>(src, ld, r0, last, dst, wave, lane);
+    }
+  }
+  // load() with each load issued as inline asm in its scalar-base form (the
+  // row base in SGPRs, the lane's 32-bit offset in one VGPR, M0 = the LDS run):
+  // no 64-bit per-lane pointers are kept.  The compiler does not see these
+  // loads, so the caller must wait for them itself (wait_loads) before any
+  // read of the stage, as the block loops do before their barriers.
+  __device__ __forceinline__ void load_asm(const uint16_t* src, int64_t ld, int r0, int last, char* dst, int wave,
+                                           int lane) const {
+    typedef __attribute__((address_space(3))) char* lptr;
+    if (r0 + ROWS - 1 <= last) {
+      const void* base = src + static_cast<int64_t>(r0) * ld;
+      const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lptr)dst));
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int j = i * NW + wave;  // wave-uniform
+        if (RUNS % NW == 0 || j < RUNS) dma16(off[i], base, lds0 + j * 1024);
       }
     } else {
       dma_tile<ROWS, HD, NW>(src, ld, r0, last, dst, wave, lane);
