@@ -117,16 +117,16 @@ __global__ __launch_bounds__(256) void k_rmsnorm_fwd(
 // gradient at T=16384, H=2048; with it (3 input rows) the extra registers cost
 // a wave of occupancy and it gained nothing (60.8 vs 62.3 us), so it is on only
 // for the 2-input form.
-template <typename T, int NVW, int WPR, bool RES, bool HAVE_RSTD, bool PF = !RES>
-__global__ __launch_bounds__(256) void k_rmsnorm_bwd(
+template <typename T, int NVW, int WPR, int NWB, bool RES, bool HAVE_RSTD, bool PF = !RES>
+__global__ __launch_bounds__(64 * NWB) void k_rmsnorm_bwd(
     const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ w,
     const float* __restrict__ rstd, const T* __restrict__ dres,
     T* __restrict__ dx, float* __restrict__ part, int64_t rows, int cols,
     float eps) {
   using Raw = typename Elem<T>::Raw;
-  constexpr int RPB = kWavesPerBlock / WPR;  // rows per block step
+  constexpr int RPB = NWB / WPR;  // rows per block step (NWB waves per block)
   extern __shared__ float lds_acc[];          // cols floats
-  __shared__ float red[2][2][kWavesPerBlock];  // [step parity][ss | dot][wave]
+  __shared__ float red[2][2][NWB];  // [step parity][ss | dot][wave]
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int rsub = wave / WPR, slice = wave % WPR;
@@ -345,15 +345,23 @@ void launch_fwd(const void* x, const void* a, const void* w, void* h, void* y, f
   }
 }
 
-// Backward row split: WPR waves per row and NVW chunks of 8 per lane.
-template <int NV>
+// Backward row split: WPR waves per row, NVW chunks of 8 per lane, NWB waves
+// per block (RPB = NWB / WPR rows per block step).  Rows of 1025-2048 columns
+// with the residual gradient (the layer's two norms) take two waves each in
+// blocks of 8: twice the waves in flight at the same partial-row count, 60 ->
+// 56 us at T = 16384, H = 2048 (one wave per row in blocks of 8 or 16 needs
+// more than the 128 registers of four waves per SIMD).
+template <int NV, bool RES>
 struct BwdSplit {
-  static constexpr int WPR = NV > 4 ? 2 : 1;
+  static constexpr int WPR = NV > 4 || (NV == 4 && RES) ? 2 : 1;
   static constexpr int NVW = NV / WPR;
+  static constexpr int NWB = NV == 4 && RES ? 8 : 4;
+  static constexpr int RPB = NWB / WPR;
 };
 
-int bwd_blocks(int64_t rows, int wpr) {
-  const int64_t rpb = kWavesPerBlock / wpr;
+// Blocks of the backward: one per RPB rows, at most kMaxBwdBlocks (each
+// writes one fp32 partial row of dw).
+int bwd_blocks(int64_t rows, int rpb) {
   const int64_t need = (rows + rpb - 1) / rpb;
   return static_cast<int>(need < kMaxBwdBlocks ? need : kMaxBwdBlocks);
 }
@@ -362,8 +370,8 @@ template <typename T, int NV, bool RES, bool HR>
 void launch_bwd_k(const void* dy, const void* x, const void* w, const float* rstd,
                   const void* dres, void* dx, float* part, int64_t rows, int cols, float eps,
                   int blocks, hipStream_t s) {
-  using SP = BwdSplit<NV>;
-  hipLaunchKernelGGL((k_rmsnorm_bwd<T, SP::NVW, SP::WPR, RES, HR>), dim3(blocks), dim3(256),
+  using SP = BwdSplit<NV, RES>;
+  hipLaunchKernelGGL((k_rmsnorm_bwd<T, SP::NVW, SP::WPR, SP::NWB, RES, HR>), dim3(blocks), dim3(64 * SP::NWB),
                      static_cast<size_t>(cols) * sizeof(float), s, static_cast<const T*>(dy),
                      static_cast<const T*>(x), static_cast<const T*>(w), rstd,
                      static_cast<const T*>(dres), static_cast<T*>(dx), part, rows, cols, eps);
@@ -373,8 +381,8 @@ template <typename T, int NV>
 void launch_bwd(const void* dy, const void* x, const void* w, const float* rstd,
                 const void* dres, void* dx, void* dw, float* part, int64_t rows, int cols,
                 float eps, hipStream_t s) {
-  const int blocks = bwd_blocks(rows, BwdSplit<NV>::WPR);
   const bool res = dres != nullptr, hr = rstd != nullptr;
+  const int blocks = bwd_blocks(rows, res ? BwdSplit<NV, true>::RPB : BwdSplit<NV, false>::RPB);
   if (res && hr) launch_bwd_k<T, NV, true, true>(dy, x, w, rstd, dres, dx, part, rows, cols, eps, blocks, s);
   else if (res) launch_bwd_k<T, NV, true, false>(dy, x, w, rstd, dres, dx, part, rows, cols, eps, blocks, s);
   else if (hr) launch_bwd_k<T, NV, false, true>(dy, x, w, rstd, dres, dx, part, rows, cols, eps, blocks, s);
@@ -444,9 +452,9 @@ extern "C" int fh_add_rmsnorm_fwd(fh_dtype dt, const void* x, const void* a, con
 
 extern "C" size_t fh_rmsnorm_bwd_workspace_size(int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0) return 0;
-  // one fp32 partial row per backward block (rows wider than 2048 take 2 waves
-  // each), then the reduction's stage rows
-  const int64_t nrows = bwd_blocks(rows, cols > 2048 ? 2 : 1) + kReduceGroups;
+  // one fp32 partial row per backward block (4 rows per block, 2 above 2048
+  // columns), then the reduction's stage rows
+  const int64_t nrows = bwd_blocks(rows, cols > 2048 ? 2 : 4) + kReduceGroups;
   return static_cast<size_t>(nrows) * static_cast<size_t>(cols) * sizeof(float);
 }
 
