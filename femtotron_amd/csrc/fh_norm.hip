@@ -18,64 +18,59 @@ namespace {
 
 constexpr int kWavesPerBlock = 4;  // 256 threads
 
-// Forward: one wave per R consecutive rows (all loads of the R rows issued
-// before the first reduction).
-#ifndef FH_NORM_FWD_ROWS
-#define FH_NORM_FWD_ROWS 1
-#endif
-template <int NV>
-struct FwdRows {
-  static constexpr int R = NV <= 4 ? FH_NORM_FWD_ROWS : 1;
-};
-
-template <typename T, int NV, bool ADD, int R>
+// Forward: each wave takes rows row, row + stride, ... (stride = 4 x grid).
+// With PIPE the next row's loads are issued before this row is reduced and
+// stored, so a wave keeps two rows in flight; without it the grid covers every
+// row once (one row per wave).  The pipelined form is used for add+RMSNorm
+// (two input rows): 45.2 -> 43.1 us at T = 16384, H = 2048 and 50.5 -> 48.8 us
+// at T = 8192, H = 4096; the one-input form measured no gain from it.
+template <typename T, int NV, bool ADD, bool PIPE>
 __global__ __launch_bounds__(256) void k_rmsnorm_fwd(
     const T* __restrict__ x, const T* __restrict__ a, const T* __restrict__ w,
     T* __restrict__ h, T* __restrict__ y, float* __restrict__ rstd,
     int64_t rows, int cols, float eps) {
   using Raw = typename Elem<T>::Raw;
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6)) * R;
-  if (row0 >= rows) return;  // uniform per wave
+  int64_t row = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  if (row >= rows) return;  // uniform per wave
 
-  Raw xr[R][NV], wr[NV];
-  [[maybe_unused]] Raw ar[R][NV];
-#pragma unroll
-  for (int k = 0; k < R; ++k) {
-    const int64_t base = (row0 + k) * cols;
-    const bool ok = row0 + k < rows;
+  Raw xn[NV], wr[NV];
+  [[maybe_unused]] Raw an[NV];
+  auto load_row = [&](int64_t rr) {
+    const int64_t base = rr * cols;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int c = (i * kWave + lane) * 8;
-      if (ok && c < cols) {
-        xr[k][i] = Elem<T>::ldraw(x + base + c);
-        if constexpr (ADD) ar[k][i] = Elem<T>::ldraw(a + base + c);
+      if (c < cols) {
+        xn[i] = Elem<T>::ldraw(x + base + c);
+        if constexpr (ADD) an[i] = Elem<T>::ldraw(a + base + c);
       }
     }
-  }
+  };
+  load_row(row);
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = (i * kWave + lane) * 8;
     if (c < cols) wr[i] = Elem<T>::ldraw(w + c);
   }
-#pragma unroll
-  for (int k = 0; k < R; ++k) {
-    if (row0 + k >= rows) break;  // uniform per wave
-    const int64_t base = (row0 + k) * cols;
+  // Normalises row rr from its loaded chunks (xr, and ar with ADD).
+  auto norm_row = [&](int64_t rr, Raw* xr, [[maybe_unused]] Raw* ar) {
+    const int64_t base = rr * cols;
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int c = (i * kWave + lane) * 8;
       if (c < cols) {
         float v[8];
-        Elem<T>::unpack(xr[k][i], v);
+        Elem<T>::unpack(xr[i], v);
         if constexpr (ADD) {  // h = to_dtype(x + a), kept packed for the normalisation
           float b[8];
-          Elem<T>::unpack(ar[k][i], b);
+          Elem<T>::unpack(ar[i], b);
 #pragma unroll
           for (int j = 0; j < 8; ++j) v[j] = Elem<T>::rnd(v[j] + b[j]);
-          xr[k][i] = Elem<T>::pack(v);
-          Elem<T>::straw(h + base + c, xr[k][i]);
+          xr[i] = Elem<T>::pack(v);
+          Elem<T>::straw(h + base + c, xr[i]);
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) ss = fmaf(v[j], v[j], ss);
@@ -88,14 +83,29 @@ __global__ __launch_bounds__(256) void k_rmsnorm_fwd(
       const int c = (i * kWave + lane) * 8;
       if (c < cols) {
         float v[8], wv[8], o[8];
-        Elem<T>::unpack(xr[k][i], v);
+        Elem<T>::unpack(xr[i], v);
         Elem<T>::unpack(wr[i], wv);
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] = Elem<T>::rnd(wv[j] * Elem<T>::rnd(v[j] * r));
         Elem<T>::store8(y + base + c, o);
       }
     }
-    if (rstd != nullptr && lane == 0) rstd[row0 + k] = r;
+    if (rstd != nullptr && lane == 0) rstd[rr] = r;
+  };
+  if constexpr (!PIPE) {
+    norm_row(row, xn, an);
+  } else {
+    for (; row < rows; row += stride) {  // uniform per wave
+      Raw xr[NV];
+      [[maybe_unused]] Raw ar[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        xr[i] = xn[i];
+        if constexpr (ADD) ar[i] = an[i];
+      }
+      if (row + stride < rows) load_row(row + stride);
+      norm_row(row, xr, ar);
+    }
   }
 }
 
@@ -112,7 +122,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_fwd(
 //   dw += dy * to_dtype(x * r)      (per-wave registers)
 // The weight-gradient partials of the block's waves are summed in a fixed
 // order through LDS into one fp32 row per block (deterministic), which
-// k_reduce_parts / k_reduce_stage fold into dw.
+// k_reduce_parts folds into dw.
 // Next-row prefetch (PF): measured 50.6 -> 43.5 us without the residual
 // gradient at T=16384, H=2048; with it (3 input rows) the extra registers cost
 // a wave of occupancy and it gained nothing (60.8 vs 62.3 us), so it is on only
@@ -270,54 +280,56 @@ __global__ __launch_bounds__(64 * NWB) void k_rmsnorm_bwd(
   for (int c = threadIdx.x; c < cols; c += blockDim.x) dst[c] = lds_acc[c];
 }
 
-// dw[c] = sum_p part[p, c], deterministic, in two stages.  Stage 1: block
-// (cx, g) sums partial rows p = g, g + G, g + 2G, ... (each of its 4 waves
-// takes every 4th of them, all loads in flight at once) for 64 columns and
-// combines its waves in a fixed order into stage[g][c].  Stage 2 sums the G
-// stage rows of a column in order.  The partial rows are few (<= 512) and
-// wide, so one stage would leave the reduction latency-bound on a handful of
-// CUs.
-constexpr int kReduceGroups = 16;
-
+// dw[c] = sum_p part[p, c], deterministic, in one launch.  A block owns 16
+// columns: its 256 threads are 64 row groups x 4 column quads; thread (g, q)
+// sums the float4 of rows p = g, g + 64, g + 128, ... in order (eight loads in
+// flight), and the 64 group sums of a column are added in group order.  One
+// launch instead of a partial pass plus a stage pass measured 1-2 us faster
+// per backward call (one launch gap fewer).
+template <typename T>
 __global__ __launch_bounds__(256) void k_reduce_parts(const float* __restrict__ part, int nparts,
-                                                      int cols, float* __restrict__ stage) {
-  __shared__ float red[4][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int c = blockIdx.x * 64 + lane, g = blockIdx.y;
-  float s = 0.f;
+                                                      int cols, T* __restrict__ out) {
+  constexpr int G = 64, U = 8;
+  __shared__ float red[G][17];
+  const int q = threadIdx.x & 3, g = threadIdx.x >> 2;
+  const int c = blockIdx.x * 16 + q * 4;  // cols % 8 == 0: a quad is wholly in or out
+  float4 s = {0.f, 0.f, 0.f, 0.f};
   if (c < cols) {
-    constexpr int U = 8;  // loads in flight per lane
-    int p = g + kReduceGroups * wave;
-    for (; p + kReduceGroups * 4 * (U - 1) < nparts; p += kReduceGroups * 4 * U) {
-      float v[U];
+    auto at = [&](int p) {
+      return *reinterpret_cast<const float4*>(part + static_cast<int64_t>(p) * cols + c);
+    };
+    int p = g;
+    for (; p + G * (U - 1) < nparts; p += G * U) {
+      float4 v[U];
 #pragma unroll
-      for (int k = 0; k < U; ++k) v[k] = part[static_cast<int64_t>(p + kReduceGroups * 4 * k) * cols + c];
+      for (int k = 0; k < U; ++k) v[k] = at(p + G * k);
 #pragma unroll
-      for (int k = 0; k < U; ++k) s += v[k];
+      for (int k = 0; k < U; ++k) {
+        s.x += v[k].x; s.y += v[k].y; s.z += v[k].z; s.w += v[k].w;
+      }
     }
-    for (; p < nparts; p += kReduceGroups * 4) s += part[static_cast<int64_t>(p) * cols + c];
+    for (; p < nparts; p += G) {
+      const float4 v = at(p);
+      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+    }
   }
-  red[wave][lane] = s;
+  red[g][q * 4 + 0] = s.x;
+  red[g][q * 4 + 1] = s.y;
+  red[g][q * 4 + 2] = s.z;
+  red[g][q * 4 + 3] = s.w;
   __syncthreads();
-  if (wave == 0 && c < cols)
-    stage[static_cast<int64_t>(g) * cols + c] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+  const int cc = blockIdx.x * 16 + static_cast<int>(threadIdx.x);
+  if (threadIdx.x < 16 && cc < cols) {
+    float t = 0.f;
+    for (int k = 0; k < G; ++k) t += red[k][threadIdx.x];
+    Elem<T>::st1(out + cc, t);
+  }
 }
 
 template <typename T>
 __global__ __launch_bounds__(256) void k_fill_zero(T* __restrict__ out, int n) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i < n) Elem<T>::st1(out + i, 0.f);
-}
-
-template <typename T>
-__global__ __launch_bounds__(256) void k_reduce_stage(const float* __restrict__ stage, int cols,
-                                                      T* __restrict__ out) {
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= cols) return;
-  float t = 0.f;
-#pragma unroll
-  for (int g = 0; g < kReduceGroups; ++g) t += stage[static_cast<int64_t>(g) * cols + c];
-  Elem<T>::st1(out + c, t);
 }
 
 // Backward grid cap: fewer blocks mean fewer fp32 dw partial rows to reduce;
@@ -327,19 +339,25 @@ __global__ __launch_bounds__(256) void k_reduce_stage(const float* __restrict__ 
 #endif
 constexpr int kMaxBwdBlocks = FH_NORM_BWD_BLOCKS;
 
+// Grid cap of the pipelined add+RMSNorm forward (768 measured best of 512,
+// 768, 1024 and 2048 at T = 16384, H = 2048).
+constexpr int64_t kFwdPipeBlocks = 768;
+
 template <typename T, int NV>
 void launch_fwd(const void* x, const void* a, const void* w, void* h, void* y, float* rstd,
                 int64_t rows, int cols, float eps, hipStream_t s) {
-  constexpr int R = FwdRows<NV>::R;
-  const int64_t per_block = static_cast<int64_t>(kWavesPerBlock) * R;
-  const dim3 grid(static_cast<unsigned>((rows + per_block - 1) / per_block));
+  const int64_t need = (rows + kWavesPerBlock - 1) / kWavesPerBlock;
   if (a != nullptr) {
-    hipLaunchKernelGGL((k_rmsnorm_fwd<T, NV, true, R>), grid, dim3(256), 0, s,
+    // add+RMSNorm: pipelined over a capped grid where the two rows of x and a
+    // in flight fit the registers (bf16 up to 4096 columns, fp32 up to 2048)
+    constexpr bool kPipe = NV * sizeof(typename Elem<T>::Raw) <= 128;
+    const dim3 grid(static_cast<unsigned>(kPipe && need > kFwdPipeBlocks ? kFwdPipeBlocks : need));
+    hipLaunchKernelGGL((k_rmsnorm_fwd<T, NV, true, kPipe>), grid, dim3(256), 0, s,
                        static_cast<const T*>(x), static_cast<const T*>(a),
                        static_cast<const T*>(w), static_cast<T*>(h), static_cast<T*>(y), rstd,
                        rows, cols, eps);
   } else {
-    hipLaunchKernelGGL((k_rmsnorm_fwd<T, NV, false, R>), grid, dim3(256), 0, s,
+    hipLaunchKernelGGL((k_rmsnorm_fwd<T, NV, false, false>), dim3(static_cast<unsigned>(need)), dim3(256), 0, s,
                        static_cast<const T*>(x), nullptr, static_cast<const T*>(w), nullptr,
                        static_cast<T*>(y), rstd, rows, cols, eps);
   }
@@ -387,10 +405,7 @@ void launch_bwd(const void* dy, const void* x, const void* w, const float* rstd,
   else if (res) launch_bwd_k<T, NV, true, false>(dy, x, w, rstd, dres, dx, part, rows, cols, eps, blocks, s);
   else if (hr) launch_bwd_k<T, NV, false, true>(dy, x, w, rstd, dres, dx, part, rows, cols, eps, blocks, s);
   else launch_bwd_k<T, NV, false, false>(dy, x, w, rstd, dres, dx, part, rows, cols, eps, blocks, s);
-  float* stage = part + static_cast<int64_t>(blocks) * cols;
-  hipLaunchKernelGGL(k_reduce_parts, dim3((cols + 63) / 64, kReduceGroups), dim3(256), 0, s, part,
-                     blocks, cols, stage);
-  hipLaunchKernelGGL((k_reduce_stage<T>), dim3((cols + 255) / 256), dim3(256), 0, s, stage, cols,
+  hipLaunchKernelGGL((k_reduce_parts<T>), dim3((cols + 15) / 16), dim3(256), 0, s, part, blocks, cols,
                      static_cast<T*>(dw));
 }
 
@@ -453,8 +468,8 @@ extern "C" int fh_add_rmsnorm_fwd(fh_dtype dt, const void* x, const void* a, con
 extern "C" size_t fh_rmsnorm_bwd_workspace_size(int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0) return 0;
   // one fp32 partial row per backward block (4 rows per block, 2 above 2048
-  // columns), then the reduction's stage rows
-  const int64_t nrows = bwd_blocks(rows, cols > 2048 ? 2 : 4) + kReduceGroups;
+  // columns)
+  const int64_t nrows = bwd_blocks(rows, cols > 2048 ? 2 : 4);
   return static_cast<size_t>(nrows) * static_cast<size_t>(cols) * sizeof(float);
 }
 
@@ -462,9 +477,9 @@ namespace fh {
 namespace {
 
 // Scratch of the allocation-free backward: the fp32 partial rows of the
-// largest valid call (kMaxBwdBlocks partial rows + kReduceGroups stage rows of
-// at most 8192 columns), 17.3 MB per device, held until the process ends.
-constexpr size_t kNoAllocScratchFloats = static_cast<size_t>(kMaxBwdBlocks + kReduceGroups) * 8192;
+// largest valid call (kMaxBwdBlocks partial rows of at most 8192 columns),
+// 16.8 MB per device, held until the process ends.
+constexpr size_t kNoAllocScratchFloats = static_cast<size_t>(kMaxBwdBlocks) * 8192;
 __device__ __align__(256) float scratch[kNoAllocScratchFloats];
 
 // Device address of `scratch` on the current device, looked up once per

@@ -97,7 +97,7 @@ int fh_rmsnorm_bwd(fh_dtype dt, const void* dy, const void* x, const void* w,
  * tight serving loops, harnesses that forbid hipMalloc.  Same arguments,
  * results (bit for bit) and errors as fh_rmsnorm_bwd; the fp32 partial rows go
  * to a scratch array the library holds in device memory, one per device
- * (fh_rmsnorm_bwd_noalloc_max_workspace() bytes, 17.3 MB, enough for every
+ * (fh_rmsnorm_bwd_noalloc_max_workspace() bytes, 16.8 MB, enough for every
  * valid rows x cols since cols <= 8192), kept until the process ends.  Calls
  * no allocating routine.  All calls on one device share that scratch: calls
  * that may overlap on one device (different streams, or different host
