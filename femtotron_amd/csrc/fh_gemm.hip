@@ -36,9 +36,16 @@
 // Few output tiles (a weight gradient of 2048 x 2048 has 64) would leave most
 // of the 256 CUs idle, so the K range can be split into S slices whose fp32
 // partial tiles are summed in slice order by k_gemm_reduce (deterministic).
+// Where the tiles leave a last round of CUs partly idle (the gate/up weight
+// gradient's 352 tiles: 1.375 rounds), the stream form instead gives every CU
+// one workgroup and the same number of k-steps: whole tiles first, then an
+// even share of the remaining tiles' k-steps, whose split tiles k_gemm_fixup
+// sums from fp32 segments in k order (deterministic, no inter-workgroup
+// waits).
 #include "fh_common.hpp"
 #include "fh_mfma.hpp"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace fh {
@@ -47,7 +54,7 @@ namespace {
 constexpr int kTm = 256, kTn = 256, kTk = 64;  // block tile and stage depth
 constexpr int kSubBytes = kTk * 128;           // KO sub-tile: [64 k x 64] bf16
 
-enum Epi { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_PARTIAL = 2, EPI_ROPE = 3 };
+enum Epi { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_PARTIAL = 2, EPI_ROPE = 3, EPI_STREAM = 4 };
 
 // The rotary embedding of EPI_ROPE: columns [0, rot_cols) of C are heads of
 // hd columns (hd a power of two dividing the 256-column tile, so no head
@@ -71,7 +78,12 @@ struct GemmArgs {
   int m, n;
   int tiles_m, tiles_n, tiles;
   int steps_per_slice, total_steps;
-  int grid;  // logical blocks (tiles * slices)
+  int grid;  // logical blocks (tiles * slices; EPI_STREAM: the workgroups)
+  // EPI_STREAM: full_rounds whole tiles per workgroup (tile r * grid + w),
+  // then the remaining tail_tiles' tail_iters = tail_tiles * total_steps
+  // k-steps split evenly over the workgroups
+  int full_rounds, tail_tiles;
+  int64_t tail_iters;
   GemmRope rope;
 };
 
@@ -170,24 +182,30 @@ __device__ __forceinline__ void wait_vm_n() {
 
 __device__ __forceinline__ int mod5(int v) { return v >= 5 ? v - 5 : v; }
 
-template <bool A_KO, bool B_KO, int EPI>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_gemm(GemmArgs g) {
-  __shared__ __align__(16) char ring[kRing * kSlot];
-  const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nb8 = gridDim.x >> 3;
-  const int lid = (blockIdx.x & 7) * nb8 + (blockIdx.x >> 3);
-  if (lid >= g.grid) return;
-  const int slice = lid / g.tiles, t = lid - slice * g.tiles;
+// Origin of tile t: tiles run in groups of GM = 4 m-tiles, n-major inside a
+// group, so consecutive tiles (and the workgroups of one XCD) share B columns
+// and A rows in L2.
+__device__ __forceinline__ void tile_origin(const GemmArgs& g, int t, int& m0, int& n0) {
   constexpr int GM = 4;
   const int width = GM * g.tiles_n;
   const int gi = t / width, first_m = gi * GM;
   const int gm = min(g.tiles_m - first_m, GM);
   const int tw = t - gi * width;
-  const int tm = first_m + tw % gm, tn = tw / gm;
-  const int m0 = tm * kTm, n0 = tn * kTn;
-  const int s_begin = slice * g.steps_per_slice;
-  const int nst = min(g.total_steps - s_begin, g.steps_per_slice);
+  m0 = (first_m + tw % gm) * kTm;
+  n0 = (tw / gm) * kTn;
+}
+
+// One tile t over k-steps s_begin .. s_begin + nst - 1.  The result goes to C
+// (bf16, with the EPI epilogue) or, for EPI_PARTIAL and for EPI_STREAM with
+// to_part, as fp32 to pdst (the tile's origin, row stride pld).  EPI_STREAM
+// ends with a barrier, as the workgroup's next tile reuses the LDS ring.
+template <bool A_KO, bool B_KO, int EPI>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* ring, int t, int s_begin, int nst,
+                                          float* pdst, int64_t pld, bool to_part) {
+  const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int m0, n0;
+  tile_origin(g, t, m0, n0);
 
   // Run jj of wave `wave`'s quarter of operand OP (0: A, 1: B) of stage
   // `step` into ring slot `slot`.  Stages past the slice's end re-load its
@@ -303,11 +321,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   wait_lds();
   bar();
 
-  if constexpr (EPI == EPI_PARTIAL) {
+  if (EPI == EPI_PARTIAL || (EPI == EPI_STREAM && to_part)) {
     // The fp32 tile goes through LDS in two halves of 128 rows ([128 rows x
     // 256 columns], 16-byte chunk c of row r stored at chunk c ^ (r % 16));
     // lane i of a wave then stores chunk i of a 1 KB row.
-    float* part = g.part + static_cast<int64_t>(slice) * g.m * g.n;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       if (wm == half) {
@@ -333,7 +350,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         const int r = 32 * wave + q2;
         const float4 v = *reinterpret_cast<const float4*>(ring + r * 1024 + ((lane ^ (r & 15)) << 4));
         const int mrow = m0 + 128 * half + r;
-        if (mrow < g.m && col < g.n) *reinterpret_cast<float4*>(part + static_cast<int64_t>(mrow) * g.n + col) = v;
+        if (mrow < g.m && col < g.n)
+          *reinterpret_cast<float4*>(pdst + static_cast<int64_t>(128 * half + r) * pld + 4 * lane) = v;
       }
       wait_lds();
       bar();
@@ -401,7 +419,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       const uint4 v = *reinterpret_cast<const uint4*>(ring + r * 512 + ((chunk ^ (r & 15)) << 4));
       const int mrow = m0 + r;
       if (mrow >= g.m || col >= g.n) continue;
-      if constexpr (EPI == EPI_RESIDUAL) {
+      if (EPI == EPI_RESIDUAL || (EPI == EPI_STREAM && g.r != nullptr)) {
         const uint4 rv = *reinterpret_cast<const uint4*>(g.r + mrow * g.ldr + col);
         auto add2 = [](uint32_t res, uint32_t c) {
           return pk_bf16(__uint_as_float(res << 16) + __uint_as_float(c << 16),
@@ -413,6 +431,115 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         *reinterpret_cast<uint4*>(g.c + mrow * g.ldc + col) = v;
       }
     }
+    if constexpr (EPI == EPI_STREAM) {
+      wait_lds();
+      bar();
+    }
+  }
+}
+
+// Split K (EPI_PARTIAL), one tile per workgroup, or stream (EPI_STREAM): the
+// workgroup runs its whole tiles, then its share of the tail's k-steps as
+// segments of one tile each.  A tail segment that is not a whole tile goes to
+// fp32 slot 2w (the workgroup's first tail segment) or 2w + 1 (its last);
+// k_gemm_fixup adds a split tile's segments in k order.
+template <bool A_KO, bool B_KO, int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_gemm(GemmArgs g) {
+  __shared__ __align__(16) char ring[kRing * kSlot];
+  const int nb8 = gridDim.x >> 3;
+  const int lid = (blockIdx.x & 7) * nb8 + (blockIdx.x >> 3);
+  if (lid >= g.grid) return;
+  if constexpr (EPI == EPI_STREAM) {
+    // One call site for both kinds of segment (one copy of the main loop).
+    const int64_t ki = g.total_steps;
+    const int64_t beg = lid * g.tail_iters / g.grid, end = (lid + 1) * g.tail_iters / g.grid;
+    int r = 0;
+    for (int64_t it = beg;;) {
+      int t, k0 = 0, len = g.total_steps;
+      float* slot = nullptr;
+      if (r < g.full_rounds) {
+        t = r++ * g.grid + lid;
+      } else if (it < end) {
+        const int tt = static_cast<int>(it / ki);
+        k0 = static_cast<int>(it - tt * ki);
+        len = static_cast<int>(min(ki - k0, end - it));
+        t = g.full_rounds * g.grid + tt;
+        slot = g.part + (2 * static_cast<int64_t>(lid) + (it == beg ? 0 : 1)) * (kTm * kTn);
+        it += len;
+      } else {
+        break;
+      }
+      gemm_tile<A_KO, B_KO, EPI>(g, ring, t, k0, len, slot, kTn, len < ki);
+    }
+  } else {
+    const int slice = lid / g.tiles, t = lid - slice * g.tiles;
+    const int s_begin = slice * g.steps_per_slice;
+    int m0, n0;
+    tile_origin(g, t, m0, n0);
+    float* pdst = EPI == EPI_PARTIAL
+                      ? g.part + static_cast<int64_t>(slice) * g.m * g.n + static_cast<int64_t>(m0) * g.n + n0
+                      : nullptr;
+    gemm_tile<A_KO, B_KO, EPI>(g, ring, t, s_begin, min(g.total_steps - s_begin, g.steps_per_slice), pdst,
+                               g.n, EPI == EPI_PARTIAL);
+  }
+}
+
+// Rows blockIdx.y * 16 .. +15 of tail tile blockIdx.x of a stream GEMM: if
+// more than one workgroup's k-range meets the tile, C = bf16(sum of their fp32
+// segments in workgroup = k order) (+ residual, rounded as k_gemm_reduce).
+// Workgroup w covers tail k-steps [w I / G, (w + 1) I / G); the one holding
+// step i is ceil((i + 1) G / I) - 1.  Thread (row group, lane) adds 4 columns
+// of 4 rows, one contributor at a time (its 4 loads in flight together).
+constexpr int kFixRows = 16;
+
+__global__ __launch_bounds__(256) void k_gemm_fixup(GemmArgs g) {
+  const int64_t ki = g.total_steps, I = g.tail_iters, G = g.grid;
+  const int64_t lo = static_cast<int64_t>(blockIdx.x) * ki;
+  auto wg_of = [&](int64_t i) { return static_cast<int>(((i + 1) * G + I - 1) / I - 1); };
+  auto start_of = [&](int64_t w) { return w * I / G; };
+  const int w0 = wg_of(lo), w1 = wg_of(lo + ki - 1);
+  if (w0 == w1) return;  // one workgroup stored the whole tile
+  int m0, n0;
+  tile_origin(g, g.full_rounds * g.grid + static_cast<int>(blockIdx.x), m0, n0);
+  const int lane = threadIdx.x & 63, r0 = blockIdx.y * kFixRows + (threadIdx.x >> 6);
+  const int col = n0 + 4 * lane;
+  if (col >= g.n) return;
+  float4 acc[kFixRows / 4];
+  bool first = true;
+  for (int w = w0; w <= w1; ++w) {
+    const int64_t sw = start_of(w);
+    if (sw == start_of(w + 1)) continue;  // empty range: wrote nothing
+    const float* src = g.part + (2 * static_cast<int64_t>(w) + (sw >= lo ? 0 : 1)) * (kTm * kTn) + 4 * lane;
+    float4 v[kFixRows / 4];
+#pragma unroll
+    for (int q = 0; q < kFixRows / 4; ++q) v[q] = *reinterpret_cast<const float4*>(src + (r0 + 4 * q) * kTn);
+#pragma unroll
+    for (int q = 0; q < kFixRows / 4; ++q) {
+      if (first) {
+        acc[q] = v[q];
+      } else {
+        acc[q].x += v[q].x;
+        acc[q].y += v[q].y;
+        acc[q].z += v[q].z;
+        acc[q].w += v[q].w;
+      }
+    }
+    first = false;
+  }
+#pragma unroll
+  for (int q = 0; q < kFixRows / 4; ++q) {
+    const int mrow = m0 + r0 + 4 * q;
+    if (mrow >= g.m) break;
+    float4 s = acc[q];
+    if (g.r != nullptr) {
+      const uint2 rv = *reinterpret_cast<const uint2*>(g.r + static_cast<int64_t>(mrow) * g.ldr + col);
+      s.x = __uint_as_float(rv.x << 16) + round_bf(s.x);
+      s.y = __uint_as_float(rv.x & 0xffff0000u) + round_bf(s.y);
+      s.z = __uint_as_float(rv.y << 16) + round_bf(s.z);
+      s.w = __uint_as_float(rv.y & 0xffff0000u) + round_bf(s.w);
+    }
+    *reinterpret_cast<uint2*>(g.c + static_cast<int64_t>(mrow) * g.ldc + col) =
+        make_uint2(pk_bf16(s.x, s.y), pk_bf16(s.z, s.w));
   }
 }
 
@@ -458,12 +585,29 @@ int device_cus() {
   return cached[dev];
 }
 
-// K slices S: the modelled time of S slices is ceil(tiles*S / CUs) / S rounds
-// of a whole-K tile plus, for S > 1, writing and re-reading the S fp32
-// partial outputs (8 bytes per output and slice at ~5 TB/s, against a
-// whole-K tile's MFMA time at ~6 TFLOP/s per CU).  Every slice keeps at least
-// 256 k.
-int gemm_slices(int64_t m, int64_t n, int64_t k) {
+// Workgroups of a stream GEMM: one per CU, a multiple of 8 (the XCD order).
+int stream_grid() { return std::max(8, device_cus() / 8 * 8); }
+
+// How a GEMM is split.  Modelled times, in rounds of a whole-K tile:
+//   K slices S: ceil(tiles*S / CUs) / S, plus for S > 1 writing and re-reading
+//     the S fp32 partial outputs (8 bytes per output and slice at ~5 TB/s,
+//     against a whole-K tile's MFMA time at ~6 TFLOP/s per CU); every slice
+//     keeps at least 256 k.
+//   stream: floor(tiles / CUs) whole rounds, then the remaining tiles' k-steps
+//     split evenly over the CUs (tail_tiles / CUs), plus the fp32 traffic of
+//     the split tiles' segments (at most CUs + tail_tiles of them, 256 x 256
+//     each).  Plain stores and the residual epilogue (not the rotation).
+//     Only with at least one whole round: with fewer tiles than CUs every
+//     workgroup starts at another k offset, so the workgroups of an XCD no
+//     longer share operand blocks in L2 (TN 2048 x 5632 x 16384, 176 tiles:
+//     450 us against 361 us split in 4; 11264 x 2048, 352 tiles: 655-660
+//     against 685 us, 10240 x 2048: 644-666 against 754 us).
+struct GemmPlan {
+  int slices;   // K slices of the split form
+  bool stream;  // the stream form models faster
+};
+
+GemmPlan gemm_plan(int64_t m, int64_t n, int64_t k) {
   const int64_t tiles = ((m + kTm - 1) / kTm) * ((n + kTn - 1) / kTn), steps = k / kTk;
   const int cus = device_cus();
   const double per_slice = 48.0 * static_cast<double>(m) * n / (655360.0 * static_cast<double>(k));
@@ -479,8 +623,18 @@ int gemm_slices(int64_t m, int64_t n, int64_t k) {
   }
   // Slices of ceil(steps / S) stages; fewer if that leaves the last one empty.
   const int64_t per = (steps + best - 1) / best;
-  return static_cast<int>((steps + per - 1) / per);
+  GemmPlan p{static_cast<int>((steps + per - 1) / per), false};
+  const int64_t sg = stream_grid(), tail = tiles % sg;
+  if (tiles > sg && tail > 0 && steps >= 4) {
+    const double segs = static_cast<double>(std::min<int64_t>(2 * sg, sg + tail));
+    const double cost = static_cast<double>(tiles / sg) + static_cast<double>(tail) / sg +
+                        per_slice * segs * (kTm * kTn) / (static_cast<double>(m) * n);
+    p.stream = cost < 0.97 * best_cost;
+  }
+  return p;
 }
+
+size_t stream_workspace_bytes() { return 2 * static_cast<size_t>(stream_grid()) * kTm * kTn * sizeof(float); }
 
 template <bool A_KO, bool B_KO>
 void launch(const GemmArgs& g, unsigned blocks, bool partial, bool resid, hipStream_t stream) {
@@ -490,7 +644,9 @@ void launch(const GemmArgs& g, unsigned blocks, bool partial, bool resid, hipStr
       return;
     }
   }
-  if (partial)
+  if (g.tail_iters > 0)
+    hipLaunchKernelGGL((k_gemm<A_KO, B_KO, EPI_STREAM>), dim3(blocks), dim3(256), 0, stream, g);
+  else if (partial)
     hipLaunchKernelGGL((k_gemm<A_KO, B_KO, EPI_PARTIAL>), dim3(blocks), dim3(256), 0, stream, g);
   else if (resid)
     hipLaunchKernelGGL((k_gemm<A_KO, B_KO, EPI_RESIDUAL>), dim3(blocks), dim3(256), 0, stream, g);
@@ -507,8 +663,10 @@ using namespace fh;
 
 extern "C" size_t fh_gemm_bf16_workspace_size(int op, int64_t m, int64_t n, int64_t k) {
   if (!valid_op(op) || m <= 0 || n <= 0 || k <= 0 || k % 64) return 0;
-  const int s = gemm_slices(m, n, k);
-  return s > 1 ? static_cast<size_t>(s) * m * n * sizeof(float) : 0;
+  // the stream form's segment slots, or the split form's partials
+  const GemmPlan p = gemm_plan(m, n, k);
+  if (p.stream) return stream_workspace_bytes();
+  return p.slices > 1 ? static_cast<size_t>(p.slices) * m * n * sizeof(float) : 0;
 }
 
 namespace {
@@ -554,10 +712,26 @@ int gemm_setup(int op, const void* a, int64_t lda, const void* b, int64_t ldb, v
   return FH_OK;
 }
 
-// Launches the GEMM of g over `slices` K slices (partials in `workspace`,
-// summed by k_gemm_reduce, when slices > 1).
-int gemm_run(int op, GemmArgs& g, int slices, void* workspace, hipStream_t stream) {
+// Launches the GEMM of g in the stream form (stream: segment slots in
+// `workspace`, split tiles summed by k_gemm_fixup) or over `slices` K slices
+// (partials in `workspace`, summed by k_gemm_reduce, when slices > 1).
+int gemm_run(int op, GemmArgs& g, int slices, bool stream_form, void* workspace, hipStream_t stream) {
   g.part = static_cast<float*>(workspace);
+  if (stream_form) {
+    const int sg = stream_grid();
+    g.grid = sg;
+    g.full_rounds = g.tiles / sg;
+    g.tail_tiles = g.tiles - g.full_rounds * sg;
+    g.tail_iters = static_cast<int64_t>(g.tail_tiles) * g.total_steps;
+    g.steps_per_slice = g.total_steps;
+    switch (op) {
+      case FH_GEMM_NT: launch<false, false>(g, sg, false, false, stream); break;
+      case FH_GEMM_NN: launch<false, true>(g, sg, false, false, stream); break;
+      default: launch<true, true>(g, sg, false, false, stream); break;
+    }
+    hipLaunchKernelGGL(k_gemm_fixup, dim3(g.tail_tiles, kTm / kFixRows), dim3(256), 0, stream, g);
+    return FH_OK;
+  }
   g.steps_per_slice = (g.total_steps + slices - 1) / slices;
   const int64_t logical = static_cast<int64_t>(g.tiles) * slices;
   FH_REQUIRE(logical <= 0x7ffffff0, "gemm_bf16: grid too large");
@@ -589,10 +763,10 @@ extern "C" int fh_gemm_bf16(int op, const void* a, int64_t lda, const void* b, i
                             int64_t k, void* workspace, hipStream_t stream) {
   GemmArgs g;
   if (int e = gemm_setup(op, a, lda, b, ldb, c, ldc, residual, ldr, m, n, k, g)) return e;
-  const int slices = gemm_slices(m, n, k);
-  FH_REQUIRE(slices == 1 || (workspace && aligned16(workspace)),
+  const GemmPlan p = gemm_plan(m, n, k);
+  FH_REQUIRE((p.slices == 1 && !p.stream) || (workspace && aligned16(workspace)),
              "gemm_bf16: workspace (fh_gemm_bf16_workspace_size bytes) required");
-  if (int e = gemm_run(op, g, slices, workspace, stream)) return e;
+  if (int e = gemm_run(op, g, p.slices, p.stream, workspace, stream)) return e;
   return check_launch("fh_gemm_bf16");
 }
 
@@ -615,6 +789,6 @@ extern "C" int fh_gemm_bf16_rope(const void* a, int64_t lda, const void* b, int6
   g.rope.per_token = cos_per_token ? 1 : 0;
   g.rope.seq_len = static_cast<int>(seq_len);
   g.rope.seq = FastDiv(static_cast<uint32_t>(seq_len));
-  if (int e = gemm_run(FH_GEMM_NT, g, 1, nullptr, stream)) return e;  // whole K: the epilogue sees final sums
+  if (int e = gemm_run(FH_GEMM_NT, g, 1, false, nullptr, stream)) return e;  // whole K: the epilogue sees final sums
   return check_launch("fh_gemm_bf16_rope");
 }

@@ -334,8 +334,11 @@ int fh_embedding_bwd(fh_dtype dt, const void* dy, const int64_t* ids, void* dwei
  * residual 16-byte aligned; m, n, k < 2^30.
  * When the output has few 256 x 256 tiles the k range is split into slices
  * whose fp32 partial sums go to `workspace` (fh_gemm_bf16_workspace_size bytes;
- * 0 = none needed) and are added in slice order, so results are bitwise
- * deterministic.
+ * 0 = none needed) and are added in slice order; when its tiles leave the
+ * last round of CUs partly idle, each CU instead takes an equal share of the
+ * k-steps and the tiles split between CUs are summed from fp32 segments in
+ * `workspace` in k order.  Either way results are bitwise deterministic (the
+ * form depends only on m, n, k and the device's CU count).
  */
 typedef enum fh_gemm_op {
   FH_GEMM_NT = 0,

@@ -7,8 +7,9 @@ rounded fp32-accumulated product can be no further off; a dropped term, a
 wrong operand row or an untransposed layout is off by O(|A||B|/sqrt(K)).  The
 bound doubles where the reference itself is fp32.  Results must be bitwise
 identical between two launches (no atomics: split-K partials are summed in
-slice order).  Shapes: every projection GEMM of BASELINE configs 3/4/5 in all
-three layouts, plus ragged, strided and split-K cases.
+slice order, stream-form segments in k order).  Shapes: every projection GEMM
+of BASELINE configs 3/4/5 in all three layouts, plus ragged, strided, split-K
+and stream-form cases.
 """
 from __future__ import annotations
 
@@ -90,6 +91,21 @@ def test_gemm_ragged_strided_split(op, m, n, k, pad):
     c = ops.gemm(op, a, b)
     _check(op, a, b, c, exact=True)
     assert torch.equal(c, ops.gemm(op, a, b))
+
+
+@pytest.mark.parametrize("m,n,k,pad", [(10232, 2040, 16384, 0), (4104, 4088, 8192, 8), (6400, 3000, 8192, 0)])
+def test_stream_form_matches_and_is_deterministic(m, n, k, pad):
+    # Weight-gradient shapes whose tiles leave the last round of CUs partly
+    # idle: the stream form spreads the k-steps evenly over the CUs and adds
+    # the split tiles' fp32 segments in k order.  Its workspace is the segment
+    # slots (two 256 x 256 fp32 tiles per CU).
+    cus = torch.cuda.get_device_properties(0).multi_processor_count // 8 * 8
+    assert _lib.lib().fh_gemm_bf16_workspace_size(_lib.FH_GEMM_TN, m, n, k) == 2 * cus * 256 * 256 * 4
+    g = torch.Generator(device=DEV).manual_seed(m + n + k)
+    a, b = _operands("tn", m, n, k, g, pad)
+    c = ops.gemm("tn", a, b)
+    _check("tn", a, b, c, exact=True)
+    assert torch.equal(c, ops.gemm("tn", a, b))
 
 
 def test_split_k_path_is_used_and_matches():
