@@ -212,6 +212,10 @@ __device__ __forceinline__ void rope_q_frags(bf16x8 (&qf)[HD / 16], const uint16
 // let every K/V fragment read from LDS feed two MFMAs, but its registers cost
 // a wave of occupancy and it measured slower at head_dim 64 (342 vs 308 us at
 // the TinyLlama shape), so QT = 1.  Heaviest (latest) query blocks first.
+// With GQA (two query heads per kv head) a block of HPB = 2 x 4 waves takes the
+// same query rows of two query heads, which read the same K/V tiles: each tile
+// loaded into LDS feeds twice the MFMAs (TinyLlama 199 -> 190 us, rotated q
+// 205-215 -> 203 us; Llama-3 slice 541-546 -> 506 us; bit-identical output).
 template <int HD>
 struct FwdTiles {
   static constexpr int QT = 1;
@@ -229,11 +233,11 @@ struct FwdTiles {
 // occupancy step, computes them per load instead (dma_tile).
 // pre() runs once after block 0's loads are issued, before they are waited
 // for (the kernel's own loads then overlap them).
-template <int BN, int HD, bool FAST, class Body, class Pre>
+template <int BN, int HD, bool FAST, int NW, class Body, class Pre>
 __device__ __forceinline__ void kv_block_loop(const uint16_t* kb_ptr, int64_t ldk, const uint16_t* vb_ptr,
                                               int64_t ldv, int nkb, int S, char* sk0, char* sk1, char* sv0,
                                               char* sv1, int wave, int lane, Body&& body, Pre&& pre) {
-  TileDma<BN, HD, 4> dk, dv;
+  TileDma<BN, HD, NW> dk, dv;
   dk.init(ldk, wave, lane);
   dv.init(ldv, wave, lane);
   auto load = [&](int r0, char* KN, char* VN) __attribute__((always_inline)) {
@@ -345,8 +349,8 @@ __device__ __forceinline__ void fwd_block(const char* K, const char* V, const bf
   for (int u = 0; u < QT; ++u) l[u] += lsum[u];
 }
 
-template <int HD>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_fwd(
+template <int HD, int HPB>
+__global__ __launch_bounds__(256 * HPB) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_fwd(
     const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
     const uint16_t* __restrict__ v, int64_t ldv, uint16_t* __restrict__ o, int64_t ldo,
     float* __restrict__ lse, int S, int nh, int group, float scale_log2, RopeRows<uint16_t> rope,
@@ -357,9 +361,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const XcdOrder ord = xcd_order();
-  const int bh = ord.y, b = bh / nh, h = bh - b * nh, kvh = h / group;
+  const int nhb = nh / HPB, bg = ord.y, b = bg / nhb;
+  const int h = (bg - b * nhb) * HPB + (wave >> 2), kvh = h / group, bh = b * nh + h;
   const int q0 = (gridDim.x - 1 - ord.rank) * BM;  // heaviest (latest) query blocks first
-  const int qw = q0 + wave * 32 * QT;  // first query of this wave
+  const int qw = q0 + (wave & 3) * 32 * QT;  // first query of this wave
   const int64_t tok0 = static_cast<int64_t>(b) * S;
   int a_off = lane_off_a<HD>(lane);
   int b0 = lane_off_b<HD>(lane, 0), b8 = lane_off_b<HD>(lane, 8);
@@ -395,7 +400,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   const int nkb = (kend + BN - 1) / BN;
   const uint16_t* kb_ptr = k + tok0 * ldk + static_cast<int64_t>(kvh) * HD;
   const uint16_t* vb_ptr = v + tok0 * ldv + static_cast<int64_t>(kvh) * HD;
-  kv_block_loop<BN, HD, true>(kb_ptr, ldk, vb_ptr, ldv, nkb, S, sk0, sk1, sv0, sv1, wave, lane,
+  kv_block_loop<BN, HD, true, 4 * HPB>(kb_ptr, ldk, vb_ptr, ldv, nkb, S, sk0, sk1, sv0, sv1, wave, lane,
                         [&](int kb, const char* K, const char* V) __attribute__((always_inline)) {
                           refresh_offsets(a_off, b0, b8);
                           const int k0 = kb * BN;
@@ -545,7 +550,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   const int nkb = (kend + BN - 1) / BN;
   const uint16_t* kb_ptr = k + tok0 * ldk + static_cast<int64_t>(kvh) * HD;
   const uint16_t* vb_ptr = v + tok0 * ldv + static_cast<int64_t>(kvh) * HD;
-  kv_block_loop<BN, HD, false>(kb_ptr, ldk, vb_ptr, ldv, nkb, S, sk0, sk1, sv0, sv1, wave, lane,
+  kv_block_loop<BN, HD, false, 4>(kb_ptr, ldk, vb_ptr, ldv, nkb, S, sk0, sk1, sv0, sv1, wave, lane,
                         [&](int kb, const char* K, const char* V) __attribute__((always_inline)) {
                           refresh_offsets(a_off, b0, b8);
                           const int k0 = kb * BN;
@@ -1197,12 +1202,19 @@ int attn_fwd_impl(fh_dtype dt, const void* q, int64_t ldq, const void* k, int64_
                                 rp.per_token};
     dispatch_hd(head_dim, [&](auto hdc) {
       constexpr int BM = 4 * 32 * FwdTiles<decltype(hdc)::value>::QT;
+      const bool pair = group % 2 == 0 && (batch * n_heads / 2) % 8 == 0;
       const dim3 grid(static_cast<unsigned>((seq_len + BM - 1) / BM),
-                      static_cast<unsigned>(batch * n_heads));
-      hipLaunchKernelGGL((k_attn_fwd<hdc()>), grid, dim3(256), 0, stream,
-                         static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(k), ldk,
-                         static_cast<const uint16_t*>(v), ldv, static_cast<uint16_t*>(o), ldo, lse,
-                         S, nh, group, scale * kLog2e, rb, static_cast<uint16_t*>(qout), ldqo);
+                      static_cast<unsigned>(batch * n_heads / (pair ? 2 : 1)));
+      if (pair)
+        hipLaunchKernelGGL((k_attn_fwd<hdc(), 2>), grid, dim3(512), 0, stream,
+                           static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(k), ldk,
+                           static_cast<const uint16_t*>(v), ldv, static_cast<uint16_t*>(o), ldo, lse,
+                           S, nh, group, scale * kLog2e, rb, static_cast<uint16_t*>(qout), ldqo);
+      else
+        hipLaunchKernelGGL((k_attn_fwd<hdc(), 1>), grid, dim3(256), 0, stream,
+                           static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(k), ldk,
+                           static_cast<const uint16_t*>(v), ldv, static_cast<uint16_t*>(o), ldo, lse,
+                           S, nh, group, scale * kLog2e, rb, static_cast<uint16_t*>(qout), ldqo);
       return 0;
     });
   } else {
