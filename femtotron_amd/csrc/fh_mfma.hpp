@@ -147,8 +147,10 @@ __device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t
 // outside the loop): a tile at row r0 is read at src + r0*ld, wave-uniform,
 // plus this lane's fixed byte offset of each of the wave's runs, so a load
 // costs no vector address arithmetic.  Only a tile that runs past `last` (the
-// ragged end of a sequence) takes dma_tile's clamped path.  Offsets are 32-bit:
-// the caller keeps ROWS * ld * 2 below 2^32.
+// ragged end of a sequence) takes dma_tile's clamped path, behind a branch
+// marked unlikely (as a select, both address forms were computed for every
+// tile: 22 instead of 11 vector instructions per K/V block of the forward).
+// Offsets are 32-bit: the caller keeps ROWS * ld * 2 below 2^32.
 template <int ROWS, int HD, int NW>
 struct TileDma {
   static constexpr int CPR = HD / 8, RPR = 64 / CPR, RUNS = ROWS / RPR, PER = (RUNS + NW - 1) / NW;
@@ -164,7 +166,7 @@ struct TileDma {
                                        int lane) const {
     typedef __attribute__((address_space(1))) const void* gptr;
     typedef __attribute__((address_space(3))) void* lptr;
-    if (r0 + ROWS - 1 <= last) {
+    if (__builtin_expect(r0 + ROWS - 1 <= last, 1)) {
       const char* base = reinterpret_cast<const char*>(src + static_cast<int64_t>(r0) * ld);
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
@@ -184,7 +186,7 @@ struct TileDma {
   __device__ __forceinline__ void load_asm(const uint16_t* src, int64_t ld, int r0, int last, char* dst, int wave,
                                            int lane) const {
     typedef __attribute__((address_space(3))) char* lptr;
-    if (r0 + ROWS - 1 <= last) {
+    if (__builtin_expect(r0 + ROWS - 1 <= last, 1)) {
       const void* base = src + static_cast<int64_t>(r0) * ld;
       const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lptr)dst));
 #pragma unroll
