@@ -108,6 +108,23 @@ def test_stream_form_matches_and_is_deterministic(m, n, k, pad):
     assert torch.equal(c, ops.gemm("tn", a, b))
 
 
+def test_stream_form_residual_epilogue_rounds_like_the_unfused_add():
+    """The stream form's residual epilogue (whole tiles in the GEMM, split tiles
+    in the fixup) gives to_bf16(R + to_bf16(A.B)) bit for bit, also in place."""
+    m, n, k = 4104, 4088, 8192
+    cus = torch.cuda.get_device_properties(0).multi_processor_count // 8 * 8
+    assert _lib.lib().fh_gemm_bf16_workspace_size(_lib.FH_GEMM_TN, m, n, k) == 2 * cus * 256 * 256 * 4
+    g = torch.Generator(device=DEV).manual_seed(17)
+    a, b = _operands("tn", m, n, k, g)
+    r = torch.randn(m, n, device=DEV, generator=g).to(BF)
+    fused = ops.gemm("tn", a, b, residual=r)
+    unfused = (r.float() + ops.gemm("tn", a, b).float()).to(BF)
+    assert torch.equal(fused, unfused)
+    inplace = r.clone()
+    ops.gemm("tn", a, b, residual=inplace, out=inplace)
+    assert torch.equal(inplace, fused)
+
+
 def test_split_k_path_is_used_and_matches():
     # 512 x 512 outputs are 4 tiles: the k range is split into slices
     m = n = 512
