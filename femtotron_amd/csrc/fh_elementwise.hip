@@ -239,6 +239,32 @@ __global__ __launch_bounds__(256) void k_add(const T* a, const T* b, T* out, int
   }
 }
 
+// out = to_dtype(x * scale[0]): the loss head's backward, which multiplies
+// its saved input and weight gradients by the incoming gradient of the loss
+// (a device scalar, so the host never waits for it).
+template <typename T>
+__global__ __launch_bounds__(256) void k_scale(const T* x, T* out, int64_t n8, const float* scale) {
+  using Raw = typename Elem<T>::Raw;
+  const float s = *scale;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * (256 * kChunks) + threadIdx.x;
+  Raw xr[kChunks];
+#pragma unroll
+  for (int k = 0; k < kChunks; ++k) {
+    const int64_t i = first + 256 * k;
+    if (i < n8) xr[k] = Elem<T>::ldraw(x + i * 8);
+  }
+#pragma unroll
+  for (int k = 0; k < kChunks; ++k) {
+    const int64_t i = first + 256 * k;
+    if (i >= n8) break;
+    float v[8];
+    Elem<T>::unpack(xr[k], v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] *= s;
+    Elem<T>::store8(out + i * 8, v);
+  }
+}
+
 inline unsigned blocks_for(int64_t threads) {
   return static_cast<unsigned>((threads + 255) / 256);
 }
@@ -380,4 +406,20 @@ extern "C" int fh_add(fh_dtype dt, const void* a, const void* b, void* out, int6
                        static_cast<const float*>(a), static_cast<const float*>(b),
                        static_cast<float*>(out), n / 8);
   return check_launch("fh_add");
+}
+
+extern "C" int fh_scale(fh_dtype dt, const void* x, void* out, int64_t n, const float* scale,
+                        hipStream_t stream) {
+  FH_REQUIRE(ok_dtype(dt), "scale: dtype must be FH_BF16 or FH_F32");
+  FH_REQUIRE(n >= 0 && n % 8 == 0, "scale: n must be a non-negative multiple of 8");
+  if (n == 0) return FH_OK;
+  FH_REQUIRE(x && out && scale, "scale: null pointer");
+  FH_REQUIRE(aligned16(x) && aligned16(out), "scale: pointers must be 16-byte aligned");
+  if (dt == FH_BF16)
+    hipLaunchKernelGGL((k_scale<uint16_t>), dim3(stream_blocks(n / 8)), dim3(256), 0, stream,
+                       static_cast<const uint16_t*>(x), static_cast<uint16_t*>(out), n / 8, scale);
+  else
+    hipLaunchKernelGGL((k_scale<float>), dim3(stream_blocks(n / 8)), dim3(256), 0, stream,
+                       static_cast<const float*>(x), static_cast<float*>(out), n / 8, scale);
+  return check_launch("fh_scale");
 }

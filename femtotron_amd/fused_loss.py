@@ -87,9 +87,14 @@ class FusedLinearCrossEntropy(torch.autograd.Function):
     def backward(ctx, grad):
         dx, dw = ctx.saved_tensors
         g = grad.to(torch.float32)
-        gx = (dx * g).to(dx.dtype) if dx is not None else None
-        gw = (dw * g).to(dw.dtype) if dw is not None else None
-        return gx, gw, None
+
+        def scaled(t):  # (t * g).to(t.dtype): fh_scale, one streaming pass
+            if t is None:
+                return None
+            if t.numel() % 8 == 0 and t.data_ptr() % 16 == 0 and t.is_contiguous():
+                return ops.scale(t, g)
+            return (t * g).to(t.dtype)
+        return scaled(dx), scaled(dw), None
 
 
 def fused_causal_lm_loss(hidden: torch.Tensor, weight: torch.Tensor,

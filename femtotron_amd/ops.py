@@ -204,6 +204,21 @@ def swiglu_bwd(dp: torch.Tensor, g: torch.Tensor, u: torch.Tensor, dg: torch.Ten
               _ptr(u), ld_gu, _ptr(dg), _ptr(du), ld_d, rows, cols, _stream(g))
 
 
+def scale(x: torch.Tensor, s: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """to_dtype(x * s) (fh_scale) for a contiguous bf16/fp32 x and an fp32 scalar tensor s on the
+    same device; what ``(x * s).to(x.dtype)`` gives, in one streaming pass."""
+    _require_gpu(x, s, out)
+    if not x.is_contiguous() or s.numel() != 1 or s.dtype != torch.float32:
+        raise ValueError("scale: x must be contiguous and s a one-element fp32 tensor")
+    o = torch.empty_like(x) if out is None else out
+    _same_dtype(x, o)
+    if o.shape != x.shape or not o.is_contiguous():
+        raise ValueError("scale: out must be a contiguous tensor of x's shape")
+    sc = s.contiguous()
+    _lib.call("fh_scale", _dtype_code(x), _ptr(x), _ptr(o), x.numel(), _ptr(sc), _stream(x))
+    return o
+
+
 def add(a: torch.Tensor, b: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
     _require_gpu(a, b, out)
     _same_dtype(a, b, out)

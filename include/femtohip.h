@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define FH_ABI_VERSION 3
+#define FH_ABI_VERSION 4
 
 typedef enum fh_dtype {
   FH_BF16 = 0, /* bfloat16 storage, fp32 arithmetic */
@@ -158,6 +158,14 @@ int fh_swiglu_bwd(fh_dtype dt, const void* dp, int64_t ld_dp, const void* g,
  * (modeling_llama.py:323).  n % 8 == 0; out may alias a or b. */
 int fh_add(fh_dtype dt, const void* a, const void* b, void* out, int64_t n,
            hipStream_t stream);
+
+/* out = to_dtype(x * scale[0]) over n elements, scale a device fp32 scalar:
+ * the chain rule of a saved gradient times the incoming gradient of a scalar
+ * loss, `(g_saved * grad).to(dtype)` in torch (the fused loss head's backward;
+ * the reference's loss backward is autograd over aten ops, model/llama.py:91-111).
+ * n % 8 == 0; out may alias x. */
+int fh_scale(fh_dtype dt, const void* x, void* out, int64_t n, const float* scale,
+             hipStream_t stream);
 
 /* ---------------------------------------------------------------- attention
  * Causal GQA softmax attention, replacing F.scaled_dot_product_attention(

@@ -240,6 +240,20 @@ def test_add_bit_exact_and_in_place():
     assert torch.equal(db.cpu(), a + b)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_scale_bit_exact_and_in_place(dtype):
+    """fh_scale = (x * s).to(x.dtype) with s an fp32 device scalar (the fused
+    loss head's backward), against torch on the CPU; also in place."""
+    ops = _ops()
+    x = randn((1000, 72), 42).to(dtype)
+    s = torch.tensor(0.3719, dtype=torch.float32)
+    ref = (x * s).to(dtype)
+    dx = _dev(x)
+    assert torch.equal(ops.scale(dx, _dev(s)).cpu(), ref)
+    ops.scale(dx, _dev(s), out=dx)
+    assert torch.equal(dx.cpu(), ref)
+
+
 # ------------------------------------------------------------- error paths
 def test_invalid_arguments_raise():
     from femtotron_amd._lib import FemtoHipError
