@@ -438,9 +438,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* ring, int t, 
   }
 }
 
-// Split K (EPI_PARTIAL), one tile per workgroup, or stream (EPI_STREAM): the
-// workgroup runs its whole tiles, then its share of the tail's k-steps as
-// segments of one tile each.  A tail segment that is not a whole tile goes to
+// One tile, or one K slice of a tile (EPI_PARTIAL), per workgroup; or the
+// stream form (EPI_STREAM): the workgroup runs its whole tiles, then its share
+// of the tail's k-steps as segments of one tile each.  A tail segment that is not a whole tile goes to
 // fp32 slot 2w (the workgroup's first tail segment) or 2w + 1 (its last);
 // k_gemm_fixup adds a split tile's segments in k order.
 template <bool A_KO, bool B_KO, int EPI>
