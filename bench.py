@@ -265,15 +265,17 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True,
         # RoPE backward runs inside the attention backward's dQ / dK stores
         ms = event_ms(torch, lambda i=0: ops.rope_fwd_(qkvs[i % 6][:, Hq:], nkv, hd, c["seq"], cos, sin), iters)
         add_row("rope_fwd", "k_rope<fwd> (k heads)", n_fwd, 4 * T * Hkv, ms)
-    # SwiGLU: g,u -> p (6TF);  dp,g,u -> dg,du (10TF)
+    # SwiGLU: g,u -> p (6TF), in the forward only (the recompute stops at the
+    # gate/up projection);  dp,g,u -> dg,du and p over dp (12TF)
     gus = sets(3, lambda: rnd(T, 2 * F))
     ps = sets(3, lambda: torch.empty(T, F, device=dev, dtype=bf))
     ms = event_ms(torch, lambda i=0: ops.swiglu_fwd(gus[i % 3][:, :F], gus[i % 3][:, F:], out=ps[i % 3]), iters)
-    add_row("swiglu_fwd", "k_swiglu_fwd", 2 * L, 6 * T * F, ms)
+    add_row("swiglu_fwd", "k_swiglu_fwd", L, 6 * T * F, ms)
     dgus = sets(3, lambda: torch.empty(T, 2 * F, device=dev, dtype=bf))
     ms = event_ms(torch, lambda i=0: ops.swiglu_bwd(ps[i % 3], gus[i % 3][:, :F], gus[i % 3][:, F:],
-                                                      dgus[i % 3][:, :F], dgus[i % 3][:, F:]), iters)
-    add_row("swiglu_bwd", "k_swiglu_bwd", L, 10 * T * F, ms)
+                                                      dgus[i % 3][:, :F], dgus[i % 3][:, F:], p_out=ps[i % 3]),
+                  iters)
+    add_row("swiglu_bwd", "k_swiglu_bwd (+ p over dp)", L, 12 * T * F, ms)
     del gus, ps, dgus
     if boundary:
         # embedding: gather (T rows read and written + int64 ids); backward:
@@ -402,7 +404,8 @@ def chain_table(torch, shape: dict, reps: int) -> list:
     row("rope_fwd", "k_rope<fwd>", 4 * T * nr * hd, lambda i: ops.rope_fwd_(q, nr, hd, T, cos, sin))
     row("rope_bwd", "k_rope<bwd>", 4 * T * nr * hd, lambda i: ops.rope_bwd_(q, nr, hd, T, cos, sin))
     row("swiglu_fwd", "k_swiglu_fwd", 6 * T * Fd, lambda i: ops.swiglu_fwd(g, u, out=p))
-    row("swiglu_bwd", "k_swiglu_bwd", 10 * T * Fd, lambda i: ops.swiglu_bwd(dp, g, u, dg, du))
+    row("swiglu_bwd", "k_swiglu_bwd (+ p over dp)", 12 * T * Fd,
+        lambda i: ops.swiglu_bwd(dp, g, u, dg, du, p_out=dp))
     row("residual_add", "k_add", 6 * T * H, lambda i: ops.add(x, dy, out=hh))
     del flush_buf
     return rows
@@ -495,8 +498,9 @@ def profile_kernel(torch, name: str, c: dict, launches: int = 10) -> dict:
         else:
             dps = [rnd(T, F) for _ in range(n)]
             out = torch.empty(T, 2 * F, device=dev, dtype=bf)
-            fn = lambda i: ops.swiglu_bwd(dps[i], gus[i][:, :F], gus[i][:, F:], out[:, :F], out[:, F:])
-            nbytes = 10 * T * F
+            fn = lambda i: ops.swiglu_bwd(dps[i], gus[i][:, :F], gus[i][:, F:], out[:, :F], out[:, F:],
+                                          p_out=dps[i])
+            nbytes = 12 * T * F
     elif name in ("rmsnorm_fwd", "add_rmsnorm_fwd", "rmsnorm_bwd", "residual_add"):
         xs = [rnd(T, H) for _ in range(n)]
         as_ = [rnd(T, H) for _ in range(n)]

@@ -12,7 +12,7 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_size_t, c_void_
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libfemtohip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 FH_BF16 = 0
 FH_F32 = 1
@@ -46,7 +46,7 @@ SIGNATURES: dict[str, tuple] = {
     "fh_rope_fwd": (c_int, [c_int, _V, _I64, _I64, _I64, _I64, _I64, _V, _V, c_int, _V]),
     "fh_rope_bwd": (c_int, [c_int, _V, _I64, _I64, _I64, _I64, _I64, _V, _V, c_int, _V]),
     "fh_swiglu_fwd": (c_int, [c_int, _V, _V, _I64, _V, _I64, _I64, _I64, _V]),
-    "fh_swiglu_bwd": (c_int, [c_int, _V, _I64, _V, _V, _I64, _V, _V, _I64, _I64, _I64, _V]),
+    "fh_swiglu_bwd": (c_int, [c_int, _V, _I64, _V, _V, _I64, _V, _V, _I64, _V, _I64, _I64, _I64, _V]),
     "fh_add": (c_int, [c_int, _V, _V, _V, _I64, _V]),
     "fh_scale": (c_int, [c_int, _V, _V, _I64, _V, _V]),
     "fh_attn_fwd": (c_int, [c_int, _V, _I64, _V, _I64, _V, _I64, _V, _I64, POINTER(c_float),

@@ -166,12 +166,18 @@ __global__ __launch_bounds__(256) void k_swiglu_fwd(const T* __restrict__ g,
   }
 }
 
-template <typename T, bool WIDE>
-__global__ __launch_bounds__(256) void k_swiglu_bwd(const T* __restrict__ dp, int64_t ld_dp,
+// With P, also p = silu(g) * u as k_swiglu_fwd rounds it (the stored silu(g)
+// times u), written to p: a backward that did not keep the forward's product
+// gets it from the pass that reads g and u anyway.  p may be dp itself (each
+// thread reads its chunk of dp before it writes the same chunk of p), so
+// neither is __restrict__.
+template <typename T, bool WIDE, bool P>
+__global__ __launch_bounds__(256) void k_swiglu_bwd(const T* dp, int64_t ld_dp,
                                                     const T* __restrict__ g,
                                                     const T* __restrict__ u, int64_t ld_gu,
                                                     T* __restrict__ dg, T* __restrict__ du,
-                                                    int64_t ld_dgu, int64_t rows, int cols, FastDiv fd) {
+                                                    int64_t ld_dgu, T* p, int64_t ld_p, int64_t rows, int cols,
+                                                    FastDiv fd) {
   using Raw = typename Elem<T>::Raw;
   const int cpr = cols >> 3;
   const int64_t total = rows * cpr;
@@ -196,20 +202,22 @@ __global__ __launch_bounds__(256) void k_swiglu_bwd(const T* __restrict__ dp, in
     int64_t r;
     int c;
     row_col<WIDE>(idx, cpr, fd, r, c);
-    float dv[8], gv[8], uv[8], og[8], ou[8];
+    float dv[8], gv[8], uv[8], og[8], ou[8], op[8];
     Elem<T>::unpack(dr[k], dv);
     Elem<T>::unpack(gr[k], gv);
     Elem<T>::unpack(ur[k], uv);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float sg = sigmoid_f(gv[j]);
-      const float s = Elem<T>::rnd(gv[j] * sg);          // the stored silu(g)
+      const float s = Elem<T>::rnd(gv[j] * sg);          // the stored silu(g) (= rnd(silu_f(g)))
       ou[j] = dv[j] * s;                                  // d(up)
       const float ds = Elem<T>::rnd(dv[j] * uv[j]);       // grad at silu output
       og[j] = ds * sg * (1.f + gv[j] * (1.f - sg));       // silu_backward
+      if constexpr (P) op[j] = s * uv[j];                 // the forward's product
     }
     Elem<T>::store8(dg + r * ld_dgu + c, og);
     Elem<T>::store8(du + r * ld_dgu + c, ou);
+    if constexpr (P) Elem<T>::store8(p + r * ld_p + c, op);
   }
 }
 
@@ -360,32 +368,39 @@ extern "C" int fh_swiglu_fwd(fh_dtype dt, const void* g, const void* u, int64_t 
 
 extern "C" int fh_swiglu_bwd(fh_dtype dt, const void* dp, int64_t ld_dp, const void* g,
                              const void* u, int64_t ld_gu, void* dg, void* du, int64_t ld_dgu,
-                             int64_t rows, int64_t cols, hipStream_t stream) {
+                             void* p, int64_t ld_p, int64_t rows, int64_t cols, hipStream_t stream) {
   FH_REQUIRE(ok_dtype(dt), "swiglu_bwd: dtype must be FH_BF16 or FH_F32");
   FH_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0, "swiglu_bwd: cols must be a positive multiple of 8");
   FH_REQUIRE(ld_dp >= cols && ld_gu >= cols && ld_dgu >= cols && ld_dp % 8 == 0 &&
                  ld_gu % 8 == 0 && ld_dgu % 8 == 0,
              "swiglu_bwd: leading dims must be >= cols and multiples of 8");
+  FH_REQUIRE(!p || (ld_p >= cols && ld_p % 8 == 0), "swiglu_bwd: ld_p must be >= cols and a multiple of 8");
+  FH_REQUIRE(!p || p != dp || ld_p == ld_dp, "swiglu_bwd: p aliasing dp must share its leading dim");
   if (rows == 0) return FH_OK;
   FH_REQUIRE(dp && g && u && dg && du, "swiglu_bwd: null pointer");
-  FH_REQUIRE(aligned16(dp) && aligned16(g) && aligned16(u) && aligned16(dg) && aligned16(du),
+  FH_REQUIRE(aligned16(dp) && aligned16(g) && aligned16(u) && aligned16(dg) && aligned16(du) &&
+                 (!p || aligned16(p)),
              "swiglu_bwd: pointers must be 16-byte aligned");
   const int64_t threads = rows * (cols / 8);
   const FastDiv fd(static_cast<uint32_t>(cols / 8));
-  auto go = [&](auto tag, auto wide_c) {
+  auto go = [&](auto tag, auto wide_c, auto p_c) {
     using T = decltype(tag);
-    hipLaunchKernelGGL((k_swiglu_bwd<T, decltype(wide_c)::value>), dim3(stream_blocks(threads)),
-                       dim3(256), 0, stream, static_cast<const T*>(dp), ld_dp,
+    hipLaunchKernelGGL((k_swiglu_bwd<T, decltype(wide_c)::value, decltype(p_c)::value>),
+                       dim3(stream_blocks(threads)), dim3(256), 0, stream, static_cast<const T*>(dp), ld_dp,
                        static_cast<const T*>(g), static_cast<const T*>(u), ld_gu,
-                       static_cast<T*>(dg), static_cast<T*>(du), ld_dgu, rows,
+                       static_cast<T*>(dg), static_cast<T*>(du), ld_dgu, static_cast<T*>(p), ld_p, rows,
                        static_cast<int>(cols), fd);
   };
+  auto with_p = [&](auto tag, auto wide_c) {
+    if (p) go(tag, wide_c, std::true_type{});
+    else go(tag, wide_c, std::false_type{});
+  };
   if (dt == FH_BF16) {
-    if (wide(threads)) go(uint16_t{}, std::true_type{});
-    else go(uint16_t{}, std::false_type{});
+    if (wide(threads)) with_p(uint16_t{}, std::true_type{});
+    else with_p(uint16_t{}, std::false_type{});
   } else {
-    if (wide(threads)) go(float{}, std::true_type{});
-    else go(float{}, std::false_type{});
+    if (wide(threads)) with_p(float{}, std::true_type{});
+    else with_p(float{}, std::false_type{});
   }
   return check_launch("fh_swiglu_bwd");
 }

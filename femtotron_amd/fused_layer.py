@@ -4,9 +4,10 @@ This is the drop-in for one ``checkpoint_fn(LlamaDecoderLayer, hidden_states, ..
 call of femtotron/training/activation_ckpt.py:78-86.  The forward keeps only the
 layer input (exactly what torch.utils.checkpoint's ``_NoopSaveInputs`` keeps,
 torch/utils/checkpoint.py:794-831); backward recomputes the layer forward up to
-the SwiGLU product (the down projection and final residual add are not needed,
-mirroring the non-reentrant checkpoint's early stop) and then runs the layer's
-backward.
+the gate/up projection (the down projection and final residual add are not
+needed, mirroring the non-reentrant checkpoint's early stop; the SwiGLU product
+p is written by the SwiGLU backward, which reads g and u anyway) and then runs
+the layer's backward.
 
 Layer arithmetic (transformers 5.15.0, models/llama/modeling_llama.py:284-325):
     y1 = RMSNorm1(x)
@@ -17,7 +18,7 @@ Layer arithmetic (transformers 5.15.0, models/llama/modeling_llama.py:284-325):
     o     = causal GQA attention(q,k,v)
     h     = x + o Wo^T;  z = RMSNorm2(h)         (fh_add_rmsnorm_fwd)
     g,u   = z Wg^T, z Wu^T                       -> one GEMM over [Wg;Wu]
-    p     = silu(g)*u                            (fh_swiglu_fwd)
+    p     = silu(g)*u                            (fh_swiglu_fwd; in backward, fh_swiglu_bwd)
     out   = h + p Wd^T                           (residual add in the GEMM epilogue)
 
 The projections' GEMMs go through femtotron_amd.projections (fh_gemm_bf16 or
@@ -111,13 +112,14 @@ def attn_bwd(do: torch.Tensor, qkv: torch.Tensor, o: torch.Tensor, lse: torch.Te
 class _Acts:
     """Recomputed activations the backward needs."""
 
-    __slots__ = ("y1", "rstd1", "qkv", "o", "lse", "h", "rstd2", "z", "gu", "p")
+    __slots__ = ("y1", "rstd1", "qkv", "o", "lse", "h", "rstd2", "z", "gu")
 
 
 def layer_forward(x2: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, shp: LayerShape,
                   batch: int, seq: int, w: tuple, *, keep: bool):
     """Run the layer on x2 [T, H].  keep=False returns the output [T, H];
-    keep=True (recompute) stops after the SwiGLU product and returns _Acts."""
+    keep=True (recompute) stops after the gate/up projection and returns _Acts
+    (the backward's SwiGLU pass writes the product p itself)."""
     wq, wk, wv, wo, wg, wu, wd, w1, w2 = w
     T, H = x2.shape
     dev = x2.device
@@ -132,11 +134,11 @@ def layer_forward(x2: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, shp: L
     del a
     gu = linear(z, _cat_rows(wg, wu))
     F_ = shp.ffn
-    p = ops.swiglu_fwd(gu[:, :F_], gu[:, F_:])
     if keep:
         acts.y1, acts.rstd1, acts.qkv, acts.o, acts.lse = y1, rstd1, qkv, o, lse
-        acts.h, acts.rstd2, acts.z, acts.gu, acts.p = h, rstd2, z, gu, p
+        acts.h, acts.rstd2, acts.z, acts.gu = h, rstd2, z, gu
         return acts
+    p = ops.swiglu_fwd(gu[:, :F_], gu[:, F_:])
     del gu, qkv, o, y1, z
     return linear_residual(p, wd, h)
 
@@ -201,14 +203,15 @@ def layer_backward(dout2: torch.Tensor, x2: torch.Tensor, cos: torch.Tensor, sin
     wq, wk, wv, wo, wg, wu, wd, w1, w2 = w
     F_ = shp.ffn
     wg_stream = _WgradStream(dout2.device)
-    # MLP: m = p Wd^T
-    dwd = wg_stream.mm_tn(dout2, acts.p)
+    # MLP: m = p Wd^T.  The SwiGLU backward also writes p (into dp's buffer,
+    # each element read before it is overwritten) for the down projection's
+    # weight gradient, so the recompute stops before the product.
     dp = linear_dgrad(dout2, wd)
-    acts.p = None
     dgu = torch.empty_like(acts.gu)
-    ops.swiglu_bwd(dp, acts.gu[:, :F_], acts.gu[:, F_:], dgu[:, :F_], dgu[:, F_:])
-    del dp
+    ops.swiglu_bwd(dp, acts.gu[:, :F_], acts.gu[:, F_:], dgu[:, :F_], dgu[:, F_:], p_out=dp)
     acts.gu = None
+    dwd = wg_stream.mm_tn(dout2, dp)
+    del dp
     dwgu = wg_stream.mm_tn(dgu, acts.z)
     dz = linear_dgrad(dgu, _cat_rows(wg, wu))
     del dgu

@@ -11,7 +11,7 @@ backward what the backward needs.
 
 MLP (HF models/llama/modeling_llama.py:163-177):
     g,u = z Wg^T, z Wu^T   -> one GEMM over [Wg;Wu] into a [T, 2F] buffer
-    p   = silu(g)*u        (fh_swiglu_fwd, HF's two bf16 roundings)
+    p   = silu(g)*u        (fh_swiglu_fwd, HF's two bf16 roundings; in backward fh_swiglu_bwd)
     m   = p Wd^T
 RMSNorm (HF models/llama/modeling_llama.py:52-70):
     y = w * to_dtype(x * rsqrt(mean(x^2) + eps))   (fh_rmsnorm_fwd; backward
@@ -28,27 +28,30 @@ from .projections import linear, linear_dgrad
 
 def mlp_forward(z2: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor, wd: torch.Tensor, *,
                 keep: bool):
-    """z2 [T, H] -> m [T, H]; keep=True stops after the SwiGLU product and
-    returns (gu, p) for the backward."""
+    """z2 [T, H] -> m [T, H]; keep=True stops after the gate/up projection and
+    returns gu for the backward (whose SwiGLU pass writes the product p)."""
     F_ = wg.shape[0]
     gu = linear(z2, _cat_rows(wg, wu))
-    p = ops.swiglu_fwd(gu[:, :F_], gu[:, F_:])
     if keep:
-        return gu, p
+        return gu
+    p = ops.swiglu_fwd(gu[:, :F_], gu[:, F_:])
     del gu
     return linear(p, wd)
 
 
 def mlp_backward(dm2: torch.Tensor, z2: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor,
-                 wd: torch.Tensor, gu: torch.Tensor, p: torch.Tensor):
+                 wd: torch.Tensor, gu: torch.Tensor):
+    """The MLP's backward from the recomputed gu (pass it without keeping a
+    reference, so that it is freed once the SwiGLU backward has read it)."""
     F_ = wg.shape[0]
     wg_stream = _WgradStream(dm2.device)
-    dwd = wg_stream.mm_tn(dm2, p)
     dp = linear_dgrad(dm2, wd)
-    del p
     dgu = torch.empty_like(gu)
-    ops.swiglu_bwd(dp, gu[:, :F_], gu[:, F_:], dgu[:, :F_], dgu[:, F_:])
-    del dp, gu
+    # also p = silu(g)*u, into dp's buffer (read before overwritten), for dWd
+    ops.swiglu_bwd(dp, gu[:, :F_], gu[:, F_:], dgu[:, :F_], dgu[:, F_:], p_out=dp)
+    del gu
+    dwd = wg_stream.mm_tn(dm2, dp)
+    del dp
     dwgu = wg_stream.mm_tn(dgu, z2)
     dz = linear_dgrad(dgu, _cat_rows(wg, wu))
     wg_stream.join()
@@ -72,8 +75,8 @@ class FusedMLPFunction(torch.autograd.Function):
         H = z.shape[-1]
         z2 = z.reshape(-1, H)
         with torch.no_grad():
-            gu, p = mlp_forward(z2, wg, wu, wd, keep=True)
-            dz, dwg, dwu, dwd = mlp_backward(dm.contiguous().view(-1, H), z2, wg, wu, wd, gu, p)
+            dz, dwg, dwu, dwd = mlp_backward(dm.contiguous().view(-1, H), z2, wg, wu, wd,
+                                             mlp_forward(z2, wg, wu, wd, keep=True))
         return dz.view(z.shape), dwg, dwu, dwd
 
 

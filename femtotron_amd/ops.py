@@ -190,18 +190,24 @@ def swiglu_fwd(g: torch.Tensor, u: torch.Tensor, *, out: torch.Tensor | None = N
 
 
 def swiglu_bwd(dp: torch.Tensor, g: torch.Tensor, u: torch.Tensor, dg: torch.Tensor,
-               du: torch.Tensor) -> None:
-    _require_gpu(dp, g, u, dg, du)
-    _same_dtype(g, dp, u, dg, du)
+               du: torch.Tensor, *, p_out: torch.Tensor | None = None) -> None:
+    """dg, du of p = to_dtype(to_dtype(silu(g)) * u); with p_out, also writes p there (bit for
+    bit swiglu_fwd's result).  p_out may be dp itself, which is then overwritten."""
+    _require_gpu(dp, g, u, dg, du, p_out)
+    _same_dtype(g, dp, u, dg, du, p_out)
     ld_gu = _rowmajor(g, "swiglu_bwd.g")
     ld_d = _rowmajor(dg, "swiglu_bwd.dg")
     if _rowmajor(u, "swiglu_bwd.u") != ld_gu or _rowmajor(du, "swiglu_bwd.du") != ld_d:
         raise ValueError("swiglu_bwd: g/u and dg/du must share row strides")
     if not (dp.shape == g.shape == u.shape == dg.shape == du.shape):
         raise ValueError("swiglu_bwd: shape mismatch")
+    if p_out is not None and p_out.shape != g.shape:
+        raise ValueError("swiglu_bwd: p_out shape mismatch")
     rows, cols = g.shape
+    ld_p = _rowmajor(p_out, "swiglu_bwd.p_out") if p_out is not None else 0
     _lib.call("fh_swiglu_bwd", _dtype_code(g), _ptr(dp), _rowmajor(dp, "swiglu_bwd.dp"), _ptr(g),
-              _ptr(u), ld_gu, _ptr(dg), _ptr(du), ld_d, rows, cols, _stream(g))
+              _ptr(u), ld_gu, _ptr(dg), _ptr(du), ld_d, _ptr(p_out), ld_p,
+              rows, cols, _stream(g))
 
 
 def scale(x: torch.Tensor, s: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define FH_ABI_VERSION 4
+#define FH_ABI_VERSION 5
 
 typedef enum fh_dtype {
   FH_BF16 = 0, /* bfloat16 storage, fp32 arithmetic */
@@ -148,11 +148,16 @@ int fh_swiglu_fwd(fh_dtype dt, const void* g, const void* u, int64_t ld_gu,
  *   du = dp * to_dtype(silu(g))
  *   dg = to_dtype(dp*u) * sig(g) * (1 + g*(1 - sig(g)))
  * dg, du share row stride ld_dgu (they may be the two halves of one buffer).
+ * p (optional, may be NULL; row stride ld_p): also writes the forward's
+ * product p = to_dtype(to_dtype(silu(g)) * u), bit for bit what fh_swiglu_fwd
+ * writes, for a recompute that stops before the product (the down
+ * projection's weight gradient reads it after this call).  p may be dp itself
+ * (same ld), which this call then overwrites; no other overlap.
  */
 int fh_swiglu_bwd(fh_dtype dt, const void* dp, int64_t ld_dp, const void* g,
                   const void* u, int64_t ld_gu, void* dg, void* du,
-                  int64_t ld_dgu, int64_t rows, int64_t cols,
-                  hipStream_t stream);
+                  int64_t ld_dgu, void* p, int64_t ld_p, int64_t rows,
+                  int64_t cols, hipStream_t stream);
 
 /* Elementwise residual add out = to_dtype(a + b) over n elements
  * (modeling_llama.py:323).  n % 8 == 0; out may alias a or b. */

@@ -219,6 +219,30 @@ def test_swiglu_fwd_bwd_bf16(rows, cols):
     assert_close(out[:, cols:], uu.grad, 2e-2, 2e-3, "du")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("rows,cols", [(256, 688), (16384, 5632), (3, 8)])
+def test_swiglu_bwd_writes_the_forward_product(rows, cols, dtype):
+    """With p_out the backward also writes swiglu_fwd's product, bit for bit,
+    into a separate buffer or over dp (the layer's form), and dg, du stay the
+    same bits as without it."""
+    ops = _ops()
+    dgu = _dev(randn((rows, 2 * cols), 35).to(dtype))
+    g, u = dgu[:, :cols], dgu[:, cols:]
+    dp = _dev(randn((rows, cols), 36).to(dtype))
+    p_fwd = ops.swiglu_fwd(g, u)
+    plain = torch.empty_like(dgu)
+    ops.swiglu_bwd(dp, g, u, plain[:, :cols], plain[:, cols:])
+    out, p = torch.empty_like(dgu), torch.empty_like(dp)
+    ops.swiglu_bwd(dp, g, u, out[:, :cols], out[:, cols:], p_out=p)
+    assert torch.equal(p, p_fwd)
+    assert torch.equal(out, plain)
+    dp_over = dp.clone()
+    out2 = torch.empty_like(dgu)
+    ops.swiglu_bwd(dp_over, g, u, out2[:, :cols], out2[:, cols:], p_out=dp_over)
+    assert torch.equal(dp_over, p_fwd)
+    assert torch.equal(out2, plain)
+
+
 def test_swiglu_fp32_closed_form():
     ops = _ops()
     g, u, dp = randn((64, 64), 32), randn((64, 64), 33), randn((64, 64), 34)
