@@ -84,6 +84,8 @@ struct GemmArgs {
   // k-steps split evenly over the workgroups
   int full_rounds, tail_tiles;
   int64_t tail_iters;
+  // > 0: the tail in XCD slabs (tail_tiles = slab_chunks * grid / 8; see k_gemm)
+  int slab_chunks;
   GemmRope rope;
 };
 
@@ -451,8 +453,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   if (lid >= g.grid) return;
   if constexpr (EPI == EPI_STREAM) {
     // One call site for both kinds of segment (one copy of the main loop).
+    // Tail: linear, workgroup lid takes tail k-steps [lid I / G, (lid + 1) I / G)
+    // of the tail tiles in order; or in XCD slabs (slab_chunks > 0, the tail a
+    // whole number C of chunks of P = G / 8 consecutive tiles): the P
+    // workgroups of XCD x (lids x P .. x P + P - 1, blockIdx % 8 == x) take
+    // chunk-k-steps [x W / 8, (x + 1) W / 8) of the W = C * ki, workgroup
+    // x P + j tile j of each chunk, so an XCD's workgroups run one chunk's
+    // tiles over the same k-steps together and share their operand blocks in
+    // L2, as in the whole rounds.  A slab is shorter than ki (C < 8): every
+    // tail tile is split.
     const int64_t ki = g.total_steps;
-    const int64_t beg = lid * g.tail_iters / g.grid, end = (lid + 1) * g.tail_iters / g.grid;
+    const int P = g.grid >> 3, xcd = lid / P, j = lid - xcd * P;
+    const int64_t W = static_cast<int64_t>(g.slab_chunks) * ki;
+    const int64_t beg = g.slab_chunks ? xcd * W / 8 : lid * g.tail_iters / g.grid;
+    const int64_t end = g.slab_chunks ? (xcd + 1) * W / 8 : (lid + 1) * g.tail_iters / g.grid;
     int r = 0;
     for (int64_t it = beg;;) {
       int t, k0 = 0, len = g.total_steps;
@@ -460,10 +474,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       if (r < g.full_rounds) {
         t = r++ * g.grid + lid;
       } else if (it < end) {
-        const int tt = static_cast<int>(it / ki);
-        k0 = static_cast<int>(it - tt * ki);
+        const int q = static_cast<int>(it / ki);  // tail tile, or chunk
+        k0 = static_cast<int>(it - q * ki);
         len = static_cast<int>(min(ki - k0, end - it));
-        t = g.full_rounds * g.grid + tt;
+        t = g.full_rounds * g.grid + (g.slab_chunks ? q * P + j : q);
         slot = g.part + (2 * static_cast<int64_t>(lid) + (it == beg ? 0 : 1)) * (kTm * kTn);
         it += len;
       } else {
@@ -485,20 +499,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 }
 
 // Rows blockIdx.y * 16 .. +15 of tail tile blockIdx.x of a stream GEMM: if
-// more than one workgroup's k-range meets the tile, C = bf16(sum of their fp32
-// segments in workgroup = k order) (+ residual, rounded as k_gemm_reduce).
-// Workgroup w covers tail k-steps [w I / G, (w + 1) I / G); the one holding
-// step i is ceil((i + 1) G / I) - 1.  Thread (row group, lane) adds 4 columns
-// of 4 rows, one contributor at a time (its 4 loads in flight together).
+// more than one workgroup's k-range meets the tile (always, with XCD slabs),
+// C = bf16(sum of their fp32 segments in k order) (+ residual, rounded as
+// k_gemm_reduce).  A holder's first segment is in its slot 0, a second in
+// slot 1.  Thread (row group, lane) adds 4 columns of 4 rows, one contributor
+// at a time (its 4 loads in flight together).
 constexpr int kFixRows = 16;
 
 __global__ __launch_bounds__(256) void k_gemm_fixup(GemmArgs g) {
-  const int64_t ki = g.total_steps, I = g.tail_iters, G = g.grid;
-  const int64_t lo = static_cast<int64_t>(blockIdx.x) * ki;
-  auto wg_of = [&](int64_t i) { return static_cast<int>(((i + 1) * G + I - 1) / I - 1); };
-  auto start_of = [&](int64_t w) { return w * I / G; };
+  // Holders of the tile's k-steps: workgroups w (linear) or the XCDs w of the
+  // tile's chunk c, whose workgroup w P + j holds tile j of it (slabs); in
+  // both, holder w covers [w I / N, (w + 1) I / N) of I steps over N holders,
+  // so the one holding step i is ceil((i + 1) N / I) - 1.
+  const int64_t ki = g.total_steps, G = g.grid, P = G >> 3;
+  const bool slab = g.slab_chunks > 0;
+  const int64_t I = slab ? g.slab_chunks * ki : g.tail_iters, N = slab ? 8 : G;
+  const int64_t c = slab ? blockIdx.x / P : blockIdx.x, jj = slab ? blockIdx.x - c * P : 0;
+  const int64_t lo = c * ki;
+  auto wg_of = [&](int64_t i) { return static_cast<int>(((i + 1) * N + I - 1) / I - 1); };
+  auto start_of = [&](int64_t w) { return w * I / N; };
   const int w0 = wg_of(lo), w1 = wg_of(lo + ki - 1);
-  if (w0 == w1) return;  // one workgroup stored the whole tile
+  if (w0 == w1 && !slab) return;  // one workgroup stored the whole tile
   int m0, n0;
   tile_origin(g, g.full_rounds * g.grid + static_cast<int>(blockIdx.x), m0, n0);
   const int lane = threadIdx.x & 63, r0 = blockIdx.y * kFixRows + (threadIdx.x >> 6);
@@ -509,7 +530,8 @@ __global__ __launch_bounds__(256) void k_gemm_fixup(GemmArgs g) {
   for (int w = w0; w <= w1; ++w) {
     const int64_t sw = start_of(w);
     if (sw == start_of(w + 1)) continue;  // empty range: wrote nothing
-    const float* src = g.part + (2 * static_cast<int64_t>(w) + (sw >= lo ? 0 : 1)) * (kTm * kTn) + 4 * lane;
+    const int64_t holder = slab ? w * P + jj : w;
+    const float* src = g.part + (2 * holder + (sw >= lo ? 0 : 1)) * (kTm * kTn) + 4 * lane;
     float4 v[kFixRows / 4];
 #pragma unroll
     for (int q = 0; q < kFixRows / 4; ++q) v[q] = *reinterpret_cast<const float4*>(src + (r0 + 4 * q) * kTn);
@@ -724,6 +746,7 @@ int gemm_run(int op, GemmArgs& g, int slices, bool stream_form, void* workspace,
     g.tail_tiles = g.tiles - g.full_rounds * sg;
     g.tail_iters = static_cast<int64_t>(g.tail_tiles) * g.total_steps;
     g.steps_per_slice = g.total_steps;
+    g.slab_chunks = g.tail_tiles % (sg / 8) == 0 ? g.tail_tiles / (sg / 8) : 0;
     switch (op) {
       case FH_GEMM_NT: launch<false, false>(g, sg, false, false, stream); break;
       case FH_GEMM_NN: launch<false, true>(g, sg, false, false, stream); break;

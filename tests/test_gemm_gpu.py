@@ -93,12 +93,15 @@ def test_gemm_ragged_strided_split(op, m, n, k, pad):
     assert torch.equal(c, ops.gemm(op, a, b))
 
 
-@pytest.mark.parametrize("m,n,k,pad", [(10232, 2040, 16384, 0), (4104, 4088, 8192, 8), (6400, 3000, 8192, 0)])
+@pytest.mark.parametrize("m,n,k,pad", [(10232, 2040, 16384, 0), (4104, 4088, 8192, 8), (6400, 3000, 8192, 0),
+                                       (12280, 2040, 16384, 8)])
 def test_stream_form_matches_and_is_deterministic(m, n, k, pad):
     # Weight-gradient shapes whose tiles leave the last round of CUs partly
     # idle: the stream form spreads the k-steps evenly over the CUs and adds
     # the split tiles' fp32 segments in k order.  Its workspace is the segment
-    # slots (two 256 x 256 fp32 tiles per CU).
+    # slots (two 256 x 256 fp32 tiles per CU).  A tail of whole chunks of
+    # CUs / 8 tiles (64 and 128 tail tiles here) runs in XCD slabs, the others
+    # (16 and 44) linearly.
     cus = torch.cuda.get_device_properties(0).multi_processor_count // 8 * 8
     assert _lib.lib().fh_gemm_bf16_workspace_size(_lib.FH_GEMM_TN, m, n, k) == 2 * cus * 256 * 256 * 4
     g = torch.Generator(device=DEV).manual_seed(m + n + k)
@@ -108,10 +111,11 @@ def test_stream_form_matches_and_is_deterministic(m, n, k, pad):
     assert torch.equal(c, ops.gemm("tn", a, b))
 
 
-def test_stream_form_residual_epilogue_rounds_like_the_unfused_add():
+@pytest.mark.parametrize("m,n,k", [(4104, 4088, 8192), (10240, 2048, 4096)])
+def test_stream_form_residual_epilogue_rounds_like_the_unfused_add(m, n, k):
     """The stream form's residual epilogue (whole tiles in the GEMM, split tiles
-    in the fixup) gives to_bf16(R + to_bf16(A.B)) bit for bit, also in place."""
-    m, n, k = 4104, 4088, 8192
+    in the fixup; linear tail and XCD slabs) gives to_bf16(R + to_bf16(A.B))
+    bit for bit, also in place."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count // 8 * 8
     assert _lib.lib().fh_gemm_bf16_workspace_size(_lib.FH_GEMM_TN, m, n, k) == 2 * cus * 256 * 256 * 4
     g = torch.Generator(device=DEV).manual_seed(17)
