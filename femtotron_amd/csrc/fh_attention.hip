@@ -349,12 +349,14 @@ __device__ __forceinline__ void fwd_block(const char* K, const char* V, const bf
   for (int u = 0; u < QT; ++u) l[u] += lsum[u];
 }
 
+// q and qout may be the same buffer (the rotated q written back in place), so
+// neither is __restrict__: a lane stores only elements it has loaded.
 template <int HD, int HPB>
 __global__ __launch_bounds__(256 * HPB) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_fwd(
-    const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
+    const uint16_t* q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
     const uint16_t* __restrict__ v, int64_t ldv, uint16_t* __restrict__ o, int64_t ldo,
     float* __restrict__ lse, int S, int nh, int group, float scale_log2, RopeRows<uint16_t> rope,
-    uint16_t* __restrict__ qout, int64_t ldqo) {
+    uint16_t* qout, int64_t ldqo) {
   constexpr int QT = FwdTiles<HD>::QT;
   constexpr int BM = 4 * 32 * QT, BN = 64, NS = HD / 16, ND = HD / 32, TILE = BN * 2 * HD;
   __shared__ __align__(16) char sk0[TILE], sk1[TILE], sv0[TILE], sv1[TILE];
@@ -1004,10 +1006,10 @@ __device__ __forceinline__ void store_row_f32(float* out, const float (&acc)[HD]
 }
 template <int HD>
 __global__ __launch_bounds__(128) void k_attn_fwd_f32(
-    const float* __restrict__ q, int64_t ldq, const float* __restrict__ k, int64_t ldk,
+    const float* q, int64_t ldq, const float* __restrict__ k, int64_t ldk,
     const float* __restrict__ v, int64_t ldv, float* __restrict__ o, int64_t ldo,
     float* __restrict__ lse, int S, int nh, int group, float scale, int64_t rows, RopeRows<float> rope,
-    float* __restrict__ qout, int64_t ldqo) {
+    float* qout, int64_t ldqo) {  // q and qout may alias (in-place rotated q)
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= rows) return;  // rows = B*nh*S, idx = (b*nh + h)*S + s
   const int s = static_cast<int>(idx % S);

@@ -46,6 +46,7 @@
 #include "fh_mfma.hpp"
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 namespace fh {
@@ -593,17 +594,20 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float* __restrict__ p
   *reinterpret_cast<uint2*>(c + row * ldc + col) = make_uint2(pk_bf16(s.x, s.y), pk_bf16(s.z, s.w));
 }
 
-// Compute units of the current device (one workgroup fits per CU).
+// Compute units of the current device (one workgroup fits per CU), looked up
+// once per device (std::call_once, so concurrent first calls are safe).
 int device_cus() {
-  static int cached[64] = {0};
+  constexpr int kMaxDevices = 64;
+  static std::once_flag once[kMaxDevices];
+  static int cached[kMaxDevices] = {};
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  std::call_once(once[dev], [dev]() {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
       cus = 256;
     cached[dev] = cus;
-  }
+  });
   return cached[dev];
 }
 

@@ -533,8 +533,8 @@ extern "C" int fh_rmsnorm_bwd(fh_dtype dt, const void* dy, const void* x, const 
   }
   FH_REQUIRE(dy && x && dx && workspace, "rmsnorm_bwd: null pointer");
   FH_REQUIRE(aligned16(dy) && aligned16(x) && aligned16(w) && aligned16(dx) &&
-                 (dres == nullptr || aligned16(dres)),
-             "rmsnorm_bwd: pointers must be 16-byte aligned");
+                 (dres == nullptr || aligned16(dres)) && aligned16(workspace),
+             "rmsnorm_bwd: pointers (workspace included) must be 16-byte aligned");
   float* part = static_cast<float*>(workspace);
   dispatch_nv(c, [&](auto nv) {
     if (dt == FH_BF16) launch_bwd<uint16_t, nv()>(dy, x, w, rstd, dres, dx, dw, part, rows, c, eps, stream);

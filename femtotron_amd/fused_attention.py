@@ -27,7 +27,9 @@ dq/dk stores) -> q/k/v projection.
 A call the kernels do not cover runs the module's own forward: off a HIP
 device, another dtype, autocast, an attention mask, a KV cache, attention
 dropout while training, projection biases or tensor-parallel size > 1, hooks
-on the projections, or an attention implementation other than sdpa/eager.
+on the projections, or an attention implementation other than sdpa (HF's eager
+attention, and an unset implementation, attend in both directions when no mask
+is given, where the kernels are causal).
 Under full activation checkpointing the fused decoder layer never calls the
 attention module, so the two compose.
 """
@@ -39,7 +41,7 @@ import types
 import torch
 
 from . import _lib, ops
-from .fused_checkpoint import _aligned, _check_params, _linear_weight
+from .fused_checkpoint import _aligned, _causal_attention_reason, _check_params, _linear_weight
 from .fused_layer import LayerShape, _WgradStream, _cat_rows, attn_bwd, qkv_attention
 from .projections import linear, linear_dgrad
 
@@ -128,9 +130,9 @@ def _plan(attn, y, position_embeddings, attention_mask, past_key_values, kwargs)
         return "explicit attention mask"
     if past_key_values is not None:
         return "KV cache"
-    cfg = getattr(attn, "config", None)
-    if cfg is None or getattr(cfg, "_attn_implementation", "sdpa") not in ("sdpa", "eager", None):
-        return "attention implementation other than sdpa/eager"
+    reason = _causal_attention_reason(attn)
+    if reason:
+        return reason
     if attn.training and float(getattr(attn, "attention_dropout", 0.0) or 0.0) > 0.0:
         return "attention dropout"
     if _projection_hooks(attn):

@@ -96,6 +96,29 @@ def _check_input(args: tuple):
     return x
 
 
+def _causal_attention_reason(attn: Any) -> str | None:
+    """None if the stock attention module computes causal attention when it is
+    called without a mask (the only calls that reach the kernels), else why not.
+
+    HF picks the attention function by ``config._attn_implementation``
+    (modeling_llama.py:258-260): "sdpa" is causal without a mask as long as the
+    module's ``is_causal`` holds (integrations/sdpa_attention.py:126-142), but
+    "eager", and an unset implementation (which ``get_interface`` resolves to
+    eager), apply no mask at all without one (modeling_llama.py:202-204): every
+    query attends to every key.  The kernels are causal, so those fall back."""
+    cfg = getattr(attn, "config", None)
+    if cfg is None:
+        return "attention has no config"
+    impl = getattr(cfg, "_attn_implementation", None)
+    if impl != "sdpa":
+        if impl in ("eager", None):
+            return f"attention implementation {impl!r} without a mask is not causal"
+        return f"attention implementation {impl!r}"
+    if not getattr(attn, "is_causal", True):
+        return "attention module is not causal"
+    return None
+
+
 def _check_params(x: torch.Tensor, weights) -> str | None:
     for t in weights:
         if t.device != x.device or t.dtype != x.dtype or not t.is_contiguous():
@@ -186,12 +209,10 @@ def _plan_layer(module: Any, x: torch.Tensor, kwargs: dict):
     ln2 = getattr(module, "post_attention_layernorm", None)
     if attn is None or mlp is None or ln1 is None or ln2 is None:
         return "not a Llama decoder layer"
-    cfg = getattr(attn, "config", None)
-    if cfg is None:
-        return "attention has no config"
-    if getattr(cfg, "_attn_implementation", "sdpa") not in ("sdpa", "eager", None):
-        return f"attention implementation {cfg._attn_implementation!r}"
-    if getattr(cfg, "hidden_act", "silu") != "silu":
+    reason = _causal_attention_reason(attn)
+    if reason:
+        return reason
+    if getattr(attn.config, "hidden_act", "silu") != "silu":
         return "MLP activation is not SiLU"
     if module.training and float(getattr(attn, "attention_dropout", 0.0) or 0.0) > 0.0:
         return "attention dropout"

@@ -87,14 +87,23 @@ def _library_shapes() -> dict[str, set]:
     return _table
 
 
-def _use_hand(op: str, a: torch.Tensor, b: torch.Tensor, table: str | None = None) -> bool:
+def _choose_hand(op: str, a: torch.Tensor, b: torch.Tensor, table: str | None = None) -> bool:
     pol = _policy[0]
     use = pol != "library" and ops.gemm_supported(op, a, b)
     if use and pol == "auto":
         use = ops.gemm_dims(op, a, b) not in _library_shapes()[table or op]
-    with _lock:
-        _counts["hand" if use else "library"] += 1
     return use
+
+
+def _count(hand: bool) -> bool:
+    """Count one GEMM as hand-written or library; returns `hand`."""
+    with _lock:
+        _counts["hand" if hand else "library"] += 1
+    return hand
+
+
+def _use_hand(op: str, a: torch.Tensor, b: torch.Tensor) -> bool:
+    return _count(_choose_hand(op, a, b))
 
 
 def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
@@ -112,20 +121,25 @@ def linear_rope(x: torch.Tensor, w: torch.Tensor, n_rot_heads: int, head_dim: in
     one without the rotation), the rotation is a separate pass that leaves heads
     0..defer_heads-1 (q) unrotated for the caller to rotate as it reads them
     (the attention forward's q load); all rotated is then False."""
-    if head_dim in (32, 64, 128) and _use_hand("nt", x, w, "nt_rope"):
+    if head_dim in (32, 64, 128) and _choose_hand("nt", x, w, "nt_rope"):
+        _count(True)
         return ops.gemm_rope(x, w, n_rot_heads, head_dim, seq_len, cos, sin), True
-    y = linear(x, w)
+    y = linear(x, w)  # counts this GEMM once
     if n_rot_heads > defer_heads:
         ops.rope_fwd_(y[:, defer_heads * head_dim:], n_rot_heads - defer_heads, head_dim, seq_len, cos, sin)
     return y, defer_heads == 0
 
 
 def linear_residual(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
-    """residual + to_dtype(x @ w^T), written into `residual`'s memory."""
-    if _use_hand("nt", x, w) and residual.is_contiguous():
+    """residual + to_dtype(x @ w^T), written into `residual`'s memory (the
+    hand-written GEMM's residual epilogue; otherwise the library GEMM followed
+    by fh_add into `residual`)."""
+    if _count(residual.is_contiguous() and _choose_hand("nt", x, w)):
         return ops.gemm("nt", x, w, residual=residual, out=residual)
     m = torch.mm(x, w.t())
-    return ops.add(residual, m, out=m)
+    if not residual.is_contiguous():
+        return residual.add_(m)  # one fp32 add, one rounding, as fh_add
+    return ops.add(residual, m, out=residual)
 
 
 def linear_dgrad(dy: torch.Tensor, w: torch.Tensor) -> torch.Tensor:

@@ -20,8 +20,13 @@
  *     and never synchronise the host.
  *   - Return value: FH_OK (0) or an FH_ERR_* code; fh_last_error() then holds
  *     a message for the calling thread.  Nothing aborts the process.
- *   - Thread-safe: the library holds no mutable global state apart from the
- *     per-thread error string.
+ *   - Thread-safe: the library's own global state is the per-thread error
+ *     string, per-device values looked up once under std::call_once (compute
+ *     unit count, the scratch address below), and one device buffer: the
+ *     file-scope scratch array of fh_rmsnorm_bwd_noalloc, shared by every
+ *     call of that entry point on a device, so calls of it that overlap on
+ *     one device (two host threads, or two streams) race on its contents.
+ *     Every other entry point works only on the caller's buffers.
  */
 #ifndef FEMTOHIP_H_
 #define FEMTOHIP_H_
@@ -84,7 +89,8 @@ size_t fh_rmsnorm_bwd_workspace_size(int64_t rows, int64_t cols);
  *   dx  = to_dtype(r * (dn - n * mean(dn * n)) + dres)   (n = x*r, r = rstd)
  *   dw  = sum_rows dy * to_dtype(n)
  * rstd nullable (recomputed from x and eps); dres nullable (no residual).
- * dw: [cols] in dtype dt, overwritten.  workspace: see above.
+ * dw: [cols] in dtype dt, overwritten.  workspace: see above, 16-byte
+ * aligned like every other pointer (the partial rows are read as float4).
  */
 int fh_rmsnorm_bwd(fh_dtype dt, const void* dy, const void* x, const void* w,
                    const float* rstd, const void* dres, void* dx, void* dw,

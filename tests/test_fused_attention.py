@@ -54,3 +54,22 @@ def test_cpu_call_runs_the_modules_own_forward():
     assert torch.equal(loss0, loss1)
     assert all(torch.equal(g0[n], g1[n]) for n in g0)
     unfuse_attention(model)
+
+
+def test_only_causal_sdpa_attention_is_fusable():
+    """The kernels are causal.  HF's eager attention, and an unset
+    implementation (resolved to eager), attend in both directions when called
+    without a mask (modeling_llama.py:202-204), so both planners refuse them;
+    sdpa without a mask is causal while the module's is_causal holds."""
+    from femtotron_amd.fused_checkpoint import _causal_attention_reason
+
+    def attn(impl):
+        return hf.LlamaAttention(llama_config(CFG1, layers=1, attn=impl), layer_idx=0)
+
+    assert _causal_attention_reason(attn("sdpa")) is None
+    for impl in ("eager", None):
+        assert "not causal" in _causal_attention_reason(attn(impl))
+    assert "flash" in _causal_attention_reason(attn("flash_attention_2"))
+    a = attn("sdpa")
+    a.is_causal = False
+    assert _causal_attention_reason(a) == "attention module is not causal"

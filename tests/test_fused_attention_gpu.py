@@ -64,7 +64,8 @@ def test_fused_attention_cfg1_fp32_vs_cpu_oracle():
         assert rel_err(grads[n], t.grad) < 1e-5, f"{n}: rel {rel_err(grads[n], t.grad):.3e}"
 
 
-@pytest.mark.parametrize("name,c,B,S", [("tinyllama", CFG3, 2, 1024), ("llama3-slice", CFG4, 1, 1024)])
+@pytest.mark.parametrize("name,c,B,S", [("tinyllama", CFG3, 2, 1024), ("llama3-slice", CFG4, 1, 1024),
+                                         ("llama3-slice-full-length", CFG4, 1, 8192)])
 def test_fused_attention_bf16_matches_stock_selective(name, c, B, S):
     """2-layer bf16 model, selective policy: fused MLPs/norms/attention vs the
     reference path (stock HF modules, torch.utils.checkpoint).  Loss within

@@ -93,39 +93,46 @@ def test_gemm_ragged_strided_split(op, m, n, k, pad):
     assert torch.equal(c, ops.gemm(op, a, b))
 
 
+_OPCODE = {"nt": _lib.FH_GEMM_NT, "nn": _lib.FH_GEMM_NN, "tn": _lib.FH_GEMM_TN}
+
+
+@pytest.mark.parametrize("op", ["nt", "nn", "tn"])
 @pytest.mark.parametrize("m,n,k,pad", [(10232, 2040, 16384, 0), (4104, 4088, 8192, 8), (6400, 3000, 8192, 0),
-                                       (12280, 2040, 16384, 8)])
-def test_stream_form_matches_and_is_deterministic(m, n, k, pad):
-    # Weight-gradient shapes whose tiles leave the last round of CUs partly
-    # idle: the stream form spreads the k-steps evenly over the CUs and adds
-    # the split tiles' fp32 segments in k order.  Its workspace is the segment
-    # slots (two 256 x 256 fp32 tiles per CU).  A tail of whole chunks of
-    # CUs / 8 tiles (64 and 128 tail tiles here) runs in XCD slabs, the others
-    # (16 and 44) linearly.
+                                       (12280, 2040, 16384, 8), (12288, 2048, 11264, 0)])
+def test_stream_form_matches_and_is_deterministic(op, m, n, k, pad):
+    # Shapes whose tiles leave the last round of CUs partly idle: the stream
+    # form spreads the k-steps evenly over the CUs and adds the split tiles'
+    # fp32 segments in k order.  Its workspace is the segment slots (two
+    # 256 x 256 fp32 tiles per CU).  A tail of whole chunks of CUs / 8 tiles
+    # (64, 128 and 96 tail tiles here) runs in XCD slabs, the others (16 and
+    # 44) linearly.  The plan depends on (m, n, k) only, so every layout takes
+    # it: TN (weight gradients), NN (input gradients such as the gate/up one
+    # at 12288 tokens) and NT.
     cus = torch.cuda.get_device_properties(0).multi_processor_count // 8 * 8
-    assert _lib.lib().fh_gemm_bf16_workspace_size(_lib.FH_GEMM_TN, m, n, k) == 2 * cus * 256 * 256 * 4
+    assert _lib.lib().fh_gemm_bf16_workspace_size(_OPCODE[op], m, n, k) == 2 * cus * 256 * 256 * 4
     g = torch.Generator(device=DEV).manual_seed(m + n + k)
-    a, b = _operands("tn", m, n, k, g, pad)
-    c = ops.gemm("tn", a, b)
-    _check("tn", a, b, c, exact=True)
-    assert torch.equal(c, ops.gemm("tn", a, b))
+    a, b = _operands(op, m, n, k, g, pad)
+    c = ops.gemm(op, a, b)
+    _check(op, a, b, c, exact=True)
+    assert torch.equal(c, ops.gemm(op, a, b))
 
 
+@pytest.mark.parametrize("op", ["nt", "nn", "tn"])
 @pytest.mark.parametrize("m,n,k", [(4104, 4088, 8192), (10240, 2048, 4096)])
-def test_stream_form_residual_epilogue_rounds_like_the_unfused_add(m, n, k):
+def test_stream_form_residual_epilogue_rounds_like_the_unfused_add(op, m, n, k):
     """The stream form's residual epilogue (whole tiles in the GEMM, split tiles
     in the fixup; linear tail and XCD slabs) gives to_bf16(R + to_bf16(A.B))
     bit for bit, also in place."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count // 8 * 8
-    assert _lib.lib().fh_gemm_bf16_workspace_size(_lib.FH_GEMM_TN, m, n, k) == 2 * cus * 256 * 256 * 4
+    assert _lib.lib().fh_gemm_bf16_workspace_size(_OPCODE[op], m, n, k) == 2 * cus * 256 * 256 * 4
     g = torch.Generator(device=DEV).manual_seed(17)
-    a, b = _operands("tn", m, n, k, g)
+    a, b = _operands(op, m, n, k, g)
     r = torch.randn(m, n, device=DEV, generator=g).to(BF)
-    fused = ops.gemm("tn", a, b, residual=r)
-    unfused = (r.float() + ops.gemm("tn", a, b).float()).to(BF)
+    fused = ops.gemm(op, a, b, residual=r)
+    unfused = (r.float() + ops.gemm(op, a, b).float()).to(BF)
     assert torch.equal(fused, unfused)
     inplace = r.clone()
-    ops.gemm("tn", a, b, residual=inplace, out=inplace)
+    ops.gemm(op, a, b, residual=inplace, out=inplace)
     assert torch.equal(inplace, fused)
 
 

@@ -293,3 +293,21 @@ def test_invalid_arguments_raise():
     with pytest.raises(FemtoHipError, match="head_dim"):
         ops.rope_fwd_(q, 2, 24, 4, torch.zeros(1, 4, 24, dtype=torch.bfloat16, device=DEV),
                       torch.zeros(1, 4, 24, dtype=torch.bfloat16, device=DEV))
+
+
+def test_rmsnorm_bwd_rejects_a_misaligned_workspace():
+    """The backward reads its fp32 partial rows as float4: a workspace that is
+    not 16-byte aligned is refused with a message, and nothing is launched."""
+    from femtotron_amd import _lib
+    L = _lib.lib()
+    rows, cols = 64, 256
+    bf = torch.bfloat16
+    dy, x, dx = (torch.zeros(rows, cols, dtype=bf, device=DEV) for _ in range(3))
+    w = torch.ones(cols, dtype=bf, device=DEV)
+    dw = torch.zeros(cols, dtype=bf, device=DEV)
+    ws = torch.zeros(L.fh_rmsnorm_bwd_workspace_size(rows, cols) // 4 + 4, dtype=torch.float32, device=DEV)
+    args = (_lib.FH_BF16, dy.data_ptr(), x.data_ptr(), w.data_ptr(), None, None, dx.data_ptr(), dw.data_ptr())
+    assert L.fh_rmsnorm_bwd(*args, ws.data_ptr() + 4, rows, cols, 1e-5, None) == 1
+    assert b"16-byte aligned" in L.fh_last_error()
+    assert L.fh_rmsnorm_bwd(*args, ws.data_ptr(), rows, cols, 1e-5, None) == 0
+    torch.cuda.synchronize()

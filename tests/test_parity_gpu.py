@@ -88,6 +88,72 @@ def test_full_shape_elementwise_accuracy_vs_exact(name, c, B, S):
     print(f"\n[{name}] fraction outside rtol 2e-2/atol 2e-3 / max err rel to peak:\n  " + "\n  ".join(report))
 
 
+def _run_layer_selective(c, B, S, *, fused: bool, seed=42):
+    """One bf16 decoder layer under the selective policy ("llama_mlp_and_norms":
+    both norms and the MLP checkpointed, attention outside the checkpoints;
+    femtotron/scripts/presets.py:45-62, ckpt_policy.py:70-87).  fused: the
+    checkpointed modules through fused_checkpoint and the attention through
+    fuse_attention; else the reference path (torch.utils.checkpoint, stock
+    HF attention)."""
+    from femtotron_amd import dispatch_counts, fuse_attention, fused_checkpoint, reset_dispatch_counts
+    from femtotron_amd.fused_attention import attention_dispatch_counts, reset_attention_dispatch_counts
+    from femtotron_amd.scripts.presets import get_ac_policy
+    from femtotron_amd.training import apply_activation_checkpointing
+    from torch.utils.checkpoint import checkpoint
+
+    layer = hf.LlamaDecoderLayer(llama_config(c, layers=1), layer_idx=0)
+    load_into_hf_layer(layer, layer_weights(c, seed=seed, norm_mean=1.0))
+    layer = layer.to(DEV, torch.bfloat16)
+    holder = torch.nn.Module()
+    holder.layer = layer
+    assert apply_activation_checkpointing(holder, get_ac_policy("llama_mlp_and_norms"),
+                                          checkpoint_fn=fused_checkpoint if fused else checkpoint) == 3
+    if fused:
+        assert fuse_attention(holder) == 1
+    hd = c["hidden"] // c["heads"]
+    cos, sin = ot.rope_cos_sin(S, hd, c["theta"], torch.bfloat16, device=DEV)
+    x = randn((B, S, c["hidden"]), seed + 1).to(DEV, torch.bfloat16).requires_grad_(True)
+    dy = randn((B, S, c["hidden"]), seed + 2).to(DEV, torch.bfloat16)
+    reset_dispatch_counts()
+    reset_attention_dispatch_counts()
+    out = layer(x, attention_mask=None, position_embeddings=(cos, sin),
+                position_ids=torch.arange(S, device=DEV)[None], past_key_values=None, use_cache=False)
+    out = out[0] if isinstance(out, tuple) else out
+    out.backward(dy)
+    if fused:
+        assert dispatch_counts() == {"fused": 3, "fallback": 0}
+        assert attention_dispatch_counts() == {"fused": 1, "fallback": 0}
+    a, m = layer.self_attn, layer.mlp.inner_module
+    grads = {"wq": a.q_proj.weight.grad, "wk": a.k_proj.weight.grad, "wv": a.v_proj.weight.grad,
+             "wo": a.o_proj.weight.grad, "wg": m.gate_proj.weight.grad, "wu": m.up_proj.weight.grad,
+             "wd": m.down_proj.weight.grad, "w1": layer.input_layernorm.inner_module.weight.grad,
+             "w2": layer.post_attention_layernorm.inner_module.weight.grad}
+    return out.detach(), x.grad, grads
+
+
+def test_full_length_selective_cfg4_elementwise_accuracy_vs_exact():
+    """BASELINE config 4 at its own length (1 x 8192) under selective
+    checkpointing with the fused attention: element-wise accuracy against the
+    exact fp32 layer, by the same measure as the full-AC test above."""
+    c, B, S = CFG4, 1, 8192
+    fused = _run_layer_selective(c, B, S, fused=True)
+    torch.cuda.synchronize()
+    stock = _run_layer_selective(c, B, S, fused=False)
+    torch.cuda.synchronize()
+    exact = _exact_layer(c, B, S)
+    pairs = [("out", fused[0], stock[0], exact[0]), ("dx", fused[1], stock[1], exact[1])]
+    pairs += [(f"d{k}", fused[2][k], stock[2][k], exact[2][k]) for k in ot.LAYER_KEYS]
+    report = []
+    for tag, f_, s_, e_ in pairs:
+        ff, fr = _outside(f_, e_)
+        sf, sr = _outside(s_, e_)
+        report.append(f"{tag}: fused {ff:.2e} / {fr:.2e}, reference {sf:.2e} / {sr:.2e}")
+        assert ff <= 1.25 * sf + 1e-4, f"selective {tag}: fraction outside {ff:.3e} vs reference {sf:.3e}"
+        assert fr <= 1.25 * sr + 1e-3, f"selective {tag}: max rel err {fr:.3e} vs reference {sr:.3e}"
+    print("\n[cfg4 selective] fraction outside rtol 2e-2/atol 2e-3 / max err rel to peak:\n  "
+          + "\n  ".join(report))
+
+
 def _stack(c, n, seed, packed):
     from femtotron_amd import pack_layer_weights
     cfg = llama_config(c, layers=n)
