@@ -11,26 +11,28 @@
 // All operands are row-major with a leading dimension (elements).
 //
 // Block tile 256 (m) x 256 (n), stages of 64 k, four waves (one per SIMD),
-// each owning a 128 x 128 part of the tile in 16 AGPR accumulators of
-// v_mfma_f32_32x32x16_bf16.  Operands go straight from global memory into LDS
+// each owning a 128 x 128 part of the tile in 64 AGPR accumulators of
+// v_mfma_f32_16x16x32_bf16 (under the power limit this MFMA sustains a ~15%
+// higher clock than 32x32x16 at the same work per cycle: 1.93 against 1.75
+// PFLOP/s in a stream of independent MFMAs).  Operands go straight from global memory into LDS
 // (global_load_lds_dwordx4, 1 KB per instruction; every load covers whole
 // 128-byte lines, as half-line requests cost a full line's L2 and DRAM
 // throughput).  LDS holds a ring of five operand slots (A or B of one stage,
 // 32 KB each: 160 KB), so the loads of stage x+2 can start while stage x is
-// multiplied and are spread over its 64 MFMAs: the load instructions issue at
+// multiplied and are spread over its 128 MFMAs: the load instructions issue at
 // ~1 KB per 16 cycles per CU, and a burst of them right after a barrier would
-// hold up the MFMAs behind it.  Fragments are read from LDS one k16 step ahead
+// hold up the MFMAs behind it.  Fragments are read from LDS one k32 step ahead
 // of the MFMAs that use them.  Tiles are XOR-swizzled so that both read
 // patterns are free of bank conflicts:
 //   * an operand with K contiguous ("KC": A of NT/NN, B of NT) is stored as
-//     its [256 x 64] tile; a fragment is one ds_read_b128 per lane (row i%32,
-//     k 8*(i/32)..+7);
+//     its [256 x 64] tile; a fragment is one ds_read_b128 per lane (row i%16,
+//     k 8*(i/16)..+7 of the k32 step);
 //   * an operand with K as the outer index ("KO": B of NN, both of TN) is
 //     stored as four [64 k x 64] sub-tiles; a fragment is two
 //     ds_read_b64_tr_b16 transposing reads that deliver the same natural K
 //     order, so any two operands can be paired.
-// The MFMA is issued as (B fragment, A fragment), so accumulator rows run
-// along n (C's contiguous index).  The finished tile goes through LDS so that
+// The MFMA is issued as (B fragment, A fragment), so each lane's four
+// accumulator values are consecutive along n (C's contiguous index).  The finished tile goes through LDS so that
 // every global store writes whole rows.
 //
 // Few output tiles (a weight gradient of 2048 x 2048 has 64) would leave most
@@ -104,26 +106,48 @@ __device__ __forceinline__ uint4 rope_fwd_chunk(uint4 x, uint4 p, uint4 c, uint4
   return Elem<uint16_t>::pack(o);
 }
 
-// Lane offset of a transposing fragment read with K in natural order: lane i
-// gets rows 8*(i/32) + plus4 + 0..3 of column i%32 of a 32-wide column block
-// of a swizzled [16 x 64] row group (128-byte rows, swz<64>).  The 16 lanes of
-// each quarter-wave read one 4-row x 16-column block, lane L 8 bytes of row L/4.
-__device__ __forceinline__ int lane_off_tr(int lane, int plus4) {
-  const int hl = lane >> 5, L = lane & 15, mh = (lane >> 4) & 1;
-  const int r = 8 * hl + (L >> 2) + plus4;
-  const int cb = 2 * mh + ((L & 3) >> 1);
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// As inline asm with the accumulator tied in place ("+a"): through the
+// builtin, the register allocator gave 64 four-register accumulators
+// different source and destination tuples and shuffled them through VGPRs
+// (~130 extra moves per stage).  The compiler's hazard checks do not see an
+// asm MFMA: the kernel pads the two hazards this code has itself (an
+// accumulator zeroed just before its first MFMA; MFMA results read right
+// after the last one) with s_nop.
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  return c;
+}
+
+// 16x16x32 KC fragment: lane i reads row i%16, k chunk i/16 of a k32 step
+// (chunk 4 ks + i/16 of the row's eight; rows o..o+15 of the [256 x 64] tile,
+// o a multiple of 16, share swz<64>, which depends on row bits 1..3 only).
+__device__ __forceinline__ int lane_off_kc16(int lane) {
+  const int r = lane & 15;
+  return r * 128 + (((lane >> 4) ^ swz<64>(r)) << 4);
+}
+
+__device__ __forceinline__ bf16x8 frag_kc16(const char* tile, int a_off, int o, int ks) {
+  return *reinterpret_cast<const bf16x8*>(tile + o * 128 + (a_off ^ (64 * ks)));
+}
+
+// 16x16x32 KO fragment lane offset: quarter-wave q = i/16 reads k rows
+// 8 q + plus4 + 0..3 of a 16-column block (lane L = i%16: 8 bytes of row L/4,
+// columns 4 (L%4) .. +3), so that lane i gets column i%16, k 8 q .. 8 q + 7
+// over the two reads, as a KC fragment holds them.
+__device__ __forceinline__ int lane_off_tr16(int lane, int plus4) {
+  const int q = lane >> 4, L = lane & 15;
+  const int r = 8 * q + (L >> 2) + plus4;
+  const int cb = (L & 3) >> 1;
   return r * 128 + ((cb ^ swz<64>(r)) << 4) + 8 * (L & 1);
 }
 
-// KC fragment: rows o..o+31 of the [256 x 64] tile, k 16*ks + 8*(lane/32) .. +7.
-__device__ __forceinline__ bf16x8 frag_kc(const char* tile, int a_off, int o, int ks) {
-  return *reinterpret_cast<const bf16x8*>(tile + o * 128 + (a_off ^ (32 * ks)));
-}
-
-// KO fragment: columns o..o+31 of the four [64 k x 64] sub-tiles, same k.
-__device__ __forceinline__ bf16x8 frag_ko(const char* tile, int t0, int t4, int o, int ks) {
-  const char* t = tile + (o >> 6) * kSubBytes + ks * 16 * 128;
-  const int x = 64 * ((o >> 5) & 1);
+// KO fragment: columns o..o+15 (o a multiple of 16) of the four [64 k x 64]
+// sub-tiles, k rows 32 ks .. 32 ks + 31.
+__device__ __forceinline__ bf16x8 frag_ko16(const char* tile, int t0, int t4, int o, int ks) {
+  const char* t = tile + (o >> 6) * kSubBytes + ks * 32 * 128;
+  const int x = 32 * ((o >> 4) & 3);  // the block's first chunk, 2 ((o % 64) / 16), as a byte XOR
   const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + (t0 ^ x)));
   const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + (t4 ^ x)));
   const uint2 ulo = __builtin_bit_cast(uint2, lo), uhi = __builtin_bit_cast(uint2, hi);
@@ -205,7 +229,7 @@ __device__ __forceinline__ void tile_origin(const GemmArgs& g, int t, int& m0, i
 template <bool A_KO, bool B_KO, int EPI>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* ring, int t, int s_begin, int nst,
                                           float* pdst, int64_t pld, bool to_part) {
-  const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   int m0, n0;
   tile_origin(g, t, m0, n0);
@@ -229,35 +253,37 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* ring, int t, 
   using OpB = std::integral_constant<int, 1>;
 
   const int wm = wave & 1, wn = wave >> 1;
-  const int a_off = lane_off_a<64>(lane);
-  const int t0 = lane_off_tr(lane, 0), t4 = lane_off_tr(lane, 4);
-  bf16x8 fa[2][4], fb[2][4];
-  // Fragment r = 0..7 of k16 step ks (order B0, A0, A1, A2, A3, B1, B2, B3:
-  // the order the MFMAs first use them) from slots sa (A) and sb (B).
+  // v_mfma_f32_16x16x32_bf16: the wave's 128 x 128 outputs are 8 (n) x 8 (m)
+  // accumulators of 16 x 16; a stage is two k32 steps of 64 MFMAs.  Operand
+  // lane i holds row/column i%16 and k 8*(i/16) .. +7 of the step.
+  const int a_off = lane_off_kc16(lane);
+  const int t0 = lane_off_tr16(lane, 0), t4 = lane_off_tr16(lane, 4);
+  bf16x8 fa[2][8], fb[2][8];
+  // Fragment r = 0..15 of k32 step ks (order B0, A0..A7, B1..B7: the order
+  // the MFMAs first use them) from slots sa (A) and sb (B).
   auto rd1 = [&](int sa, int sb, int ks, int buf, int r) __attribute__((always_inline)) {
-    if (r >= 1 && r <= 4) {
+    if (r >= 1 && r <= 8) {
       const char* tile = ring + sa * kSlot;
-      const int j = r - 1, o = 128 * wm + 32 * j;
-      fa[buf][j] = A_KO ? frag_ko(tile, t0, t4, o, ks) : frag_kc(tile, a_off, o, ks);
+      const int j = r - 1, o = 128 * wm + 16 * j;
+      fa[buf][j] = A_KO ? frag_ko16(tile, t0, t4, o, ks) : frag_kc16(tile, a_off, o, ks);
     } else {
       const char* tile = ring + sb * kSlot;
-      const int i = r == 0 ? 0 : r - 4, o = 128 * wn + 32 * i;
-      fb[buf][i] = B_KO ? frag_ko(tile, t0, t4, o, ks) : frag_kc(tile, a_off, o, ks);
+      const int i = r == 0 ? 0 : r - 8, o = 128 * wn + 16 * i;
+      fb[buf][i] = B_KO ? frag_ko16(tile, t0, t4, o, ks) : frag_kc16(tile, a_off, o, ks);
     }
   };
-  f32x16 acc[4][4];
+  f32x4 acc[8][8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = zero16();
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   auto mf1 = [&](int buf, int nn) __attribute__((always_inline)) {
-    const int i = nn >> 2, j = nn & 3;
-    acc[i][j] = mfma(fb[buf][i], fa[buf][j], acc[i][j]);
+    const int i = nn >> 3, j = nn & 7;
+    acc[i][j] = mfma16(fb[buf][i], fa[buf][j], acc[i][j]);
   };
 
   // Operand u (A of stage x: u = 2x, B: 2x+1) lives in ring slot u % 5.
-  // Prologue: stages 0 and 1 (B of 1 without its last two runs, which
-  // stage 0 issues), wait for stage 0.
+  // Prologue: stages 0 and 1, wait for stage 0, read its step-0 fragments.
 #pragma unroll
   for (int jj = 0; jj < 8; ++jj) dma(OpA(), 0, 0, jj);
 #pragma unroll
@@ -265,59 +291,54 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* ring, int t, 
 #pragma unroll
   for (int jj = 0; jj < 8; ++jj) dma(OpA(), 1, 2, jj);
 #pragma unroll
-  for (int jj = 0; jj < 6; ++jj) dma(OpB(), 1, 3, jj);
-  wait_vm_n<14>();
+  for (int jj = 0; jj < 8; ++jj) dma(OpB(), 1, 3, jj);
+  wait_vm_n<16>();
   bar();
-  // In the order the loop's tail issues them, so that the loop's first MFMAs
-  // wait for their own fragments only (a different order here would make the
-  // compiler wait for all eight reads at the top of every stage).
 #pragma unroll
-  for (int r = 0; r < 8; ++r) {
+  for (int r = 0; r < 16; ++r) {
     rd1(0, 1, 0, 0, r);
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  // Stage x: 64 MFMAs (k16 steps 0..3 x 16) on fragments read one step
-  // ahead.  Loads issued during stage x (slot s = 2x % 5):
-  //   B(x+1) runs 6, 7 at MFMAs 0, 2        (slot s+3, free since stage x-1)
-  //   A(x+2) runs 0..7 at MFMAs 6..46       (slot s+4, free since stage x-1)
-  //   B(x+2) runs 0..5 at MFMAs 56..61      (slot s, after this stage's reads)
-  // Before the barrier in step 3 each wave waits for all but its last 8 loads
-  // (A(x+2)): stage x+1 is then complete in LDS.
+  // Stage x (A in slot s, B in s+1; stage x+1 in s+2, s+3; s+4 free):
+  //   step 0: 64 MFMAs on buffer 0 while step 1's fragments are read into
+  //     buffer 1 (one read per 4 MFMAs) and A(x+2) is loaded into s+4;
+  //   then each wave waits for its reads and for every load but A(x+2)'s
+  //   (stage x+1 complete in LDS), and the barrier: stage x's slots are
+  //   read no more;
+  //   step 1: 64 MFMAs on buffer 1 while the next stage's step-0 fragments
+  //     are read into buffer 0 and B(x+2) is loaded into slot s.
   int s = 0;
   for (int x = 0; x < nst; ++x) {
     const int sB = mod5(s + 1), nA = mod5(s + 2), nB = mod5(s + 3), fA = mod5(s + 4);
+    // VALU writes of an accumulator (the zeroing before the loop) need wait
+    // states before an MFMA reads it.
+    asm volatile("s_nop 4");
 #pragma unroll
-    for (int ks = 0; ks < 3; ++ks) {
-#pragma unroll
-      for (int nn = 0; nn < 16; ++nn) {
-        const int p = 16 * ks + nn;
-        if ((nn & 1) == 0) rd1(s, sB, ks + 1, (ks + 1) & 1, nn >> 1);
-        if (p == 0) dma(OpB(), x + 1, nB, 6);
-        if (p == 2) dma(OpB(), x + 1, nB, 7);
-        if (p >= 6 && p <= 46 && (p - 6) % 6 == 0 && (p - 6) / 6 < 7) dma(OpA(), x + 2, fA, (p - 6) / 6);
-        if (p == 46) dma(OpA(), x + 2, fA, 7);
-        mf1(ks & 1, nn);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+    for (int p = 0; p < 64; ++p) {
+      if ((p & 3) == 0) rd1(s, sB, 1, 1, p >> 2);
+      if ((p & 7) == 2) dma(OpA(), x + 2, fA, p >> 3);
+      mf1(0, p);
+      __builtin_amdgcn_sched_barrier(0);
     }
-#pragma unroll
-    for (int nn = 0; nn < 8; ++nn) mf1(1, nn);
-    __builtin_amdgcn_sched_barrier(0);
-    // This stage's fragment reads finish before the barrier after which its
-    // slots are refilled.
     wait_lds();
     wait_vm_n<8>();
     bar();
 #pragma unroll
-    for (int tt = 0; tt < 8; ++tt) {
-      if (tt < 6) dma(OpB(), x + 2, s, tt);
-      rd1(nA, nB, 0, 0, tt);
-      mf1(1, 8 + tt);
+    for (int p = 0; p < 64; ++p) {
+      if ((p & 3) == 0) rd1(nA, nB, 0, 0, p >> 2);
+      if ((p & 7) == 2) dma(OpB(), x + 2, s, p >> 3);
+      mf1(1, p);
       __builtin_amdgcn_sched_barrier(0);
     }
     s = nA;
+    // MFMA results need wait states before other instructions read them
+    // (at most 18): after the last stage, before anything (the staging
+    // below, or a copy the register allocator places at the loop's exit)
+    // reads the accumulators.
+    if (x == nst - 1) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
   }
+  __builtin_amdgcn_sched_barrier(0);
   // The re-loads past the end and the last stale fragment reads complete
   // before the ring is reused for the output tile.
   wait_vm();
@@ -331,18 +352,18 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* ring, int t, 
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       if (wm == half) {
+        // lane i of accumulator (i, j): row 16 j + i%16, columns
+        // 128 wn + 16 i + 4 (i/16) .. +3 (one 16-byte chunk)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int r = 32 * j + l32;
+        for (int j = 0; j < 8; ++j) {
+          const int r = 16 * j + (lane & 15);
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int chunk = 32 * wn + 8 * i + 2 * e + hl;
-              const f32x16& v = acc[i][j];
-              *reinterpret_cast<float4*>(ring + r * 1024 + ((chunk ^ (r & 15)) << 4)) =
-                  make_float4(v[4 * e], v[4 * e + 1], v[4 * e + 2], v[4 * e + 3]);
-            }
+          for (int i = 0; i < 8; ++i) {
+            const int chunk = 32 * wn + 4 * i + (lane >> 4);
+            const f32x4& v = acc[i][j];
+            *reinterpret_cast<float4*>(ring + r * 1024 + ((chunk ^ (r & 15)) << 4)) =
+                make_float4(v[0], v[1], v[2], v[3]);
+          }
         }
       }
       wait_lds();
@@ -363,18 +384,18 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* ring, int t, 
     // The bf16 tile goes through LDS ([256 rows x 256 columns], 16-byte chunk
     // c of row r stored at chunk c ^ (r % 16)) so that every global store
     // writes whole rows: lane i of a wave stores chunk i % 32 of row 2q + i / 32.
+    // lane i of accumulator (i, j): row 128 wm + 16 j + i%16, columns
+    // 128 wn + 16 i + 4 (i/16) .. +3 (half a 16-byte chunk)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int r = 128 * wm + 32 * j + l32;
+    for (int j = 0; j < 8; ++j) {
+      const int r = 128 * wm + 16 * j + (lane & 15);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int chunk = 16 * wn + 4 * i + e;
-          const f32x16& v = acc[i][j];
-          *reinterpret_cast<uint2*>(ring + r * 512 + ((chunk ^ (r & 15)) << 4) + 8 * hl) =
-              make_uint2(pk_bf16(v[4 * e], v[4 * e + 1]), pk_bf16(v[4 * e + 2], v[4 * e + 3]));
-        }
+      for (int i = 0; i < 8; ++i) {
+        const int chunk = 16 * wn + 2 * i + (lane >> 5);
+        const f32x4& v = acc[i][j];
+        *reinterpret_cast<uint2*>(ring + r * 512 + ((chunk ^ (r & 15)) << 4) + 8 * ((lane >> 4) & 1)) =
+            make_uint2(pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3]));
+      }
     }
     wait_lds();
     bar();
