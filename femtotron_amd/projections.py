@@ -166,22 +166,25 @@ def layer_gemm_forms(tokens: int, hidden: int, q_width: int, kv_width: int, ffn:
     return forms
 
 
-def measure_dispatch(workloads: dict, path: str | Path = TABLE_FILE, *, iters: int = 20,
+def measure_dispatch(workloads: dict, path: str | Path = TABLE_FILE, *, iters: int = 10, reps: int = 5,
                      log=print) -> Path:
     """Time the hand-written kernel against the library GEMM (with whatever
     library solutions the process has enabled) for every layer GEMM of
     `workloads` ({name: (tokens, hidden, q width, kv width, ffn, head_dim,
     seq_len)}) and write the shapes where the library was faster; for the
     q/k/v projection also the rotating kernel (fh_gemm_bf16_rope) against the
-    library GEMM + fh_rope_fwd.  Needs a HIP device."""
+    library GEMM + fh_rope_fwd.  The two candidates run alternately, `reps`
+    times `iters` launches each, and their medians are compared: the GPU's
+    clock drifts by several percent between back-to-back measurements.  Needs
+    a HIP device."""
+    import statistics
+
     dev, bf = "cuda", torch.bfloat16
     g = torch.Generator(device=dev).manual_seed(0)
     lib_faster: dict[str, list] = {"nt": [], "nn": [], "tn": []}
     rows = []
 
-    def timed(fn) -> float:
-        for _ in range(3):
-            fn()
+    def one(fn) -> float:
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
         for _ in range(iters):
@@ -189,6 +192,16 @@ def measure_dispatch(workloads: dict, path: str | Path = TABLE_FILE, *, iters: i
         e.record()
         e.synchronize()
         return s.elapsed_time(e) / iters * 1e3
+
+    def timed_pair(hand, lib) -> tuple[float, float]:
+        for _ in range(3):
+            hand()
+            lib()
+        th, tl = [], []
+        for _ in range(reps):
+            th.append(one(hand))
+            tl.append(one(lib))
+        return statistics.median(th), statistics.median(tl)
 
     lib_faster["nt_rope"] = []
     for name, (T, H, hq, hkv, F, hd, S) in workloads.items():
@@ -200,8 +213,8 @@ def measure_dispatch(workloads: dict, path: str | Path = TABLE_FILE, *, iters: i
         cos = torch.randn(S, hd, device=dev, generator=g).to(bf)
         sin = torch.randn(S, hd, device=dev, generator=g).to(bf)
         nr = (hq + hkv) // hd
-        t_hand = timed(lambda: ops.gemm_rope(a, b, nr, hd, S, cos, sin))
-        t_lib = timed(lambda: ops.rope_fwd_(torch.mm(a, b.t()), nr, hd, S, cos, sin))
+        t_hand, t_lib = timed_pair(lambda: ops.gemm_rope(a, b, nr, hd, S, cos, sin),
+                                   lambda: ops.rope_fwd_(torch.mm(a, b.t()), nr, hd, S, cos, sin))
         rows.append(dict(workload=name, op="nt_rope", m=m, n=n, k=k, hand_us=round(t_hand, 1),
                          library_us=round(t_lib, 1)))
         if t_lib < t_hand * HAND_MARGIN and [m, n, k] not in lib_faster["nt_rope"]:
@@ -216,8 +229,7 @@ def measure_dispatch(workloads: dict, path: str | Path = TABLE_FILE, *, iters: i
             b = torch.randn(*b_shape, device=dev, generator=g).to(bf)
             lib = {"nt": lambda: torch.mm(a, b.t()), "nn": lambda: torch.mm(a, b),
                    "tn": lambda: torch.mm(a.t(), b)}[op]
-            t_hand = timed(lambda: ops.gemm(op, a, b))
-            t_lib = timed(lib)
+            t_hand, t_lib = timed_pair(lambda: ops.gemm(op, a, b), lib)
             rows.append(dict(workload=name, op=op, m=m, n=n, k=k, hand_us=round(t_hand, 1),
                              library_us=round(t_lib, 1)))
             if t_lib < t_hand * HAND_MARGIN and [m, n, k] not in lib_faster[op]:
