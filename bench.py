@@ -189,6 +189,32 @@ def event_ms(torch, fn, iters: int) -> float:
     return start.elapsed_time(end) / iters
 
 
+def kernel_us(torch, fn, launches: int, before=None, sessions: int = 1) -> float:
+    """Execution time of the kernels of this build that fn(i) launches (names
+    in the fh:: namespace), per call, from the device timestamps torch.profiler
+    collects (roctracer on ROCm: the kernel's own start and end, as
+    rocprofv3 --kernel-trace reports them; launch gaps and host time are not
+    included).  `launches` calls per profiling session, each preceded by
+    before() if given; the median over `sessions` sessions of the per-call
+    mean."""
+    from torch.profiler import ProfilerActivity, profile
+    fn(0)
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(sessions):
+        with profile(activities=[ProfilerActivity.CUDA]) as prof:
+            for i in range(launches):
+                if before is not None:
+                    before()
+                fn(i)
+            torch.cuda.synchronize()
+        evs = [e for e in prof.events()
+               if e.device_type == torch.autograd.DeviceType.CUDA and "fh::" in e.name]
+        per.append(sum(e.device_time_total for e in evs) / launches)
+    per.sort()
+    return per[len(per) // 2]
+
+
 def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True,
                  fused_attention: bool = False):
     """Fused kernels at the step's shapes.  Each launch reads a different buffer
@@ -212,10 +238,15 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True,
     w = (1 + 0.02 * rnd(H)).contiguous()
     rows = []
 
-    def add_row(name, kernel, launches_per_step, bytes_per_launch, ms):
-        gbs = bytes_per_launch / (ms * 1e-3) / 1e9
+    def add_row(name, kernel, launches_per_step, bytes_per_launch, ms, fn=None):
+        # ms: HIP events around `iters` back-to-back launches (launch gaps
+        # included); kernel_ms: the kernels' own execution time (fn re-run
+        # under the profiler); achieved/frac from the latter
+        kms = kernel_us(torch, fn, iters) / 1e3 if fn is not None else ms
+        gbs = bytes_per_launch / (kms * 1e-3) / 1e9
         rows.append(dict(kernel=name, symbol=kernel, launches_per_step=launches_per_step,
-                         bytes_per_launch=int(bytes_per_launch), ms_per_launch=round(ms, 5),
+                         bytes_per_launch=int(bytes_per_launch), ms_per_launch=round(kms, 5),
+                         event_ms_per_launch=round(ms, 5),
                          achieved_gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4)))
 
     L = c["layers"]
@@ -229,32 +260,37 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True,
     xs = sets(8, lambda: rnd(T, H))
     ys = sets(8, lambda: torch.empty(T, H, device=dev, dtype=bf))
     rs = torch.empty(T, device=dev, dtype=torch.float32)
-    ms = event_ms(torch, lambda i=0: ops.rmsnorm_fwd(xs[i % 8], w, 1e-5, out=ys[i % 8], rstd=rs), iters)
+    f = lambda i=0: ops.rmsnorm_fwd(xs[i % 8], w, 1e-5, out=ys[i % 8], rstd=rs)
+    ms = event_ms(torch, f, iters)
     # + the final norm: checkpointed under the selective policy, FusedRMSNorm otherwise
-    add_row("rmsnorm_fwd", "k_rmsnorm_fwd", 2 * L + (1 if sel or boundary else 0), 4 * T * H, ms)
+    add_row("rmsnorm_fwd", "k_rmsnorm_fwd", 2 * L + (1 if sel or boundary else 0), 4 * T * H, ms, f)
     # add_rmsnorm_fwd: x, a -> h, y   (8TH)
     as_ = sets(8, lambda: rnd(T, H))
-    ms = event_ms(torch, lambda i=0: ops.add_rmsnorm_fwd(xs[i % 8], as_[i % 8], w, 1e-5, rstd=rs), iters)
+    f = lambda i=0: ops.add_rmsnorm_fwd(xs[i % 8], as_[i % 8], w, 1e-5, rstd=rs)
+    ms = event_ms(torch, f, iters)
     if not sel:
-        add_row("add_rmsnorm_fwd", "k_rmsnorm_fwd (ADD)", 2 * L, 8 * T * H, ms)
+        add_row("add_rmsnorm_fwd", "k_rmsnorm_fwd (ADD)", 2 * L, 8 * T * H, ms, f)
     if sel:
         # rmsnorm_bwd without residual, statistic recomputed: dy, x -> dx   (6TH)
-        ms = event_ms(torch, lambda i=0: ops.rmsnorm_bwd(ys[i % 8], xs[i % 8], w, 1e-5), iters)
-        add_row("rmsnorm_bwd", "k_rmsnorm_bwd", 2 * L + 1, 6 * T * H, ms)
+        f = lambda i=0: ops.rmsnorm_bwd(ys[i % 8], xs[i % 8], w, 1e-5)
+        ms = event_ms(torch, f, iters)
+        add_row("rmsnorm_bwd", "k_rmsnorm_bwd + k_reduce_parts", 2 * L + 1, 6 * T * H, ms, f)
     else:
         # rmsnorm_bwd with residual: dy, x, dres -> dx   (8TH)
-        ms = event_ms(torch, lambda i=0: ops.rmsnorm_bwd(ys[i % 8], xs[i % 8], w, 1e-5, rstd=rs,
-                                                           dres=as_[i % 8]), iters)
-        add_row("rmsnorm_bwd", "k_rmsnorm_bwd", 2 * L, 8 * T * H, ms)
+        f = lambda i=0: ops.rmsnorm_bwd(ys[i % 8], xs[i % 8], w, 1e-5, rstd=rs, dres=as_[i % 8])
+        ms = event_ms(torch, f, iters)
+        add_row("rmsnorm_bwd", "k_rmsnorm_bwd + k_reduce_parts", 2 * L, 8 * T * H, ms, f)
         if boundary:
             # the final norm's backward: no residual, statistic recomputed: dy, x -> dx   (6TH)
-            ms = event_ms(torch, lambda i=0: ops.rmsnorm_bwd(ys[i % 8], xs[i % 8], w, 1e-5), iters)
-            add_row("final_rmsnorm_bwd", "k_rmsnorm_bwd", 1, 6 * T * H, ms)
+            f = lambda i=0: ops.rmsnorm_bwd(ys[i % 8], xs[i % 8], w, 1e-5)
+            ms = event_ms(torch, f, iters)
+            add_row("final_rmsnorm_bwd", "k_rmsnorm_bwd + k_reduce_parts", 1, 6 * T * H, ms, f)
     del as_
     if not sel:
         # residual add: h + m -> out   (6TH)
-        ms = event_ms(torch, lambda i=0: ops.add(xs[i % 8], ys[i % 8], out=ys[(i + 1) % 8]), iters)
-        add_row("residual_add", "k_add", L, 6 * T * H, ms)
+        f = lambda i=0: ops.add(xs[i % 8], ys[i % 8], out=ys[(i + 1) % 8])
+        ms = event_ms(torch, f, iters)
+        add_row("residual_add", "k_add", L, 6 * T * H, ms, f)
     del xs, ys
     # rope on the k heads of the qkv buffer   (4T Hkv)
     qkvs = sets(6, lambda: rnd(T, Hq + 2 * Hkv))
@@ -263,19 +299,21 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True,
     if attn:
         # k heads only: q is rotated as the attention forward loads it, and the
         # RoPE backward runs inside the attention backward's dQ / dK stores
-        ms = event_ms(torch, lambda i=0: ops.rope_fwd_(qkvs[i % 6][:, Hq:], nkv, hd, c["seq"], cos, sin), iters)
-        add_row("rope_fwd", "k_rope<fwd> (k heads)", n_fwd, 4 * T * Hkv, ms)
+        f = lambda i=0: ops.rope_fwd_(qkvs[i % 6][:, Hq:], nkv, hd, c["seq"], cos, sin)
+        ms = event_ms(torch, f, iters)
+        add_row("rope_fwd", "k_rope<fwd> (k heads)", n_fwd, 4 * T * Hkv, ms, f)
     # SwiGLU: g,u -> p (6TF), in the forward only (the recompute stops at the
     # gate/up projection);  dp,g,u -> dg,du and p over dp (12TF)
     gus = sets(3, lambda: rnd(T, 2 * F))
     ps = sets(3, lambda: torch.empty(T, F, device=dev, dtype=bf))
-    ms = event_ms(torch, lambda i=0: ops.swiglu_fwd(gus[i % 3][:, :F], gus[i % 3][:, F:], out=ps[i % 3]), iters)
-    add_row("swiglu_fwd", "k_swiglu_fwd", L, 6 * T * F, ms)
+    f = lambda i=0: ops.swiglu_fwd(gus[i % 3][:, :F], gus[i % 3][:, F:], out=ps[i % 3])
+    ms = event_ms(torch, f, iters)
+    add_row("swiglu_fwd", "k_swiglu_fwd", L, 6 * T * F, ms, f)
     dgus = sets(3, lambda: torch.empty(T, 2 * F, device=dev, dtype=bf))
-    ms = event_ms(torch, lambda i=0: ops.swiglu_bwd(ps[i % 3], gus[i % 3][:, :F], gus[i % 3][:, F:],
-                                                      dgus[i % 3][:, :F], dgus[i % 3][:, F:], p_out=ps[i % 3]),
-                  iters)
-    add_row("swiglu_bwd", "k_swiglu_bwd (+ p over dp)", L, 12 * T * F, ms)
+    f = lambda i=0: ops.swiglu_bwd(ps[i % 3], gus[i % 3][:, :F], gus[i % 3][:, F:],
+                                   dgus[i % 3][:, :F], dgus[i % 3][:, F:], p_out=ps[i % 3])
+    ms = event_ms(torch, f, iters)
+    add_row("swiglu_bwd", "k_swiglu_bwd (+ p over dp)", L, 12 * T * F, ms, f)
     del gus, ps, dgus
     if boundary:
         # embedding: gather (T rows read and written + int64 ids); backward:
@@ -284,12 +322,14 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True,
         V = c["vocab"]
         emb = rnd(V, H)
         ids = torch.randint(0, V, (T,), device=dev, generator=g)
-        ms = event_ms(torch, lambda i=0: ops.embedding_fwd(ids, emb), iters)
-        add_row("embedding_fwd", "k_embed_fwd", 1, 4 * T * H + 8 * T, ms)
+        f = lambda i=0: ops.embedding_fwd(ids, emb)
+        ms = event_ms(torch, f, iters)
+        add_row("embedding_fwd", "k_embed_fwd", 1, 4 * T * H + 8 * T, ms, f)
         dys = sets(3, lambda: rnd(T, H))
-        ms = event_ms(torch, lambda i=0: ops.embedding_bwd(dys[i % 3], ids, V), iters)
+        f = lambda i=0: ops.embedding_bwd(dys[i % 3], ids, V)
+        ms = event_ms(torch, f, iters)
         add_row("embedding_bwd", "k_embed_keys + 3 x k_radix_* + k_embed_bounds + k_embed_rows", 1,
-                2 * T * H + 2 * V * H + 8 * T, ms)
+                2 * T * H + 2 * V * H + 8 * T, ms, f)
         del emb, dys
     if not attn:  # HF's attention outside the checkpointed modules (selective, --stock-attention)
         return rows, []
@@ -313,17 +353,42 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True,
     # backward: dK/dV kernel 4 products + dQ kernel 3 products (the dQ kernel
     # recomputes S and dP); algorithmic = the 5 products of attention backward
     bwd_flop = 2.5 * fwd_flop
+    # The reference's own kernel at the same shapes: torch's SDPA, causal, GQA
+    # (HF integrations/sdpa_attention.py:154-163), on [B, heads, S, hd]
+    # tensors; forward, and forward + backward (autograd.grad, so no
+    # accumulation into .grad), the backward taken as their difference.
+    import torch.nn.functional as Fn
+    gqa = nkv != nh
+    qh = q.reshape(B, S, nh, hd).transpose(1, 2).contiguous()
+    kh = k.reshape(B, S, nkv, hd).transpose(1, 2).contiguous()
+    vh = v.reshape(B, S, nkv, hd).transpose(1, 2).contiguous()
+    doh = do.reshape(B, S, nh, hd).transpose(1, 2).contiguous()
+
+    def sdpa(a, b_, c_):
+        return Fn.scaled_dot_product_attention(a, b_, c_, is_causal=True, scale=hd ** -0.5, enable_gqa=gqa)
+
+    lib_f = event_ms(torch, lambda i=0: sdpa(qh, kh, vh), iters)
+    qg, kg, vg = (t.detach().requires_grad_(True) for t in (qh, kh, vh))
+    lib_fb = event_ms(torch, lambda i=0: torch.autograd.grad(sdpa(qg, kg, vg), (qg, kg, vg), doh),
+                      max(3, iters // 4))
+    lib_b = max(lib_fb - lib_f, 1e-6)
+    del qh, kh, vh, doh, qg, kg, vg
+    lib_note = "torch.nn.functional.scaled_dot_product_attention(is_causal=True, enable_gqa) at the same shape"
     mfma = [dict(kernel="attn_fwd", symbol=f"k_attn_fwd<{hd}>, q rotated on load and written out "
                                            "(fh_attn_fwd_rope)", launches_per_step=n_fwd,
                  flop_per_launch=fwd_flop, ms_per_launch=round(ms_f, 4),
                  achieved_tflops=round(fwd_flop / ms_f / 1e9, 1),
-                 frac=round(fwd_flop / ms_f / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)),
+                 frac=round(fwd_flop / ms_f / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
+                 library_ms=round(lib_f, 4), library=lib_note + " (forward; the library's forward does "
+                                                                "no RoPE)"),
             dict(kernel="attn_bwd", symbol=f"k_attn_bwd_dq<{hd}> + k_attn_bwd_dkdv"
                                            f"{'_fused' if hd <= 64 else ''}<{hd}>, RoPE backward in the "
                                            "dQ / dK stores (fh_attn_bwd_rope)",
                  launches_per_step=L, flop_per_launch=bwd_flop, ms_per_launch=round(ms_b, 4),
                  achieved_tflops=round(bwd_flop / ms_b / 1e9, 1),
-                 frac=round(bwd_flop / ms_b / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4))]
+                 frac=round(bwd_flop / ms_b / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
+                 library_ms=round(lib_b, 4), library=lib_note + " (forward + backward less forward; "
+                                                                "no RoPE)")]
     mfma += projection_gemm_rows(torch, c, iters, sel, fused_attention, rnd)
     return rows, mfma
 
@@ -390,9 +455,13 @@ def chain_table(torch, shape: dict, reps: int) -> list:
     rows = []
 
     def row(name, symbol, nbytes, fn):
-        ms = flushed_ms(torch, fn, reps, flush)
+        # kernel-only time (profiler, one launch per session after the flush,
+        # median) and the HIP-event time around the launch for comparison
+        ms = kernel_us(torch, fn, 1, before=flush, sessions=reps) / 1e3
+        ev = flushed_ms(torch, fn, reps, flush)
         gbs = nbytes / (ms * 1e-3) / 1e9
         rows.append(dict(kernel=name, symbol=symbol, bytes_per_launch=int(nbytes), ms_per_launch=round(ms, 5),
+                         event_ms_per_launch=round(ev, 5),
                          achieved_gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4)))
 
     row("rmsnorm_fwd", "k_rmsnorm_fwd", 4 * T * H, lambda i: ops.rmsnorm_fwd(x, w, 1e-5, out=y, rstd=rs))
@@ -407,6 +476,24 @@ def chain_table(torch, shape: dict, reps: int) -> list:
     row("swiglu_bwd", "k_swiglu_bwd (+ p over dp)", 12 * T * Fd,
         lambda i: ops.swiglu_bwd(dp, g, u, dg, du, p_out=dp))
     row("residual_add", "k_add", 6 * T * H, lambda i: ops.add(x, dy, out=hh))
+    # Practical ceiling at these sizes: torch's device-to-device copy of x
+    # (T H bf16 read and written: the bytes of rmsnorm_fwd), cold as above.
+    from torch.profiler import ProfilerActivity, profile
+    cp = []
+    for _ in range(reps):
+        flush()
+        with profile(activities=[ProfilerActivity.CUDA]) as prof:
+            hh.copy_(x)
+            torch.cuda.synchronize()
+        cp.append(sum(e.device_time_total for e in prof.events()
+                      if e.device_type == torch.autograd.DeviceType.CUDA and "Memcpy" in e.name) / 1e3)
+    cp.sort()
+    ms = cp[len(cp) // 2]
+    if ms > 0:
+        gbs = 4 * T * H / (ms * 1e-3) / 1e9
+        rows.append(dict(kernel="device_copy (calibration)", symbol="torch copy_ (hipMemcpy device to device)",
+                         bytes_per_launch=4 * T * H, ms_per_launch=round(ms, 5), achieved_gbs=round(gbs, 1),
+                         frac=round(gbs / HBM_PEAK_GBS, 4)))
     del flush_buf
     return rows
 
@@ -819,17 +906,20 @@ def main() -> int:
     rows, mfma = kernel_table(torch, c, args.kernel_iters, args.ac, boundary=bool(boundary),
                               fused_attention=bool(attn_fused))
     for r in rows:
-        r["ms_per_step"] = round(r["ms_per_launch"] * r["launches_per_step"], 4)
+        r["ms_per_step"] = round(r["event_ms_per_launch"] * r["launches_per_step"], 4)
     for r in mfma:
         r["ms_per_step"] = round(r["ms_per_launch"] * r["launches_per_step"], 4)
     timing = (f"mean of {args.kernel_iters} back-to-back launches alone at the step's shape, HIP events "
-              "on the launch stream")
+              "on the launch stream (fused_kernels_hbm rows: ms_per_launch is the kernels' own execution "
+              "time from torch.profiler device timestamps, event_ms_per_launch the HIP-event mean)")
     dom = max(rows, key=lambda r: r["ms_per_step"])
-    roofline_hbm = {"bound": "hbm", "kernel": dom["kernel"], "achieved": dom["achieved_gbs"],
-                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["frac"],
+    ev_gbs = dom["bytes_per_launch"] / (dom["event_ms_per_launch"] * 1e-3) / 1e9
+    roofline_hbm = {"bound": "hbm", "kernel": dom["kernel"], "achieved": round(ev_gbs, 1),
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ev_gbs / HBM_PEAK_GBS, 4),
                     "traffic": measured_traffic(dom["kernel"]) if args.workload == "tinyllama" else None,
-                    "bytes_per_launch": dom["bytes_per_launch"], "us_per_launch": round(dom["ms_per_launch"] * 1e3, 2),
-                    "duration": timing}
+                    "bytes_per_launch": dom["bytes_per_launch"],
+                    "us_per_launch": round(dom["event_ms_per_launch"] * 1e3, 2), "duration": timing,
+                    "kernel_only_frac": dom["frac"]}
     # The dominant kernel of this build: the hand-written kernel (fused HBM,
     # attention or projection GEMM on fh_gemm_bf16) with the most time per step.
     own = [r for r in mfma if not r.get("path", "fh").startswith("library")]
@@ -898,7 +988,9 @@ def main() -> int:
     if not args.no_chain:
         log("BASELINE config 2: the memory-bound chain op-level, MALL flushed before every launch")
         chain = {"shape": CHAIN_CFG2, "rows": chain_table(torch, CHAIN_CFG2, max(10, args.kernel_iters)),
-                 "duration": "median of per-launch HIP events, a 512 MiB read before each launch"}
+                 "duration": "kernel execution time (torch.profiler device timestamps, the rocprofv3 kernel-trace "
+                             "durations), median of one launch per session after a 512 MiB read that evicts the "
+                             "MALL; event_ms_per_launch: HIP events around the same launch"}
         torch.cuda.empty_cache()
 
     cpu = None

@@ -124,10 +124,10 @@ __global__ __launch_bounds__(256) void k_rmsnorm_fwd(
 // order through LDS into one fp32 row per block (deterministic), which
 // k_reduce_parts folds into dw.
 // Next-row prefetch (PF): measured 50.6 -> 43.5 us without the residual
-// gradient at T=16384, H=2048; with it (3 input rows) the extra registers cost
-// a wave of occupancy and it gained nothing (60.8 vs 62.3 us), so it is on only
-// for the 2-input form.
-template <typename T, int NVW, int WPR, int NWB, bool RES, bool HAVE_RSTD, bool PF = !RES>
+// gradient at T=16384, H=2048; with it (3 input rows) at that width the extra
+// registers cost a wave of occupancy and it gained nothing (60.8 vs 62.3 us);
+// BwdSplit chooses it per width.
+template <typename T, int NVW, int WPR, int NWB, bool RES, bool HAVE_RSTD, bool PF>
 __global__ __launch_bounds__(64 * NWB) void k_rmsnorm_bwd(
     const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ w,
     const float* __restrict__ rstd, const T* __restrict__ dres,
@@ -342,6 +342,8 @@ constexpr int kMaxBwdBlocks = FH_NORM_BWD_BLOCKS;
 // Grid cap of the pipelined add+RMSNorm forward (768 measured best of 512,
 // 768, 1024 and 2048 at T = 16384, H = 2048).
 constexpr int64_t kFwdPipeBlocks = 768;
+// Grid cap of the pipelined one-input forward (2049-4096 bf16 columns).
+constexpr int64_t kFwdPipeBlocks1 = 512;
 
 template <typename T, int NV>
 void launch_fwd(const void* x, const void* a, const void* w, void* h, void* y, float* rstd,
@@ -356,6 +358,12 @@ void launch_fwd(const void* x, const void* a, const void* w, void* h, void* y, f
                        static_cast<const T*>(x), static_cast<const T*>(a),
                        static_cast<const T*>(w), static_cast<T*>(h), static_cast<T*>(y), rstd,
                        rows, cols, eps);
+  } else if (NV == 8 && sizeof(typename Elem<T>::Raw) == 16 && need > kFwdPipeBlocks1) {
+    // one input, 2049-4096 bf16 columns: pipelined over a capped grid (kernel
+    // time 15.3 -> 14.1 us at T = 4096, 26.1 -> 23.7 us at 8192, H = 4096)
+    hipLaunchKernelGGL((k_rmsnorm_fwd<T, NV, false, true>), dim3(static_cast<unsigned>(kFwdPipeBlocks1)), dim3(256),
+                       0, s, static_cast<const T*>(x), nullptr, static_cast<const T*>(w), nullptr,
+                       static_cast<T*>(y), rstd, rows, cols, eps);
   } else {
     hipLaunchKernelGGL((k_rmsnorm_fwd<T, NV, false, false>), dim3(static_cast<unsigned>(need)), dim3(256), 0, s,
                        static_cast<const T*>(x), nullptr, static_cast<const T*>(w), nullptr,
@@ -364,17 +372,22 @@ void launch_fwd(const void* x, const void* a, const void* w, void* h, void* y, f
 }
 
 // Backward row split: WPR waves per row, NVW chunks of 8 per lane, NWB waves
-// per block (RPB = NWB / WPR rows per block step).  Rows of 1025-2048 columns
-// with the residual gradient (the layer's two norms) take two waves each in
-// blocks of 8: twice the waves in flight at the same partial-row count, 60 ->
-// 56 us at T = 16384, H = 2048 (one wave per row in blocks of 8 or 16 needs
-// more than the 128 registers of four waves per SIMD).
+// per block (RPB = NWB / WPR rows per block step), PF: next-row prefetch.
+// Rows of 1025-2048 columns with the residual gradient (the layer's two
+// norms) take two waves each in blocks of 8: twice the waves in flight at the
+// same partial-row count, 60 -> 56 us at T = 16384, H = 2048 (one wave per
+// row in blocks of 8 or 16 needs more than the 128 registers of four waves
+// per SIMD).  Rows of 2049-4096 columns with the residual gradient take four
+// waves each, with the next row prefetched: kernel time 37.7 -> 33.7 us at
+// T = 4096, 60.1 -> 53.8 us at 8192, 206.9 -> 191.6 us at 32768 (H = 4096).
 template <int NV, bool RES>
 struct BwdSplit {
-  static constexpr int WPR = NV > 4 || (NV == 4 && RES) ? 2 : 1;
+  static constexpr bool kWide = NV == 8 && RES;
+  static constexpr int WPR = kWide ? 4 : NV > 4 || (NV == 4 && RES) ? 2 : 1;
   static constexpr int NVW = NV / WPR;
-  static constexpr int NWB = NV == 4 && RES ? 8 : 4;
+  static constexpr int NWB = kWide || (NV == 4 && RES) ? 8 : 4;
   static constexpr int RPB = NWB / WPR;
+  static constexpr bool PF = !RES || kWide;
 };
 
 // Blocks of the backward: one per RPB rows, at most kMaxBwdBlocks (each
@@ -389,7 +402,7 @@ void launch_bwd_k(const void* dy, const void* x, const void* w, const float* rst
                   const void* dres, void* dx, float* part, int64_t rows, int cols, float eps,
                   int blocks, hipStream_t s) {
   using SP = BwdSplit<NV, RES>;
-  hipLaunchKernelGGL((k_rmsnorm_bwd<T, SP::NVW, SP::WPR, SP::NWB, RES, HR>), dim3(blocks), dim3(64 * SP::NWB),
+  hipLaunchKernelGGL((k_rmsnorm_bwd<T, SP::NVW, SP::WPR, SP::NWB, RES, HR, SP::PF>), dim3(blocks), dim3(64 * SP::NWB),
                      static_cast<size_t>(cols) * sizeof(float), s, static_cast<const T*>(dy),
                      static_cast<const T*>(x), static_cast<const T*>(w), rstd,
                      static_cast<const T*>(dres), static_cast<T*>(dx), part, rows, cols, eps);

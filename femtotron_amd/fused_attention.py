@@ -42,7 +42,8 @@ import torch
 
 from . import _lib, ops
 from .fused_checkpoint import _aligned, _causal_attention_reason, _check_params, _linear_weight
-from .fused_layer import LayerShape, _WgradStream, _cat_rows, attn_bwd, qkv_attention
+from .fused_layer import (LayerShape, _WgradStream, _cat_rows, attn_bwd, grad_target, qkv_attention,
+                          split_rows)
 from .projections import linear, linear_dgrad
 
 _ACCEPTED_KWARGS = {"position_ids", "use_cache", "cache_position"}
@@ -88,16 +89,14 @@ class FusedAttentionFunction(torch.autograd.Function):
         da2 = da.contiguous().view(B * S, H)
         with torch.no_grad():
             side = _WgradStream(da2.device)
-            dwo = side.mm_tn(da2, o)
+            dwo = side.mm_tn(da2, o, grad_target(wo))
             do = linear_dgrad(da2, wo)
             dqkv = attn_bwd(do, qkv, o, lse, B, S, shp, cos, sin)
             del do
-            dwqkv = side.mm_tn(dqkv, y.reshape(B * S, H))
+            dwqkv = side.mm_tn(dqkv, y.reshape(B * S, H), grad_target(wq, wk, wv))
             dy = linear_dgrad(dqkv, _cat_rows(wq, wk, wv))
             side.join()
-        hq, hkv = shp.hq, shp.hkv
-        return (dy.view(B, S, H), None, None, None, dwqkv[:hq], dwqkv[hq:hq + hkv],
-                dwqkv[hq + hkv:], dwo)
+        return (dy.view(B, S, H), None, None, None, *split_rows(dwqkv, shp.hq, shp.hkv, shp.hkv), dwo)
 
 
 def _projection_hooks(attn: torch.nn.Module) -> bool:

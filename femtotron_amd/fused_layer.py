@@ -37,7 +37,7 @@ from dataclasses import dataclass
 import torch
 
 from . import ops
-from .projections import linear, linear_dgrad, linear_residual, linear_rope, linear_wgrad
+from .projections import linear, linear_dgrad, linear_residual, linear_rope, linear_wgrad, linear_wgrad_into
 from .weight_packing import packed
 
 
@@ -161,6 +161,48 @@ def wgrad_side_stream() -> bool:
     return _use_side_stream
 
 
+_accumulate_in_gemm = True
+
+
+def set_grad_accumulation_in_gemm(enabled: bool) -> None:
+    """Accumulate weight gradients into existing bf16 .grad tensors inside the
+    weight-gradient GEMM (True, the default) instead of returning them for
+    autograd to add.  The reference's training loop keeps .grad between
+    steps (GradAccumulator.reset zeroes it in place,
+    femtotron/training/grad_accumulator.py:55-60, and micro-batches after the
+    first accumulate into it, :24-36), so every backward but the very first
+    adds into an existing gradient; done in the GEMM's epilogue it costs no
+    separate pass over the 9 gradients (3 x their bytes per layer).  Same bits
+    as autograd's addition: grad + to_bf16(dW), rounded."""
+    global _accumulate_in_gemm
+    _accumulate_in_gemm = bool(enabled)
+
+
+def grad_accumulation_in_gemm() -> bool:
+    return _accumulate_in_gemm
+
+
+def grad_target(*params: torch.Tensor) -> torch.Tensor | None:
+    """The existing gradients of `params` (the parameters one weight-gradient
+    GEMM produces, its output rows in this order) as one [rows, cols] tensor,
+    when the GEMM can accumulate into them: every .grad present, bf16,
+    contiguous, of the parameter's shape, laid out row-contiguously in one
+    buffer (as autograd leaves them after a first backward, which stores the
+    row views of the GEMM output), and no gradient hooks on the parameters
+    (their AccumulateGrad step is what the in-place accumulation skips).
+    None otherwise."""
+    if not _accumulate_in_gemm:
+        return None
+    gs = []
+    for p in params:
+        g = p.grad
+        if (g is None or g.dtype != torch.bfloat16 or g.shape != p.shape or g.requires_grad
+                or p._backward_hooks or getattr(p, "_post_accumulate_grad_hooks", None)):
+            return None
+        gs.append(g)
+    return packed(*gs)
+
+
 class _WgradStream:
     """Weight-gradient GEMMs, on a side stream (default priority) when
     set_wgrad_side_stream(True), else in order on the main stream.
@@ -180,17 +222,23 @@ class _WgradStream:
             side = _side_streams[device.index] = torch.cuda.Stream(device=device)
         self.side = side
 
-    def mm_tn(self, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    def mm_tn(self, a: torch.Tensor, b: torch.Tensor, into: torch.Tensor | None = None) -> torch.Tensor | None:
         """a^T @ b on the side stream (projections.linear_wgrad); on the main
-        stream when the side stream is switched off."""
+        stream when the side stream is switched off.  With `into` (grad_target)
+        the product is accumulated into it where the hand-written GEMM runs
+        (returns None), else returned."""
         if not _use_side_stream:
+            if into is not None and linear_wgrad_into(a, b, into):
+                return None
             return linear_wgrad(a, b)
         self.side.wait_stream(self.main)
         with torch.cuda.stream(self.side):
-            out = linear_wgrad(a, b)
+            done = into is not None and linear_wgrad_into(a, b, into)
+            out = None if done else linear_wgrad(a, b)
         a.record_stream(self.side)
         b.record_stream(self.side)
-        out.record_stream(self.main)
+        if out is not None:
+            out.record_stream(self.main)
         return out
 
     def join(self) -> None:
@@ -198,8 +246,22 @@ class _WgradStream:
             self.main.wait_stream(self.side)
 
 
+def split_rows(dw: torch.Tensor | None, *rows: int) -> tuple:
+    """Row blocks of a packed weight gradient (all None where it was
+    accumulated into the existing gradients)."""
+    if dw is None:
+        return (None,) * len(rows)
+    out, r = [], 0
+    for n in rows:
+        out.append(dw[r:r + n])
+        r += n
+    return tuple(out)
+
+
 def layer_backward(dout2: torch.Tensor, x2: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                    shp: LayerShape, batch: int, seq: int, w: tuple, acts: _Acts):
+    """dx and the 9 weight gradients; a weight gradient accumulated into the
+    parameter's existing .grad inside its GEMM (grad_target) comes back as None."""
     wq, wk, wv, wo, wg, wu, wd, w1, w2 = w
     F_ = shp.ffn
     wg_stream = _WgradStream(dout2.device)
@@ -210,9 +272,9 @@ def layer_backward(dout2: torch.Tensor, x2: torch.Tensor, cos: torch.Tensor, sin
     dgu = torch.empty_like(acts.gu)
     ops.swiglu_bwd(dp, acts.gu[:, :F_], acts.gu[:, F_:], dgu[:, :F_], dgu[:, F_:], p_out=dp)
     acts.gu = None
-    dwd = wg_stream.mm_tn(dout2, dp)
+    dwd = wg_stream.mm_tn(dout2, dp, grad_target(wd))
     del dp
-    dwgu = wg_stream.mm_tn(dgu, acts.z)
+    dwgu = wg_stream.mm_tn(dgu, acts.z, grad_target(wg, wu))
     dz = linear_dgrad(dgu, _cat_rows(wg, wu))
     del dgu
     acts.z = None
@@ -221,20 +283,19 @@ def layer_backward(dout2: torch.Tensor, x2: torch.Tensor, cos: torch.Tensor, sin
     del dz
     acts.h = None
     # attention output projection
-    dwo = wg_stream.mm_tn(dh, acts.o)
+    dwo = wg_stream.mm_tn(dh, acts.o, grad_target(wo))
     do = linear_dgrad(dh, wo)
     dqkv = attn_bwd(do, acts.qkv, acts.o, acts.lse, batch, seq, shp, cos, sin)
     del do
     acts.o = acts.lse = acts.qkv = None
-    dwqkv = wg_stream.mm_tn(dqkv, acts.y1)
+    dwqkv = wg_stream.mm_tn(dqkv, acts.y1, grad_target(wq, wk, wv))
     dy1 = linear_dgrad(dqkv, _cat_rows(wq, wk, wv))
     del dqkv
     acts.y1 = None
     dx, dw1 = ops.rmsnorm_bwd(dy1, x2, w1, shp.eps1, rstd=acts.rstd1, dres=dh)
     wg_stream.join()
-    hq, hkv = shp.hq, shp.hkv
-    dwq, dwk, dwv = dwqkv[:hq], dwqkv[hq:hq + hkv], dwqkv[hq + hkv:]
-    dwg, dwu = dwgu[:F_], dwgu[F_:]
+    dwq, dwk, dwv = split_rows(dwqkv, shp.hq, shp.hkv, shp.hkv)
+    dwg, dwu = split_rows(dwgu, F_, F_)
     return dx, (dwq, dwk, dwv, dwo, dwg, dwu, dwd, dw1, dw2)
 
 

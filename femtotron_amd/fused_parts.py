@@ -22,7 +22,7 @@ from __future__ import annotations
 import torch
 
 from . import ops
-from .fused_layer import _cat_rows, _WgradStream
+from .fused_layer import _cat_rows, _WgradStream, grad_target, split_rows
 from .projections import linear, linear_dgrad
 
 
@@ -42,7 +42,8 @@ def mlp_forward(z2: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor, wd: torch.
 def mlp_backward(dm2: torch.Tensor, z2: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor,
                  wd: torch.Tensor, gu: torch.Tensor):
     """The MLP's backward from the recomputed gu (pass it without keeping a
-    reference, so that it is freed once the SwiGLU backward has read it)."""
+    reference, so that it is freed once the SwiGLU backward has read it).
+    Weight gradients accumulated into existing .grad tensors come back None."""
     F_ = wg.shape[0]
     wg_stream = _WgradStream(dm2.device)
     dp = linear_dgrad(dm2, wd)
@@ -50,12 +51,12 @@ def mlp_backward(dm2: torch.Tensor, z2: torch.Tensor, wg: torch.Tensor, wu: torc
     # also p = silu(g)*u, into dp's buffer (read before overwritten), for dWd
     ops.swiglu_bwd(dp, gu[:, :F_], gu[:, F_:], dgu[:, :F_], dgu[:, F_:], p_out=dp)
     del gu
-    dwd = wg_stream.mm_tn(dm2, dp)
+    dwd = wg_stream.mm_tn(dm2, dp, grad_target(wd))
     del dp
-    dwgu = wg_stream.mm_tn(dgu, z2)
+    dwgu = wg_stream.mm_tn(dgu, z2, grad_target(wg, wu))
     dz = linear_dgrad(dgu, _cat_rows(wg, wu))
     wg_stream.join()
-    return dz, dwgu[:F_], dwgu[F_:], dwd
+    return (dz, *split_rows(dwgu, F_, F_), dwd)
 
 
 class FusedMLPFunction(torch.autograd.Function):

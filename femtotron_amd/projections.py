@@ -156,6 +156,21 @@ def linear_wgrad(dy: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     return torch.mm(dy.t(), x)
 
 
+def linear_wgrad_into(dy: torch.Tensor, x: torch.Tensor, grad: torch.Tensor) -> bool:
+    """grad = to_bf16(grad + to_bf16(dy^T x)) in place, where the hand-written
+    GEMM takes the shape: its residual epilogue with the residual and the
+    output both `grad`, the two roundings of accumulating a bf16 weight
+    gradient into an existing bf16 .grad (autograd's grad + new_grad after the
+    GEMM rounded new_grad).  Returns False, doing nothing, where the shape
+    runs on the library (whose accumulating GEMM rounds once): the caller
+    then computes the gradient and lets autograd add it."""
+    if not _choose_hand("tn", dy, x):
+        return False
+    _count(True)
+    ops.gemm("tn", dy, x, residual=grad, out=grad)
+    return True
+
+
 def layer_gemm_forms(tokens: int, hidden: int, q_width: int, kv_width: int, ffn: int):
     """(op, m, n, k) of every GEMM a fused decoder layer issues (packed q/k/v and
     gate/up), in fh_gemm_bf16's convention."""

@@ -180,3 +180,34 @@ def test_fused_attention_falls_back_where_kernels_do_not_apply():
     assert dispatch_counts() == {"fused": 1, "fallback": 0}
     assert attention_dispatch_counts() == {"fused": 0, "fallback": 0}
     unfuse_attention(model)
+
+
+def test_selective_gradient_accumulation_in_the_gemm_equals_autograds():
+    """Selective AC with the fused attention: two backward passes into
+    existing gradients, weight gradients accumulated inside the GEMMs (fused
+    attention's o and q/k/v, the MLP's gate/up and down) against autograd's
+    accumulation of the same gradients: bit for bit."""
+    from femtotron_amd import fuse_attention, fused_checkpoint
+    from femtotron_amd.fused_layer import set_grad_accumulation_in_gemm
+    from femtotron_amd.scripts.presets import get_ac_policy
+    from femtotron_amd.training import apply_activation_checkpointing
+
+    c = CFG3
+    ids = torch.randint(0, c["vocab"], (1, 512), generator=torch.Generator().manual_seed(2000)).to(DEV)
+    grads = []
+    try:
+        for in_gemm in (False, True):
+            set_grad_accumulation_in_gemm(in_gemm)
+            model = _model(c, 2, torch.bfloat16)
+            fuse_attention(model)
+            apply_activation_checkpointing(model, get_ac_policy("llama_mlp_and_norms"),
+                                           checkpoint_fn=fused_checkpoint)
+            for _ in range(2):
+                model(ids, labels=ids)["loss"].backward()
+            grads.append({n: p.grad.clone() for n, p in model.named_parameters()})
+            del model
+    finally:
+        set_grad_accumulation_in_gemm(True)
+    assert grads[0].keys() == grads[1].keys()
+    for n in grads[0]:
+        assert torch.equal(grads[0][n], grads[1][n]), n

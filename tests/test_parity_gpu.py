@@ -314,3 +314,47 @@ def test_unsupported_head_dim_falls_back_to_stock_checkpoint(hd):
     want = checkpoint(layer, x, use_reentrant=False, position_embeddings=(cos, sin))
     want = want[0] if isinstance(want, tuple) else want
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("packed", [False, True], ids=["unpacked", "packed"])
+def test_gradient_accumulation_in_the_gemm_equals_autograds(packed):
+    """With .grad already present (the reference's GradAccumulator keeps it
+    between steps and accumulates micro-batches into it,
+    femtotron/training/grad_accumulator.py:24-60), the weight-gradient GEMMs
+    add into it in their epilogue.  The result must be autograd's own
+    accumulation of the same gradients bit for bit: to_bf16(grad + to_bf16(dW)).
+    A .grad that is not laid out as the GEMM's output (here: a fresh
+    non-contiguous tensor) takes autograd's path."""
+    from femtotron_amd import dispatch_counts, reset_dispatch_counts
+    from femtotron_amd.fused_layer import grad_accumulation_in_gemm, set_grad_accumulation_in_gemm
+    from femtotron_amd.projections import gemm_dispatch_counts, reset_gemm_dispatch_counts
+    c = CFG3
+    assert grad_accumulation_in_gemm()
+    results = []
+    try:
+        for in_gemm in (False, True):
+            set_grad_accumulation_in_gemm(in_gemm)
+            layers = _stack(c, 2, 600, packed)
+            reset_dispatch_counts()
+            reset_gemm_dispatch_counts()
+            results.append(_two_micro_batches(layers, c, 256, fused=True))
+            assert dispatch_counts() == {"fused": 4, "fallback": 0}
+    finally:
+        set_grad_accumulation_in_gemm(True)
+    for i, (a, b) in enumerate(zip(*results)):
+        assert torch.equal(a, b), f"param {i}"
+    # a gradient the GEMM cannot write (transposed storage) is left to autograd
+    layers = _stack(c, 1, 700, packed)
+    wo = layers[0].self_attn.o_proj.weight
+    wo.grad = torch.zeros(wo.shape[1], wo.shape[0], device=DEV, dtype=torch.bfloat16).t()
+    assert not wo.grad.is_contiguous()
+    hd = c["hidden"] // c["heads"]
+    cos, sin = ot.rope_cos_sin(128, hd, c["theta"], torch.bfloat16, device=DEV)
+    x = randn((1, 128, c["hidden"]), 5).to(DEV, torch.bfloat16).requires_grad_(True)
+    _wrapped(layers[0], True)(x, attention_mask=None, position_embeddings=(cos, sin)).backward(
+        randn((1, 128, c["hidden"]), 6).to(DEV, torch.bfloat16))
+    ref = _stack(c, 1, 700, packed)
+    _wrapped(ref[0], True)(x.detach().requires_grad_(True), attention_mask=None,
+                           position_embeddings=(cos, sin)).backward(
+        randn((1, 128, c["hidden"]), 6).to(DEV, torch.bfloat16))
+    assert torch.equal(wo.grad, ref[0].self_attn.o_proj.weight.grad)
