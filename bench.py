@@ -117,7 +117,9 @@ def parse_args():
                          "add_rmsnorm_fwd, rmsnorm_bwd, rope_fwd, residual_add, attn_fwd, attn_bwd; "
                          "embedding_fwd, embedding_bwd; gemm_<nt|nn|tn>_<qkv|o|gate_up|down> "
                          "(fh_gemm_bf16 at that projection GEMM); "
-                         "adamw: one optimizer step over the workload's parameter shapes) at "
+                         "adamw: one optimizer step over the workload's parameter shapes; "
+                         "chain_cfg2: BASELINE config 2's memory-bound chain, each launch after a "
+                         "MALL-evicting read) at "
                          "--workload's step shape, after a 1 GiB device copy that calibrates HBM byte "
                          "counters, for rocprofv3 --pmc runs; prints one JSON line and exits")
     return ap.parse_args()
@@ -559,7 +561,8 @@ def projection_gemm_rows(torch, c: dict, iters: int, sel: bool, fused_attention:
 def profile_kernel(torch, name: str, c: dict, launches: int = 10) -> dict:
     """A 1 GiB device-to-device copy (known traffic: 1 GiB read + 1 GiB written),
     then `launches` launches of one fused kernel at the step's shape of workload
-    `c`, each on a fresh buffer set (attention: on one buffer set).  Under
+    `c`, each on a fresh buffer set (attention: on one buffer set; chain_cfg2:
+    BASELINE config 2's chain, each launch after a MALL-evicting read).  Under
     rocprofv3 --pmc FETCH_SIZE (or WRITE_SIZE) the copy's reading calibrates the
     counter's units."""
     from femtotron_amd import ops
@@ -643,6 +646,36 @@ def profile_kernel(torch, name: str, c: dict, launches: int = 10) -> dict:
         operands = {"nt": (xs, ws), "nn": (dys, ws), "tn": (dys, xs)}[op]
         fn = lambda i: ops.gemm(op, operands[0][i % 2], operands[1][i % 2])
         nbytes = None  # MFMA-bound: 2*T*n_out*k_in FLOP per launch
+    elif name == "chain_cfg2":
+        # BASELINE config 2's memory-bound chain, each kernel `launches` times,
+        # every launch after a 512 MiB read that evicts the MALL (the launches
+        # of chain_table, without its profiler or events)
+        sh = CHAIN_CFG2
+        Tc, Hc, Fc, nr, hdc = sh["tokens"], sh["hidden"], sh["ffn"], sh["rope_heads"], sh["head_dim"]
+        x, dy, hh = rnd(Tc, Hc), rnd(Tc, Hc), torch.empty(Tc, Hc, device=dev, dtype=bf)
+        w = (1 + 0.02 * rnd(Hc)).contiguous()
+        gg, uu, dp = rnd(Tc, Fc), rnd(Tc, Fc), rnd(Tc, Fc)
+        dg, du, pp = (torch.empty(Tc, Fc, device=dev, dtype=bf) for _ in range(3))
+        q = rnd(Tc, nr * hdc)
+        cos, sin = rnd(1, Tc, hdc), rnd(1, Tc, hdc)
+        rs = torch.empty(Tc, device=dev, dtype=torch.float32)
+        ops.rmsnorm_fwd(x, w, 1e-5, out=hh, rstd=rs)
+        flush_buf = torch.ones(MALL_FLUSH_BYTES // 4, device=dev, dtype=torch.float32)
+        chain = [lambda: ops.rmsnorm_fwd(x, w, 1e-5, out=hh, rstd=rs),
+                 lambda: ops.add_rmsnorm_fwd(x, dy, w, 1e-5, rstd=rs),
+                 lambda: ops.rmsnorm_bwd(dy, x, w, 1e-5, rstd=rs, dres=hh),
+                 lambda: ops.rmsnorm_bwd(dy, x, w, 1e-5),
+                 lambda: ops.rope_fwd_(q, nr, hdc, Tc, cos, sin),
+                 lambda: ops.rope_bwd_(q, nr, hdc, Tc, cos, sin),
+                 lambda: ops.swiglu_fwd(gg, uu, out=pp),
+                 lambda: ops.swiglu_bwd(dp, gg, uu, dg, du, p_out=dp),
+                 lambda: ops.add(x, dy, out=hh)]
+
+        def fn(i):
+            for f in chain:
+                flush_buf.sum()
+                f()
+        nbytes = None
     elif name == "adamw":
         from femtotron_amd.optim import FusedAdamW
         V, L = c["vocab"], c["layers"]

@@ -41,11 +41,12 @@ import torch
 from . import ops
 
 TABLE_FILE = Path(__file__).resolve().parent / "tuned" / "gemm_dispatch_gfx950.json"
-# The hand-written kernel takes a shape only when it measured at least this much
-# faster alone: inside the step, the library's kernel measured the faster of
-# near-ties (the gate/up input gradient at TinyLlama: 568 vs 570 us alone,
-# ~570 vs ~527 us inside the step).
-HAND_MARGIN = 1.01
+# The library takes a shape only when it measured at least this much faster
+# than the hand-written kernel alone (the two alternate, medians compared):
+# inside the TinyLlama step the input-gradient (NN) GEMMs, each within 1% of
+# the library alone, ran faster hand-written (126.7k against 125.8k tokens/s
+# with the library taking those near-ties).
+LIBRARY_MARGIN = 1.02
 
 _lock = threading.Lock()
 _policy = ["auto"]
@@ -232,7 +233,7 @@ def measure_dispatch(workloads: dict, path: str | Path = TABLE_FILE, *, iters: i
                                    lambda: ops.rope_fwd_(torch.mm(a, b.t()), nr, hd, S, cos, sin))
         rows.append(dict(workload=name, op="nt_rope", m=m, n=n, k=k, hand_us=round(t_hand, 1),
                          library_us=round(t_lib, 1)))
-        if t_lib < t_hand * HAND_MARGIN and [m, n, k] not in lib_faster["nt_rope"]:
+        if t_lib * LIBRARY_MARGIN < t_hand and [m, n, k] not in lib_faster["nt_rope"]:
             lib_faster["nt_rope"].append([m, n, k])
         log(f"[gemm-dispatch] {name} nt_rope m={m} n={n} k={k}: hand {t_hand:.1f} us, "
             f"library + rope {t_lib:.1f} us")
@@ -247,15 +248,15 @@ def measure_dispatch(workloads: dict, path: str | Path = TABLE_FILE, *, iters: i
             t_hand, t_lib = timed_pair(lambda: ops.gemm(op, a, b), lib)
             rows.append(dict(workload=name, op=op, m=m, n=n, k=k, hand_us=round(t_hand, 1),
                              library_us=round(t_lib, 1)))
-            if t_lib < t_hand * HAND_MARGIN and [m, n, k] not in lib_faster[op]:
+            if t_lib * LIBRARY_MARGIN < t_hand and [m, n, k] not in lib_faster[op]:
                 lib_faster[op].append([m, n, k])
             log(f"[gemm-dispatch] {name} {op} m={m} n={n} k={k}: hand {t_hand:.1f} us, "
                 f"library {t_lib:.1f} us")
             del a, b
-    data = {"note": "shapes (m, n, k of fh_gemm_bf16) where the tuned library GEMM measured faster "
-                    "than the hand-written kernel on an MI355X, or within 1% of it (inside a step the "
-                    "library's kernel measured the faster of such near-ties); nt_rope: the library GEMM "
-                    "followed by fh_rope_fwd against fh_gemm_bf16_rope; everything else runs hand-written",
+    data = {"note": "shapes (m, n, k of fh_gemm_bf16) where the tuned library GEMM measured at least 2% "
+                    "faster than the hand-written kernel on an MI355X (medians of alternating runs); "
+                    "nt_rope: the library GEMM followed by fh_rope_fwd against fh_gemm_bf16_rope; "
+                    "everything else runs hand-written",
             "library": lib_faster, "measurements": rows}
     Path(path).write_text(json.dumps(data, indent=1) + "\n")
     global _table

@@ -347,7 +347,12 @@ int fh_embedding_bwd(fh_dtype dt, const void* dy, const int64_t* ids, void* dwei
  * projection output rounded, then the residual add `hidden_states = residual +
  * hidden_states` of modeling_llama.py:323 fused into the epilogue with its own
  * rounding.  `residual` may be C itself (same ldc), any other overlap is not
- * allowed.
+ * allowed.  With residual == C this is the accumulating epilogue (alpha =
+ * beta = 1) of gradient accumulation: FH_GEMM_TN into an existing bf16 weight
+ * gradient gives C = to_bf16(C + to_bf16(dY^T X)), bit for bit autograd's
+ * `param.grad += new_grad` after the GEMM rounded new_grad (the in-place
+ * accumulation of femtotron/training/grad_accumulator.py:24-36 with
+ * grad_acc_dtype None).
  * Requirements: k % 64 == 0; n % 8 == 0 (and m % 8 == 0 for FH_GEMM_TN);
  * lda, ldb, ldc and ldr multiples of 8 (< 2^26 for lda, ldb); A, B, C and the
  * residual 16-byte aligned; m, n, k < 2^30.
