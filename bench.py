@@ -116,7 +116,7 @@ def parse_args():
                     help="launch only this fused kernel (swiglu_fwd, swiglu_bwd, rmsnorm_fwd, "
                          "add_rmsnorm_fwd, rmsnorm_bwd, rope_fwd, residual_add, attn_fwd, attn_bwd; "
                          "embedding_fwd, embedding_bwd; gemm_<nt|nn|tn>_<qkv|o|gate_up|down> "
-                         "(fh_gemm_bf16 at that projection GEMM); "
+                         "(fh_gemm_bf16 at that projection GEMM; libgemm_...: the library GEMM); "
                          "adamw: one optimizer step over the workload's parameter shapes; "
                          "chain_cfg2: BASELINE config 2's memory-bound chain, each launch after a "
                          "MALL-evicting read) at "
@@ -636,15 +636,21 @@ def profile_kernel(torch, name: str, c: dict, launches: int = 10) -> dict:
             dys = [rnd(T, H) for _ in range(n)]
             fn = lambda i: ops.embedding_bwd(dys[i], ids, V)
             nbytes = 2 * T * H + 2 * V * H + 8 * T
-    elif name.startswith("gemm_"):
-        _, op, proj = name.split("_", 2)
+    elif name.startswith("gemm_") or name.startswith("libgemm_"):
+        # gemm_<op>_<proj>: fh_gemm_bf16; libgemm_<op>_<proj>: the library GEMM
+        # (torch.mm, with the shipped TunableOp solutions) at the same shape
+        lib_, op, proj = name.split("_", 2)
         n_out, k_in = {"qkv": (Hq + 2 * Hkv, H), "o": (H, Hq), "gate_up": (2 * F, H),
                        "down": (H, F)}[proj]
         xs = [rnd(T, k_in) for _ in range(2)]
         ws = [rnd(n_out, k_in) for _ in range(2)]
         dys = [rnd(T, n_out) for _ in range(2)]
         operands = {"nt": (xs, ws), "nn": (dys, ws), "tn": (dys, xs)}[op]
-        fn = lambda i: ops.gemm(op, operands[0][i % 2], operands[1][i % 2])
+        if lib_ == "libgemm":
+            mm = {"nt": lambda a, b: torch.mm(a, b.t()), "nn": torch.mm, "tn": lambda a, b: torch.mm(a.t(), b)}[op]
+            fn = lambda i: mm(operands[0][i % 2], operands[1][i % 2])
+        else:
+            fn = lambda i: ops.gemm(op, operands[0][i % 2], operands[1][i % 2])
         nbytes = None  # MFMA-bound: 2*T*n_out*k_in FLOP per launch
     elif name == "chain_cfg2":
         # BASELINE config 2's memory-bound chain, each kernel `launches` times,
