@@ -178,9 +178,30 @@ def measured_traffic(kernel: str):
         return None
 
 
-def event_ms(torch, fn, iters: int) -> float:
-    """Mean launch time of fn() with HIP events on the current (launch) stream."""
+def warm_up(torch, fn, ms: float = 40.0) -> None:
+    """Launch fn() back to back for about `ms` milliseconds: under MFMA load
+    the shader clock takes tens of milliseconds to settle (a cold first batch
+    of attention-forward launches measured 225 us each, the same launches
+    after 60 ms 176 us), so a kernel timed right after other work would be
+    timed partly at a lower clock than it runs at inside the step."""
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
     fn()
+    end.record(stream)
+    end.synchronize()
+    n = max(1, int(ms / max(start.elapsed_time(end), 1e-3)))
+    for _ in range(n):
+        fn()
+    torch.cuda.synchronize()
+
+
+def event_ms(torch, fn, iters: int, warm: bool = False) -> float:
+    """Mean launch time of fn() with HIP events on the current (launch) stream
+    (after warm_up() when `warm`)."""
+    fn()
+    if warm:
+        warm_up(torch, fn)
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
@@ -345,13 +366,13 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True,
     # the recompute's form: q rotated on load and written out rotated for the backward
     q_rot = torch.empty_like(q)
     ms_f = event_ms(torch, lambda i=0: ops.attn_fwd(q, k, v, B, S, nh, nkv, hd, hd ** -0.5, rope=(cos, sin),
-                                                      q_out=q_rot), iters)
+                                                      q_out=q_rot), iters, warm=True)
     do = rnd(T, Hq)
     dqkv = torch.empty_like(qkv)
     ms_b = event_ms(torch, lambda i=0: ops.attn_bwd(q, k, v, o, do, lse, dqkv[:, :Hq], dqkv[:, Hq:Hq + Hkv],
                                                       dqkv[:, Hq + Hkv:], B, S, nh, nkv, hd, hd ** -0.5,
                                                       rope=(cos, sin)),
-                    max(3, iters // 4))
+                    iters, warm=True)
     # backward: dK/dV kernel 4 products + dQ kernel 3 products (the dQ kernel
     # recomputes S and dP); algorithmic = the 5 products of attention backward
     bwd_flop = 2.5 * fwd_flop
@@ -369,10 +390,10 @@ def kernel_table(torch, c: dict, iters: int, ac: str, boundary: bool = True,
     def sdpa(a, b_, c_):
         return Fn.scaled_dot_product_attention(a, b_, c_, is_causal=True, scale=hd ** -0.5, enable_gqa=gqa)
 
-    lib_f = event_ms(torch, lambda i=0: sdpa(qh, kh, vh), iters)
+    lib_f = event_ms(torch, lambda i=0: sdpa(qh, kh, vh), iters, warm=True)
     qg, kg, vg = (t.detach().requires_grad_(True) for t in (qh, kh, vh))
     lib_fb = event_ms(torch, lambda i=0: torch.autograd.grad(sdpa(qg, kg, vg), (qg, kg, vg), doh),
-                      max(3, iters // 4))
+                      max(3, iters // 4), warm=True)
     lib_b = max(lib_fb - lib_f, 1e-6)
     del qh, kh, vh, doh, qg, kg, vg
     lib_note = "torch.nn.functional.scaled_dot_product_attention(is_causal=True, enable_gqa) at the same shape"
@@ -541,8 +562,8 @@ def projection_gemm_rows(torch, c: dict, iters: int, sel: bool, fused_attention:
         for op, a, b, lib, per_layer in (("nt", x, w, lambda: torch.mm(x, w.t()), fwd_per_layer),
                                          ("nn", dy, w, lambda: torch.mm(dy, w), 1),
                                          ("tn", dy, x, lambda: torch.mm(dy.t(), x), 1)):
-            ms_hand = event_ms(torch, lambda i=0: ops.gemm(op, a, b), iters)
-            ms_lib = event_ms(torch, lambda i=0: lib(), iters)
+            ms_hand = event_ms(torch, lambda i=0: ops.gemm(op, a, b), iters, warm=True)
+            ms_lib = event_ms(torch, lambda i=0: lib(), iters, warm=True)
             hand = projections.gemm_policy() != "library" and (
                 projections.gemm_policy() == "hand"
                 or ops.gemm_dims(op, a, b) not in projections._library_shapes()[op])
@@ -949,7 +970,7 @@ def main() -> int:
     for r in mfma:
         r["ms_per_step"] = round(r["ms_per_launch"] * r["launches_per_step"], 4)
     timing = (f"mean of {args.kernel_iters} back-to-back launches alone at the step's shape, HIP events "
-              "on the launch stream (fused_kernels_hbm rows: ms_per_launch is the kernels' own execution "
+              "on the launch stream, after ~40 ms of launches that let the clock settle (fused_kernels_hbm rows: ms_per_launch is the kernels' own execution "
               "time from torch.profiler device timestamps, event_ms_per_launch the HIP-event mean)")
     dom = max(rows, key=lambda r: r["ms_per_step"])
     ev_gbs = dom["bytes_per_launch"] / (dom["event_ms_per_launch"] * 1e-3) / 1e9
