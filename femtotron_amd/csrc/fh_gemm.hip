@@ -159,34 +159,57 @@ __device__ __forceinline__ bf16x8 frag_ko16(const char* tile, int t0, int t4, in
 // any LDS read); the kernel waits for its loads itself (s_waitcnt vmcnt) before
 // the barrier that hands a stage to the other waves.
 
-// Run jj (0..7) of wave q's quarter of an operand's stage, into its 1 KB slot
-// (8q + jj) of the stage's tile at `dst`.  KC: tile rows 64q + 8jj .. +7
+// Wave q's quarter of one operand's stage is 8 runs jj, each one 1 KB load
+// into slot (8q + jj) of the stage's tile.  KC: tile rows 64q + 8jj .. +7
 // (clamped to `last`), k0 .. k0+63: lane i fills 16-byte slot i%8 of row i/8,
 // i.e. it loads the chunk the swizzle puts there.  KO: sub-tile q, k rows
 // k0 + 8jj .. +7, columns o0 + 64q .. +63 (chunks clamped to `last`, the last
-// 8-column chunk start).  The address is a wave-uniform 64-bit base (clamped
-// too, so the lane offset is never negative) plus a 32-bit lane offset
-// (leading dims < 2^26 keep it in range).
+// 8-column chunk start).  A load's address is a wave-uniform 64-bit base
+// (clamped too, so the lane offset is never negative) plus a 32-bit lane offset
+// (leading dims < 2^26 keep it in range).  The plan holds, per tile, each run's
+// base without the k offset and the lane offsets, so that a load in the loop
+// costs one 64-bit scalar add of the stage's k offset (k0 elements for KC, k0
+// rows for KO); recomputing (k0 + 8jj) * ld for every KO load put a 64-bit
+// scalar multiply chain in front of each one, ~180 cycles per stage and KO
+// operand.  A KO lane offset depends on the run through the swizzle only,
+// which repeats every two runs.
 template <bool KO>
-__device__ __forceinline__ void dma_one(const uint16_t* base, int64_t ld, int o0, int last, int k0, int q,
-                                        char* dst, int lane, int jj) {
-  typedef __attribute__((address_space(3))) char* lptr;
-  const int lr = lane >> 3;
-  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lptr)dst));
-  const int c = (lane & 7) ^ swz<64>(8 * jj + lr);
-  const char* sp;
-  uint32_t off;
-  if constexpr (KO) {
-    const int col0 = min(o0 + 64 * q, last);
-    sp = reinterpret_cast<const char*>(base + static_cast<int64_t>(k0 + 8 * jj) * ld + col0);
-    off = static_cast<uint32_t>(lr * static_cast<int>(ld) + min(o0 + 64 * q + 8 * c, last) - col0) * 2u;
-  } else {
-    const int row0 = min(o0 + 64 * q + 8 * jj, last);
-    sp = reinterpret_cast<const char*>(base + static_cast<int64_t>(row0) * ld + k0);
-    off = static_cast<uint32_t>((min(o0 + 64 * q + 8 * jj + lr, last) - row0) * static_cast<int>(ld) + 8 * c) * 2u;
+struct RunPlan {
+  const char* run[8];
+  uint32_t off[KO ? 2 : 8];
+  int64_t k_bytes;  // bytes per k (KO: a row, ld elements; KC: one element)
+
+  __device__ __forceinline__ void init(const uint16_t* base, int64_t ld, int o0, int last, int q, int lane) {
+    const int lr = lane >> 3;
+    if constexpr (KO) {
+      const int col0 = min(o0 + 64 * q, last);
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj)
+        run[jj] = reinterpret_cast<const char*>(base + static_cast<int64_t>(8 * jj) * ld + col0);
+#pragma unroll
+      for (int par = 0; par < 2; ++par) {
+        const int c = (lane & 7) ^ swz<64>(8 * par + lr);
+        off[par] = static_cast<uint32_t>(lr * static_cast<int>(ld) + min(o0 + 64 * q + 8 * c, last) - col0) * 2u;
+      }
+      k_bytes = ld * 2;
+    } else {
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const int row0 = min(o0 + 64 * q + 8 * jj, last);
+        const int c = (lane & 7) ^ swz<64>(8 * jj + lr);
+        run[jj] = reinterpret_cast<const char*>(base + static_cast<int64_t>(row0) * ld);
+        off[jj] = static_cast<uint32_t>((min(o0 + 64 * q + 8 * jj + lr, last) - row0) * static_cast<int>(ld) + 8 * c) * 2u;
+      }
+      k_bytes = 2;
+    }
   }
-  dma16(off, sp, lds0 + (8 * q + jj) * 1024);
-}
+
+  // Run jj of the stage k_off bytes along k (k0 * k_bytes) into the LDS
+  // slot at byte address lds_slot.
+  __device__ __forceinline__ void load(int64_t k_off, int jj, uint32_t lds_slot) const {
+    dma16(off[KO ? (jj & 1) : jj], run[jj] + k_off, lds_slot);
+  }
+};
 
 __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
@@ -234,20 +257,22 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* ring, int t, 
   int m0, n0;
   tile_origin(g, t, m0, n0);
 
+  RunPlan<A_KO> pa;
+  RunPlan<B_KO> pb;
+  pa.init(g.a, g.lda, m0, A_KO ? g.m - 8 : g.m - 1, wave, lane);
+  pb.init(g.b, g.ldb, n0, B_KO ? g.n - 8 : g.n - 1, wave, lane);
+  typedef __attribute__((address_space(3))) char* lptr;
+  const uint32_t ring0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lptr)ring)) + wave * 8192;
+
   // Run jj of wave `wave`'s quarter of operand OP (0: A, 1: B) of stage
   // `step` into ring slot `slot`.  Stages past the slice's end re-load its
   // last stage (in bounds, never used): the loop has no branches.
   auto dma = [&](auto op_tag, int step, int slot, int jj) __attribute__((always_inline)) {
     constexpr int OP = decltype(op_tag)::value;
-    const int k0 = (s_begin + min(step, nst - 1)) * kTk;
-    char* dst = ring + slot * kSlot;
-    if constexpr (OP == 0) {
-      if constexpr (A_KO) dma_one<true>(g.a, g.lda, m0, g.m - 8, k0, wave, dst, lane, jj);
-      else dma_one<false>(g.a, g.lda, m0, g.m - 1, k0, wave, dst, lane, jj);
-    } else {
-      if constexpr (B_KO) dma_one<true>(g.b, g.ldb, n0, g.n - 8, k0, wave, dst, lane, jj);
-      else dma_one<false>(g.b, g.ldb, n0, g.n - 1, k0, wave, dst, lane, jj);
-    }
+    const int64_t k0 = static_cast<int64_t>(s_begin + min(step, nst - 1)) * kTk;
+    const uint32_t lds_slot = ring0 + slot * kSlot + jj * 1024;
+    if constexpr (OP == 0) pa.load(k0 * pa.k_bytes, jj, lds_slot);
+    else pb.load(k0 * pb.k_bytes, jj, lds_slot);
   };
   using OpA = std::integral_constant<int, 0>;
   using OpB = std::integral_constant<int, 1>;
