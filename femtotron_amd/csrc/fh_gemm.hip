@@ -22,15 +22,20 @@
 // multiplied and are spread over its 128 MFMAs: the load instructions issue at
 // ~1 KB per 16 cycles per CU, and a burst of them right after a barrier would
 // hold up the MFMAs behind it.  Fragments are read from LDS one k32 step ahead
-// of the MFMAs that use them.  Tiles are XOR-swizzled so that both read
-// patterns are free of bank conflicts:
+// of the MFMAs that use them.  The two tile layouts keep their read
+// patterns free of bank conflicts:
 //   * an operand with K contiguous ("KC": A of NT/NN, B of NT) is stored as
 //     its [256 x 64] tile; a fragment is one ds_read_b128 per lane (row i%16,
 //     k 8*(i/16)..+7 of the k32 step);
 //   * an operand with K as the outer index ("KO": B of NN, both of TN) is
-//     stored as four [64 k x 64] sub-tiles; a fragment is two
-//     ds_read_b64_tr_b16 transposing reads that deliver the same natural K
-//     order, so any two operands can be paired.
+//     stored as four [64 k x 64] sub-tiles of eight 1 KB units (8 k rows),
+//     each unit four 256-byte blocks of 16 columns (row r's 32 bytes at 32 r:
+//     no swizzle); a fragment is two ds_read_b64_tr_b16 transposing reads
+//     that deliver the same natural K order, so any two operands can be
+//     paired.  A quarter-wave's read covers 128 contiguous bytes (full LDS
+//     rate: 4 cycles per read and wave, against 4.8 with the 64-column rows
+//     XOR-swizzled), and a fragment's address is one per-lane offset plus
+//     immediates.
 // The MFMA is issued as (B fragment, A fragment), so each lane's four
 // accumulator values are consecutive along n (C's contiguous index).  The finished tile goes through LDS so that
 // every global store writes whole rows.
@@ -132,24 +137,22 @@ __device__ __forceinline__ bf16x8 frag_kc16(const char* tile, int a_off, int o, 
   return *reinterpret_cast<const bf16x8*>(tile + o * 128 + (a_off ^ (64 * ks)));
 }
 
-// 16x16x32 KO fragment lane offset: quarter-wave q = i/16 reads k rows
-// 8 q + plus4 + 0..3 of a 16-column block (lane L = i%16: 8 bytes of row L/4,
-// columns 4 (L%4) .. +3), so that lane i gets column i%16, k 8 q .. 8 q + 7
-// over the two reads, as a KC fragment holds them.
-__device__ __forceinline__ int lane_off_tr16(int lane, int plus4) {
+// 16x16x32 KO fragment lane offset: quarter-wave q = i/16 reads unit q of the
+// k32 step (k rows 8 q .. 8 q + 7) and in it rows plus4 + 0..3 of a 16-column
+// block (lane L = i%16: 8 bytes of row L/4, columns 4 (L%4) .. +3), so that
+// lane i gets column i%16, k 8 q .. 8 q + 7 over the two reads, as a KC
+// fragment holds them.  The reads with plus4 = 4 are 128 bytes further.
+__device__ __forceinline__ int lane_off_tr16(int lane) {
   const int q = lane >> 4, L = lane & 15;
-  const int r = 8 * q + (L >> 2) + plus4;
-  const int cb = (L & 3) >> 1;
-  return r * 128 + ((cb ^ swz<64>(r)) << 4) + 8 * (L & 1);
+  return q * 1024 + (2 * (L >> 2) + ((L & 3) >> 1)) * 16 + 8 * (L & 1);
 }
 
-// KO fragment: columns o..o+15 (o a multiple of 16) of the four [64 k x 64]
-// sub-tiles, k rows 32 ks .. 32 ks + 31.
-__device__ __forceinline__ bf16x8 frag_ko16(const char* tile, int t0, int t4, int o, int ks) {
-  const char* t = tile + (o >> 6) * kSubBytes + ks * 32 * 128;
-  const int x = 32 * ((o >> 4) & 3);  // the block's first chunk, 2 ((o % 64) / 16), as a byte XOR
-  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + (t0 ^ x)));
-  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + (t4 ^ x)));
+// KO fragment: columns o..o+15 (o a multiple of 16, block (o % 64) / 16 of
+// sub-tile o / 64), k rows 32 ks .. 32 ks + 31 (units 4 ks .. 4 ks + 3).
+__device__ __forceinline__ bf16x8 frag_ko16(const char* tile, int t0, int o, int ks) {
+  const char* t = tile + (o >> 6) * kSubBytes + ks * 4096 + ((o >> 4) & 3) * 256 + t0;
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)t);
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + 128));
   const uint2 ulo = __builtin_bit_cast(uint2, lo), uhi = __builtin_bit_cast(uint2, hi);
   return as_bf16x8(make_uint4(ulo.x, ulo.y, uhi.x, uhi.y));
 }
@@ -162,37 +165,34 @@ __device__ __forceinline__ bf16x8 frag_ko16(const char* tile, int t0, int t4, in
 // Wave q's quarter of one operand's stage is 8 runs jj, each one 1 KB load
 // into slot (8q + jj) of the stage's tile.  KC: tile rows 64q + 8jj .. +7
 // (clamped to `last`), k0 .. k0+63: lane i fills 16-byte slot i%8 of row i/8,
-// i.e. it loads the chunk the swizzle puts there.  KO: sub-tile q, k rows
-// k0 + 8jj .. +7, columns o0 + 64q .. +63 (chunks clamped to `last`, the last
-// 8-column chunk start).  A load's address is a wave-uniform 64-bit base
+// i.e. it loads the chunk the swizzle puts there.  KO: unit jj of sub-tile q,
+// k rows k0 + 8jj .. +7, columns o0 + 64q .. +63 (chunks clamped to `last`,
+// the last 8-column chunk start): lane i fills 16-byte slot i%16 of block
+// i/16, i.e. chunk i%2 of that block's 32 bytes of row (i%16)/2.  A load's address is a wave-uniform 64-bit base
 // (clamped too, so the lane offset is never negative) plus a 32-bit lane offset
 // (leading dims < 2^26 keep it in range).  The plan holds, per tile, each run's
 // base without the k offset and the lane offsets, so that a load in the loop
 // costs one 64-bit scalar add of the stage's k offset (k0 elements for KC, k0
 // rows for KO); recomputing (k0 + 8jj) * ld for every KO load put a 64-bit
 // scalar multiply chain in front of each one, ~180 cycles per stage and KO
-// operand.  A KO lane offset depends on the run through the swizzle only,
-// which repeats every two runs.
+// operand.  A KO lane offset is the same for every run.
 template <bool KO>
 struct RunPlan {
   const char* run[8];
-  uint32_t off[KO ? 2 : 8];
+  uint32_t off[KO ? 1 : 8];
   int64_t k_bytes;  // bytes per k (KO: a row, ld elements; KC: one element)
 
   __device__ __forceinline__ void init(const uint16_t* base, int64_t ld, int o0, int last, int q, int lane) {
-    const int lr = lane >> 3;
     if constexpr (KO) {
       const int col0 = min(o0 + 64 * q, last);
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj)
         run[jj] = reinterpret_cast<const char*>(base + static_cast<int64_t>(8 * jj) * ld + col0);
-#pragma unroll
-      for (int par = 0; par < 2; ++par) {
-        const int c = (lane & 7) ^ swz<64>(8 * par + lr);
-        off[par] = static_cast<uint32_t>(lr * static_cast<int>(ld) + min(o0 + 64 * q + 8 * c, last) - col0) * 2u;
-      }
+      const int r = (lane >> 1) & 7, c = 2 * (lane >> 4) + (lane & 1);
+      off[0] = static_cast<uint32_t>(r * static_cast<int>(ld) + min(o0 + 64 * q + 8 * c, last) - col0) * 2u;
       k_bytes = ld * 2;
     } else {
+      const int lr = lane >> 3;
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) {
         const int row0 = min(o0 + 64 * q + 8 * jj, last);
@@ -207,7 +207,7 @@ struct RunPlan {
   // Run jj of the stage k_off bytes along k (k0 * k_bytes) into the LDS
   // slot at byte address lds_slot.
   __device__ __forceinline__ void load(int64_t k_off, int jj, uint32_t lds_slot) const {
-    dma16(off[KO ? (jj & 1) : jj], run[jj] + k_off, lds_slot);
+    dma16(off[KO ? 0 : jj], run[jj] + k_off, lds_slot);
   }
 };
 
@@ -282,7 +282,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* ring, int t, 
   // accumulators of 16 x 16; a stage is two k32 steps of 64 MFMAs.  Operand
   // lane i holds row/column i%16 and k 8*(i/16) .. +7 of the step.
   const int a_off = lane_off_kc16(lane);
-  const int t0 = lane_off_tr16(lane, 0), t4 = lane_off_tr16(lane, 4);
+  const int t0 = lane_off_tr16(lane);
   bf16x8 fa[2][8], fb[2][8];
   // Fragment r = 0..15 of k32 step ks (order B0, A0..A7, B1..B7: the order
   // the MFMAs first use them) from slots sa (A) and sb (B).
@@ -290,11 +290,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* ring, int t, 
     if (r >= 1 && r <= 8) {
       const char* tile = ring + sa * kSlot;
       const int j = r - 1, o = 128 * wm + 16 * j;
-      fa[buf][j] = A_KO ? frag_ko16(tile, t0, t4, o, ks) : frag_kc16(tile, a_off, o, ks);
+      fa[buf][j] = A_KO ? frag_ko16(tile, t0, o, ks) : frag_kc16(tile, a_off, o, ks);
     } else {
       const char* tile = ring + sb * kSlot;
       const int i = r == 0 ? 0 : r - 8, o = 128 * wn + 16 * i;
-      fb[buf][i] = B_KO ? frag_ko16(tile, t0, t4, o, ks) : frag_kc16(tile, a_off, o, ks);
+      fb[buf][i] = B_KO ? frag_ko16(tile, t0, o, ks) : frag_kc16(tile, a_off, o, ks);
     }
   };
   f32x4 acc[8][8];
