@@ -59,6 +59,10 @@
 namespace fh {
 namespace {
 
+#ifndef FH_GEMM_PERSIST
+#define FH_GEMM_PERSIST 1  // whole-K GEMMs with plain stores in the persistent form
+#endif
+
 constexpr int kTm = 256, kTn = 256, kTk = 64;  // block tile and stage depth
 constexpr int kSubBytes = kTk * 128;           // KO sub-tile: [64 k x 64] bf16
 
@@ -122,6 +126,14 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // after the last one) with s_nop.
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  return c;
+}
+
+// The first MFMA of an accumulator: C = 0 as an inline constant, so the
+// accumulators need no zeroing by VALU writes.
+__device__ __forceinline__ f32x4 mfma16z(bf16x8 a, bf16x8 b) {
+  f32x4 c;
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
   return c;
 }
 
@@ -487,6 +499,183 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* ring, int t, 
   }
 }
 
+// Lane offsets (bytes) of the 8 runs of wave q's quarter of an operand's
+// stage in a whole tile (no clamping), relative to the wave's base: the
+// operand at row (KC) or column (KO) o0 + 64q, k 0.  The same as RunPlan's
+// (KC: row 8jj + lane/8, the chunk the swizzle puts in slot lane%8; KO: k row
+// 8jj + (lane%16)/2, chunk 2 (lane/16) + lane%2), so the tiles agree.  Leading
+// dims below 2^24 keep them in range.
+template <bool KO>
+__device__ __forceinline__ void whole_run_offsets(int64_t ld, int lane, uint32_t (&off)[8]) {
+  const uint32_t l = static_cast<uint32_t>(ld);
+  if constexpr (KO) {
+    const int r = (lane >> 1) & 7, c = 2 * (lane >> 4) + (lane & 1);
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) off[jj] = (static_cast<uint32_t>(8 * jj + r) * l + 8u * c) * 2u;
+  } else {
+    const int lr = lane >> 3;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const int c = (lane & 7) ^ swz<64>(8 * jj + lr);
+      off[jj] = (static_cast<uint32_t>(8 * jj + lr) * l + 8u * c) * 2u;
+    }
+  }
+}
+
+// Wave q's base (bytes) of an operand in the tile at o0 (rows for KC,
+// columns for KO).
+template <bool KO>
+__device__ __forceinline__ const char* whole_base(const uint16_t* base, int64_t ld, int o0, int q) {
+  return reinterpret_cast<const char*>(base + (KO ? static_cast<int64_t>(o0 + 64 * q)
+                                                   : static_cast<int64_t>(o0 + 64 * q) * ld));
+}
+
+// Persistent whole-K form with plain stores (no residual, no rotation; K of
+// at least two stages; m and n multiples of the tile; more tiles than
+// workgroups): one workgroup per CU runs tiles lid, lid + G, lid + 2G, ... of
+// the G workgroups (in k_gemm's XCD order).  The ring runs on across tiles:
+// the loads issued in a tile's last two stages bring the next tile's first two,
+// and
+// the output goes from the accumulators straight to global memory (8
+// consecutive columns per lane and store, gathered by a lane swap), with no
+// LDS staging.  So the next tile's operands land while the epilogue runs, and
+// its first stage needs no prologue.  Against one workgroup per tile
+// this saves, per tile, the prologue (two stages loaded and the first waited
+// for), the output's round trip through LDS with its barriers, and the gap
+// between a CU's consecutive workgroups.
+template <bool A_KO, bool B_KO>
+__device__ __forceinline__ void gemm_persist(const GemmArgs& g, char* ring, int lid) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int nst = g.total_steps;
+  int t = lid, m0, n0;
+  tile_origin(g, t, m0, n0);
+  uint32_t offa[8], offb[8];
+  whole_run_offsets<A_KO>(g.lda, lane, offa);
+  whole_run_offsets<B_KO>(g.ldb, lane, offb);
+  const int64_t kba = A_KO ? g.lda * 2 : 2, kbb = B_KO ? g.ldb * 2 : 2;  // bytes per k
+  const char* ba = whole_base<A_KO>(g.a, g.lda, m0, wave);
+  const char* bb = whole_base<B_KO>(g.b, g.ldb, n0, wave);
+  typedef __attribute__((address_space(3))) char* lptr;
+  const uint32_t ring0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lptr)ring)) + wave * 8192;
+
+  const int wm16 = 128 * wm, wn16 = 128 * wn;
+  const int a_off = lane_off_kc16(lane);
+  const int t0 = lane_off_tr16(lane);
+  bf16x8 fa[2][8], fb[2][8];
+  auto rd1 = [&](int sa, int sb, int ks, int buf, int r) __attribute__((always_inline)) {
+    if (r >= 1 && r <= 8) {
+      const char* tile = ring + sa * kSlot;
+      const int j = r - 1, o = wm16 + 16 * j;
+      fa[buf][j] = A_KO ? frag_ko16(tile, t0, o, ks) : frag_kc16(tile, a_off, o, ks);
+    } else {
+      const char* tile = ring + sb * kSlot;
+      const int i = r == 0 ? 0 : r - 8, o = wn16 + 16 * i;
+      fb[buf][i] = B_KO ? frag_ko16(tile, t0, o, ks) : frag_kc16(tile, a_off, o, ks);
+    }
+  };
+  f32x4 acc[8][8];
+  auto mf1 = [&](int buf, int nn) __attribute__((always_inline)) {
+    const int i = nn >> 3, j = nn & 7;
+    acc[i][j] = mfma16(fb[buf][i], fa[buf][j], acc[i][j]);
+  };
+
+  // Prologue of the first tile (as gemm_tile's).
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) dma16(offa[jj], ba, ring0 + 0 * kSlot + jj * 1024);
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) dma16(offb[jj], bb, ring0 + 1 * kSlot + jj * 1024);
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) dma16(offa[jj], ba + kTk * kba, ring0 + 2 * kSlot + jj * 1024);
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) dma16(offb[jj], bb + kTk * kbb, ring0 + 3 * kSlot + jj * 1024);
+  wait_vm_n<16>();
+  bar();
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    rd1(0, 1, 0, 0, r);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  int s = 0;  // ring slot of the current stage's A (stage x: A in s, B in s+1)
+  for (;;) {
+    const int tn = t + g.grid;
+    const bool more = tn < g.tiles;
+    int m1 = m0, n1 = n0;
+    if (more) tile_origin(g, tn, m1, n1);
+    const char* na = whole_base<A_KO>(g.a, g.lda, m1, wave);
+    const char* nb = whole_base<B_KO>(g.b, g.ldb, n1, wave);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // Stage x (as gemm_tile's): the loads issued in it are stage x + 2's, of
+    // this tile, of the next, or past the last tile's end (its last stage
+    // again: in bounds, never used).
+    for (int x = 0; x < nst; ++x) {
+      const int sB = mod5(s + 1), nA = mod5(s + 2), nB = mod5(s + 3), fA = mod5(s + 4);
+      const bool ahead = more && x + 2 >= nst;
+      const int64_t k2 = static_cast<int64_t>(ahead ? x + 2 - nst : min(x + 2, nst - 1)) * kTk;
+      const char* srcA = (ahead ? na : ba) + k2 * kba;
+      const char* srcB = (ahead ? nb : bb) + k2 * kbb;
+      const uint32_t dA = ring0 + fA * kSlot, dB = ring0 + s * kSlot;
+      asm volatile("s_nop 4");
+#pragma unroll
+      for (int p = 0; p < 64; ++p) {
+        if ((p & 3) == 0) rd1(s, sB, 1, 1, p >> 2);
+        if ((p & 7) == 2) dma16(offa[p >> 3], srcA, dA + (p >> 3) * 1024);
+        mf1(0, p);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      wait_lds();
+      wait_vm_n<8>();
+      bar();
+#pragma unroll
+      for (int p = 0; p < 64; ++p) {
+        if ((p & 3) == 0) rd1(nA, nB, 0, 0, p >> 2);
+        if ((p & 7) == 2) dma16(offb[p >> 3], srcB, dB + (p >> 3) * 1024);
+        mf1(1, p);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      s = nA;
+      // MFMA results need wait states before the epilogue reads them.
+      if (x == nst - 1) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // Lane i of accumulator (i, j) holds row 128 wm + 16 j + i%16, columns
+    // 128 wn + 16 i + 4 g .. +3 (g = i/16, its row of 16 lanes).  For a pair
+    // of accumulators (i, i+1), one v_permlane16_swap per dword trades the
+    // odd rows' block-i columns for the even rows' block-(i+1) columns, after
+    // which lane g holds 8 consecutive columns, 8 (g/2) .. +7 of block
+    // i + g%2: one 16-byte store (64 contiguous bytes per row and store).
+    // The form runs whole tiles only.
+    uint16_t* cp = g.c + static_cast<int64_t>(m0 + wm16 + (lane & 15)) * g.ldc + n0 + wn16 +
+                   16 * ((lane >> 4) & 1) + 8 * (lane >> 5);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 v0 = acc[2 * q][j], v1 = acc[2 * q + 1][j];
+        const auto lo = __builtin_amdgcn_permlane16_swap(pk_bf16(v0[0], v0[1]), pk_bf16(v1[0], v1[1]), false, false);
+        const auto hi = __builtin_amdgcn_permlane16_swap(pk_bf16(v0[2], v0[3]), pk_bf16(v1[2], v1[3]), false, false);
+        *reinterpret_cast<uint4*>(cp + static_cast<int64_t>(16 * j) * g.ldc + 32 * q) =
+            make_uint4(lo[0], hi[0], lo[1], hi[1]);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+    if (!more) break;
+    t = tn;
+    m0 = m1;
+    n0 = n1;
+    ba = na;
+    bb = nb;
+  }
+  // The loads past the last tile's end land before the workgroup's LDS is
+  // released.
+  wait_vm();
+  wait_lds();
+}
+
 // One tile, or one K slice of a tile (EPI_PARTIAL), per workgroup; or the
 // stream form (EPI_STREAM): the workgroup runs its whole tiles, then its share
 // of the tail's k-steps as segments of one tile each.  A tail segment that is not a whole tile goes to
@@ -543,6 +732,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     gemm_tile<A_KO, B_KO, EPI>(g, ring, t, s_begin, min(g.total_steps - s_begin, g.steps_per_slice), pdst,
                                g.n, EPI == EPI_PARTIAL);
   }
+}
+
+// The persistent form (gemm_persist): G = gridDim.x workgroups, a multiple of
+// 8, at most the number of tiles.
+template <bool A_KO, bool B_KO>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_gemm_persist(GemmArgs g) {
+  __shared__ __align__(16) char ring[kRing * kSlot];
+  const int nb8 = gridDim.x >> 3;
+  gemm_persist<A_KO, B_KO>(g, ring, (blockIdx.x & 7) * nb8 + (blockIdx.x >> 3));
 }
 
 // Rows blockIdx.y * 16 .. +15 of tail tile blockIdx.x of a stream GEMM: if
@@ -806,6 +1004,18 @@ int gemm_run(int op, GemmArgs& g, int slices, bool stream_form, void* workspace,
     return FH_OK;
   }
   g.steps_per_slice = (g.total_steps + slices - 1) / slices;
+#if FH_GEMM_PERSIST
+  if (slices == 1 && g.r == nullptr && g.rope.cos == nullptr && g.total_steps >= 2 && g.m % kTm == 0 &&
+      g.n % kTn == 0 && g.lda < (int64_t(1) << 24) && g.ldb < (int64_t(1) << 24) && g.tiles > stream_grid()) {
+    g.grid = stream_grid();
+    switch (op) {
+      case FH_GEMM_NT: hipLaunchKernelGGL((k_gemm_persist<false, false>), dim3(g.grid), dim3(256), 0, stream, g); break;
+      case FH_GEMM_NN: hipLaunchKernelGGL((k_gemm_persist<false, true>), dim3(g.grid), dim3(256), 0, stream, g); break;
+      default: hipLaunchKernelGGL((k_gemm_persist<true, true>), dim3(g.grid), dim3(256), 0, stream, g); break;
+    }
+    return FH_OK;
+  }
+#endif
   const int64_t logical = static_cast<int64_t>(g.tiles) * slices;
   FH_REQUIRE(logical <= 0x7ffffff0, "gemm_bf16: grid too large");
   g.grid = static_cast<int>(logical);
