@@ -641,6 +641,7 @@ struct DkdvFusedTiles {
 // One wave's share of a query tile in the dK/dV kernel: the 32 queries at
 // row hrow of the LDS tiles Q and dO (first query qh) against the wave's 32
 // keys (first key kw, this lane's key ki), accumulated into dK^T and dV^T.
+// The lane offsets a_off, b0, b8 already include row hrow.
 template <int HD>
 __device__ __forceinline__ void dkdv_tile(const char* Q, const char* G, const float* sl, const float* sd,
                                           const bf16x8 (&kf)[HD / 16], const bf16x8 (&vf)[HD / 16],
@@ -654,8 +655,8 @@ __device__ __forceinline__ void dkdv_tile(const char* Q, const char* G, const fl
   __builtin_amdgcn_iglp_opt(0);
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    x = mfma(lds_frag<HD>(Q, a_off, hrow, s), kf[s], x);
-    y = mfma(lds_frag<HD>(G, a_off, hrow, s), vf[s], y);
+    x = mfma(lds_frag<HD>(Q, a_off, 0, s), kf[s], x);
+    y = mfma(lds_frag<HD>(G, a_off, 0, s), vf[s], y);
   }
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
@@ -689,8 +690,8 @@ __device__ __forceinline__ void dkdv_tile(const char* Q, const char* G, const fl
     const bf16x8 df = pack_frag(y, 8 * s2);
 #pragma unroll
     for (int dt = 0; dt < ND; ++dt) {
-      dvacc[dt] = mfma(lds_frag_tr<HD>(G, b0, b8, hrow + 16 * s2, dt), pf, dvacc[dt]);
-      dkacc[dt] = mfma(lds_frag_tr<HD>(Q, b0, b8, hrow + 16 * s2, dt), df, dkacc[dt]);
+      dvacc[dt] = mfma(lds_frag_tr<HD>(G, b0, b8, 16 * s2, dt), pf, dvacc[dt]);
+      dkacc[dt] = mfma(lds_frag_tr<HD>(Q, b0, b8, 16 * s2, dt), df, dkacc[dt]);
     }
   }
 }
@@ -709,9 +710,24 @@ __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves
   // Two LDS stages as separate arrays: the loop is unrolled by two, so every
   // access names its stage statically and the compiler can tell that the
   // direct-to-LDS loads into one stage do not alias the reads of the other.
-  __shared__ __align__(16) char sq0[TILE], sq1[TILE], sg0[TILE], sg1[TILE];
-  __shared__ __align__(16) float sl0[BQ], sl1[BQ], sd0[BQ], sd1[BQ];  // -lse*log2(e) and delta
-  __shared__ __align__(16) float xchg[2][NWH][ND * 16][64];  // [0]: dV of half 0, [1]: dK of half 1
+  // One struct fixes the layout: the tiles the loop reads first, below 64 KB,
+  // so that their base is a read's immediate offset (placed after the 64 KB
+  // exchange buffer, every tile read added its base in a VGPR).
+  struct Lds {
+    char sq0[TILE], sq1[TILE], sg0[TILE], sg1[TILE];
+    float sl0[BQ], sl1[BQ], sd0[BQ], sd1[BQ];  // -lse*log2(e) and delta
+    float xchg[2][NWH][ND * 16][64];           // [0]: dV of half 0, [1]: dK of half 1
+  };
+  __shared__ __align__(16) Lds lds;
+  char(&sq0)[TILE] = lds.sq0;
+  char(&sq1)[TILE] = lds.sq1;
+  char(&sg0)[TILE] = lds.sg0;
+  char(&sg1)[TILE] = lds.sg1;
+  float(&sl0)[BQ] = lds.sl0;
+  float(&sl1)[BQ] = lds.sl1;
+  float(&sd0)[BQ] = lds.sd0;
+  float(&sd1)[BQ] = lds.sd1;
+  auto& xchg = lds.xchg;
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const int half = wave / NWH, wq = wave % NWH;
@@ -720,15 +736,19 @@ __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves
   const int nkb = (S + BKN - 1) / BKN;
   const int jlo = ord.rank, jhi = nkb - 1 - ord.rank;
   const int64_t tok0 = static_cast<int64_t>(b) * S;
-  int a_off = lane_off_a<HD>(lane);
-  int b0 = lane_off_b<HD>(lane, 0), b8 = lane_off_b<HD>(lane, 8);
+  const int hrow = 32 * half;  // this wave's first query row within a tile
+  // The LDS read offsets include the wave's first row (its byte offset lies
+  // above the bits the swizzle XORs touch, so it commutes with them): the
+  // tile reads are then a lane offset plus an immediate, with no address
+  // additions in the loop (32 per query tile otherwise).
+  int a_off = lane_off_a<HD>(lane) + hrow * 2 * HD;
+  int b0 = lane_off_b<HD>(lane, 0) + hrow * 2 * HD, b8 = lane_off_b<HD>(lane, 8) + hrow * 2 * HD;
   const int64_t h0 = static_cast<int64_t>(kvh) * group;
   const uint16_t* qg = q + tok0 * ldq + h0 * HD;
   const uint16_t* gg = dO + tok0 * lddo + h0 * HD;
   const float* lg = nl2 + (static_cast<int64_t>(b) * nh + h0) * S;
   const float* dg = delta + (static_cast<int64_t>(b) * nh + h0) * S;
   const int qt_end = (S + BQ - 1) / BQ;
-  const int hrow = 32 * half;  // this wave's first query row within a tile
 
   for (int ph = 0; ph < 2; ++ph) {
     if (ph == 1 && jhi <= jlo) break;  // block-uniform: the middle key block of an odd count
