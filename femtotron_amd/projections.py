@@ -10,19 +10,20 @@ i.e. ``F.linear(x, W)`` with W [out, in] and no bias.  Its three GEMMs are:
 
 plus ``residual + x W^T`` with the residual add fused into the forward GEMM's
 epilogue (linear_residual; modeling_llama.py:323 rounds the projection output
-to bf16, then the sum), and the q/k/v projection with the rotary embedding of
-q and k in its epilogue (linear_rope, fh_gemm_bf16_rope) or, on the library
-path, the GEMM followed by the separate rotation (fh_rope_fwd).
+to bf16, then the sum), and the q/k/v projection followed by the rotary
+embedding of its k heads (linear_rope: the GEMM, then fh_rope_fwd; the
+attention forward rotates q as it loads it).  fh_gemm_bf16_rope, the
+rotation in the GEMM's epilogue, measured slower than the plain GEMM and the
+separate pass at every workload (TinyLlama q/k/v: 214 against ~157 us) and
+is not dispatched.
 
 Each call runs either the hand-written gfx950 kernel or the tuned library
 GEMM (``torch.mm`` on hipBLASLt/rocBLAS), by policy:
 
 * ``"auto"`` (default): the shipped per-shape table
   ``tuned/gemm_dispatch_gfx950.json`` names the shapes measured on an MI355X
-  where the library was faster than the hand-written kernel (for linear_rope:
-  the library GEMM plus the separate rotation against the rotating kernel);
-  those run on the library, every other supported shape on the hand-written
-  kernel;
+  where the library was faster than the hand-written kernel; those run on
+  the library, every other supported shape on the hand-written kernel;
 * ``"hand"``: the hand-written kernel wherever it supports the operands;
 * ``"library"``: always the library.
 
@@ -79,7 +80,7 @@ def reset_gemm_dispatch_counts() -> None:
 def _library_shapes() -> dict[str, set]:
     global _table
     if _table is None:
-        shapes: dict[str, set] = {"nt": set(), "nn": set(), "tn": set(), "nt_rope": set()}
+        shapes: dict[str, set] = {"nt": set(), "nn": set(), "tn": set()}
         if TABLE_FILE.is_file():
             data = json.loads(TABLE_FILE.read_text())
             for op in shapes:
@@ -118,13 +119,9 @@ def linear_rope(x: torch.Tensor, w: torch.Tensor, n_rot_heads: int, head_dim: in
                 cos: torch.Tensor, sin: torch.Tensor, *, defer_heads: int = 0) -> tuple[torch.Tensor, bool]:
     """x [T, in] @ w[out, in]^T with heads 0..n_rot_heads-1 of the output (q and
     k of the packed q/k/v projection) rotated by RoPE (rope_fwd_'s arithmetic).
-    Returns (y, all rotated).  Where the GEMM is the library's (or the hand-written
-    one without the rotation), the rotation is a separate pass that leaves heads
-    0..defer_heads-1 (q) unrotated for the caller to rotate as it reads them
-    (the attention forward's q load); all rotated is then False."""
-    if head_dim in (32, 64, 128) and _choose_hand("nt", x, w, "nt_rope"):
-        _count(True)
-        return ops.gemm_rope(x, w, n_rot_heads, head_dim, seq_len, cos, sin), True
+    The GEMM is routed as linear's; the rotation is a separate pass that leaves
+    heads 0..defer_heads-1 (q) unrotated for the caller to rotate as it reads
+    them (the attention forward's q load).  Returns (y, all rotated)."""
     y = linear(x, w)  # counts this GEMM once
     if n_rot_heads > defer_heads:
         ops.rope_fwd_(y[:, defer_heads * head_dim:], n_rot_heads - defer_heads, head_dim, seq_len, cos, sin)
@@ -187,9 +184,8 @@ def measure_dispatch(workloads: dict, path: str | Path = TABLE_FILE, *, iters: i
     """Time the hand-written kernel against the library GEMM (with whatever
     library solutions the process has enabled) for every layer GEMM of
     `workloads` ({name: (tokens, hidden, q width, kv width, ffn, head_dim,
-    seq_len)}) and write the shapes where the library was faster; for the
-    q/k/v projection also the rotating kernel (fh_gemm_bf16_rope) against the
-    library GEMM + fh_rope_fwd.  The two candidates run alternately, `reps`
+    seq_len)}) and write the shapes where the library was faster.  The two
+    candidates run alternately, `reps`
     times `iters` launches each, and their medians are compared: the GPU's
     clock drifts by several percent between back-to-back measurements.  Needs
     a HIP device."""
@@ -219,25 +215,7 @@ def measure_dispatch(workloads: dict, path: str | Path = TABLE_FILE, *, iters: i
             tl.append(one(lib))
         return statistics.median(th), statistics.median(tl)
 
-    lib_faster["nt_rope"] = []
     for name, (T, H, hq, hkv, F, hd, S) in workloads.items():
-        # the q/k/v projection with its rotation: fused kernel against the
-        # library GEMM + fh_rope_fwd
-        m, n, k = T, hq + 2 * hkv, H
-        a = torch.randn(m, k, device=dev, generator=g).to(bf)
-        b = torch.randn(n, k, device=dev, generator=g).to(bf)
-        cos = torch.randn(S, hd, device=dev, generator=g).to(bf)
-        sin = torch.randn(S, hd, device=dev, generator=g).to(bf)
-        nr = (hq + hkv) // hd
-        t_hand, t_lib = timed_pair(lambda: ops.gemm_rope(a, b, nr, hd, S, cos, sin),
-                                   lambda: ops.rope_fwd_(torch.mm(a, b.t()), nr, hd, S, cos, sin))
-        rows.append(dict(workload=name, op="nt_rope", m=m, n=n, k=k, hand_us=round(t_hand, 1),
-                         library_us=round(t_lib, 1)))
-        if t_lib * LIBRARY_MARGIN < t_hand and [m, n, k] not in lib_faster["nt_rope"]:
-            lib_faster["nt_rope"].append([m, n, k])
-        log(f"[gemm-dispatch] {name} nt_rope m={m} n={n} k={k}: hand {t_hand:.1f} us, "
-            f"library + rope {t_lib:.1f} us")
-        del a, b
         for op, m, n, k in layer_gemm_forms(T, H, hq, hkv, F):
             a_shape = (k, m) if op == "tn" else (m, k)
             b_shape = (n, k) if op == "nt" else (k, n)
@@ -255,7 +233,6 @@ def measure_dispatch(workloads: dict, path: str | Path = TABLE_FILE, *, iters: i
             del a, b
     data = {"note": "shapes (m, n, k of fh_gemm_bf16) where the tuned library GEMM measured at least 2% "
                     "faster than the hand-written kernel on an MI355X (medians of alternating runs); "
-                    "nt_rope: the library GEMM followed by fh_rope_fwd against fh_gemm_bf16_rope; "
                     "everything else runs hand-written",
             "library": lib_faster, "measurements": rows}
     Path(path).write_text(json.dumps(data, indent=1) + "\n")
