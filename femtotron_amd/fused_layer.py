@@ -87,8 +87,7 @@ def qkv_attention(y: torch.Tensor, wqkv: torch.Tensor, batch: int, seq: int, shp
                   cos: torch.Tensor, sin: torch.Tensor, *, keep: bool):
     """q/k/v projection, RoPE and causal attention: (qkv, o, lse).  qkv holds the
     rotated q and k when keep (what the backward reads).  k is rotated by a pass
-    over the kv heads, q as the attention forward loads it, unless the dispatch
-    runs the rotating GEMM (fh_gemm_bf16_rope), which rotates both."""
+    over the kv heads, q as the attention forward loads it."""
     qkv, rotated = linear_rope(y, wqkv, shp.n_heads + shp.n_kv_heads, shp.head_dim, seq, cos, sin,
                                defer_heads=shp.n_heads)
     o, lse = attn_fwd(qkv, batch, seq, shp, need_lse=keep, rope=None if rotated else (cos, sin),
