@@ -12,7 +12,7 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_size_t, c_void_
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libfemtohip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 FH_BF16 = 0
 FH_F32 = 1
@@ -32,6 +32,13 @@ class FhAdamHyper(ctypes.Structure):
     """FhAdamHyper of include/femtohip.h (passed by value to fh_adamw_step)."""
     _fields_ = [("one_minus_beta1", c_float), ("beta2", c_float), ("one_minus_beta2", c_float),
                 ("eps", c_float)]
+
+class FhGemmProblem(ctypes.Structure):
+    """fh_gemm_problem of include/femtohip.h (an array of them is passed to
+    fh_gemm_bf16_grouped)."""
+    _fields_ = [("a", _V), ("lda", _I64), ("b", _V), ("ldb", _I64), ("c", _V), ("ldc", _I64),
+                ("residual", _V), ("ldr", _I64), ("m", _I64), ("n", _I64)]
+
 
 # name -> (restype, argtypes); mirrors include/femtohip.h exactly.
 SIGNATURES: dict[str, tuple] = {
@@ -66,6 +73,8 @@ SIGNATURES: dict[str, tuple] = {
     "fh_gemm_bf16": (c_int, [c_int, _V, _I64, _V, _I64, _V, _I64, _V, _I64, _I64, _I64, _I64, _V, _V]),
     "fh_gemm_bf16_rope": (c_int, [_V, _I64, _V, _I64, _V, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
                                   _V, _V, c_int, _V]),
+    "fh_gemm_bf16_grouped_workspace_size": (c_size_t, [c_int, c_int, POINTER(FhGemmProblem), _I64]),
+    "fh_gemm_bf16_grouped": (c_int, [c_int, c_int, POINTER(FhGemmProblem), _I64, _V, _V]),
     "fh_embedding_fwd": (c_int, [c_int, _V, _V, _V, _I64, _I64, _I64, _V]),
     "fh_embedding_bwd_workspace_size": (c_size_t, [_I64, _I64]),
     "fh_embedding_bwd": (c_int, [c_int, _V, _V, _V, _I64, _I64, _I64, _I64, _V, _V]),

@@ -80,6 +80,18 @@ struct GemmRope {
   FastDiv seq;
 };
 
+// One problem of a grouped stream GEMM (the same op and k for all): its
+// operands and the first of its tiles in the group's tile order.
+constexpr int kMaxGroup = 3;
+struct GemmProblem {
+  const uint16_t* a;
+  const uint16_t* b;
+  uint16_t* c;
+  const uint16_t* r;
+  int64_t lda, ldb, ldc, ldr;
+  int m, n, tiles_m, tiles_n, tile0;
+};
+
 struct GemmArgs {
   const uint16_t* a;
   const uint16_t* b;
@@ -99,6 +111,10 @@ struct GemmArgs {
   // > 0: the tail in XCD slabs (tail_tiles = slab_chunks * grid / 8; see k_gemm)
   int slab_chunks;
   GemmRope rope;
+  // EPI_STREAM: the problems (one, or several of the same op and k that share
+  // the launch), tiles numbered problem by problem
+  int ngroup;
+  GemmProblem grp[kMaxGroup];
 };
 
 // 8 outputs of the forward rotation (rope_fwd_one) from this chunk x, its
@@ -255,6 +271,31 @@ __device__ __forceinline__ void tile_origin(const GemmArgs& g, int t, int& m0, i
   const int tw = t - gi * width;
   m0 = (first_m + tw % gm) * kTm;
   n0 = (tw / gm) * kTn;
+}
+
+// The arguments of the problem that holds tile t of a stream GEMM's tile
+// order, with t made local to it (the group table holds every stream GEMM's
+// problems, one or more).
+__device__ __forceinline__ GemmArgs for_tile(const GemmArgs& g, int& t) {
+  int p = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxGroup; ++i) p = (i < g.ngroup && t >= g.grp[i].tile0) ? i : p;
+  const GemmProblem& P = g.grp[p];
+  GemmArgs q = g;
+  q.a = P.a;
+  q.b = P.b;
+  q.c = P.c;
+  q.r = P.r;
+  q.lda = P.lda;
+  q.ldb = P.ldb;
+  q.ldc = P.ldc;
+  q.ldr = P.ldr;
+  q.m = P.m;
+  q.n = P.n;
+  q.tiles_m = P.tiles_m;
+  q.tiles_n = P.tiles_n;
+  t -= P.tile0;
+  return q;
 }
 
 // One tile t over k-steps s_begin .. s_begin + nst - 1.  The result goes to C
@@ -719,7 +760,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       } else {
         break;
       }
-      gemm_tile<A_KO, B_KO, EPI>(g, ring, t, k0, len, slot, kTn, len < ki);
+      const GemmArgs pg = for_tile(g, t);
+      gemm_tile<A_KO, B_KO, EPI>(pg, ring, t, k0, len, slot, kTn, len < ki);
     }
   } else {
     const int slice = lid / g.tiles, t = lid - slice * g.tiles;
@@ -765,11 +807,12 @@ __global__ __launch_bounds__(256) void k_gemm_fixup(GemmArgs g) {
   auto start_of = [&](int64_t w) { return w * I / N; };
   const int w0 = wg_of(lo), w1 = wg_of(lo + ki - 1);
   if (w0 == w1 && !slab) return;  // one workgroup stored the whole tile
-  int m0, n0;
-  tile_origin(g, g.full_rounds * g.grid + static_cast<int>(blockIdx.x), m0, n0);
+  int m0, n0, tl = g.full_rounds * g.grid + static_cast<int>(blockIdx.x);
+  const GemmArgs pg = for_tile(g, tl);  // the tile's problem: pg.c, pg.r, pg.m, pg.n
+  tile_origin(pg, tl, m0, n0);
   const int lane = threadIdx.x & 63, r0 = blockIdx.y * kFixRows + (threadIdx.x >> 6);
   const int col = n0 + 4 * lane;
-  if (col >= g.n) return;
+  if (col >= pg.n) return;
   float4 acc[kFixRows / 4];
   bool first = true;
   for (int w = w0; w <= w1; ++w) {
@@ -796,16 +839,16 @@ __global__ __launch_bounds__(256) void k_gemm_fixup(GemmArgs g) {
 #pragma unroll
   for (int q = 0; q < kFixRows / 4; ++q) {
     const int mrow = m0 + r0 + 4 * q;
-    if (mrow >= g.m) break;
+    if (mrow >= pg.m) break;
     float4 s = acc[q];
-    if (g.r != nullptr) {
-      const uint2 rv = *reinterpret_cast<const uint2*>(g.r + static_cast<int64_t>(mrow) * g.ldr + col);
+    if (pg.r != nullptr) {
+      const uint2 rv = *reinterpret_cast<const uint2*>(pg.r + static_cast<int64_t>(mrow) * pg.ldr + col);
       s.x = __uint_as_float(rv.x << 16) + round_bf(s.x);
       s.y = __uint_as_float(rv.x & 0xffff0000u) + round_bf(s.y);
       s.z = __uint_as_float(rv.y << 16) + round_bf(s.z);
       s.w = __uint_as_float(rv.y & 0xffff0000u) + round_bf(s.w);
     }
-    *reinterpret_cast<uint2*>(g.c + static_cast<int64_t>(mrow) * g.ldc + col) =
+    *reinterpret_cast<uint2*>(pg.c + static_cast<int64_t>(mrow) * pg.ldc + col) =
         make_uint2(pk_bf16(s.x, s.y), pk_bf16(s.z, s.w));
   }
 }
@@ -979,6 +1022,8 @@ int gemm_setup(int op, const void* a, int64_t lda, const void* b, int64_t ldb, v
   g.tiles_n = static_cast<int>((n + kTn - 1) / kTn);
   g.tiles = g.tiles_m * g.tiles_n;
   g.total_steps = static_cast<int>(k / kTk);
+  g.ngroup = 1;
+  g.grp[0] = GemmProblem{g.a, g.b, g.c, g.r, lda, ldb, ldc, ldr, g.m, g.n, g.tiles_m, g.tiles_n, 0};
   return FH_OK;
 }
 
@@ -1000,7 +1045,8 @@ int gemm_run(int op, GemmArgs& g, int slices, bool stream_form, void* workspace,
       case FH_GEMM_NN: launch<false, true>(g, sg, false, false, stream); break;
       default: launch<true, true>(g, sg, false, false, stream); break;
     }
-    hipLaunchKernelGGL(k_gemm_fixup, dim3(g.tail_tiles, kTm / kFixRows), dim3(256), 0, stream, g);
+    if (g.tail_tiles > 0)
+      hipLaunchKernelGGL(k_gemm_fixup, dim3(g.tail_tiles, kTm / kFixRows), dim3(256), 0, stream, g);
     return FH_OK;
   }
   g.steps_per_slice = (g.total_steps + slices - 1) / slices;
@@ -1051,6 +1097,82 @@ extern "C" int fh_gemm_bf16(int op, const void* a, int64_t lda, const void* b, i
              "gemm_bf16: workspace (fh_gemm_bf16_workspace_size bytes) required");
   if (int e = gemm_run(op, g, p.slices, p.stream, workspace, stream)) return e;
   return check_launch("fh_gemm_bf16");
+}
+
+namespace {
+
+// A group runs as one stream launch when its tiles fill more than a round of
+// the CUs (the tail, if any, in XCD slabs when it is a whole number of
+// 32-tile chunks); otherwise its problems run one by one, each by its own plan.
+bool group_stream(int64_t tiles, int64_t steps) { return tiles > stream_grid() && steps >= 4; }
+
+// Checks every problem of a group and fills g with the group's table (tiles
+// numbered problem by problem).
+int group_setup(int op, int count, const fh_gemm_problem* probs, int64_t k, GemmArgs& g) {
+  FH_REQUIRE(count >= 1 && count <= kMaxGroup && probs != nullptr,
+             "gemm_bf16_grouped: between 1 and 3 problems required");
+  int tile0 = 0;
+  for (int i = 0; i < count; ++i) {
+    const fh_gemm_problem& p = probs[i];
+    GemmArgs gi;
+    if (int e = gemm_setup(op, p.a, p.lda, p.b, p.ldb, p.c, p.ldc, p.residual, p.ldr, p.m, p.n, k, gi)) return e;
+    if (i == 0) g = gi;
+    g.grp[i] = gi.grp[0];
+    g.grp[i].tile0 = tile0;
+    tile0 += gi.tiles;
+  }
+  g.ngroup = count;
+  g.tiles = tile0;
+  return FH_OK;
+}
+
+}  // namespace
+
+extern "C" size_t fh_gemm_bf16_grouped_workspace_size(int op, int count, const fh_gemm_problem* problems,
+                                                      int64_t k) {
+  if (!valid_op(op) || count < 1 || count > kMaxGroup || problems == nullptr || k <= 0 || k % kTk) return 0;
+  int64_t tiles = 0;
+  size_t most = 0;
+  for (int i = 0; i < count; ++i) {
+    const int64_t m = problems[i].m, n = problems[i].n;
+    if (m <= 0 || n <= 0) return 0;
+    tiles += ((m + kTm - 1) / kTm) * ((n + kTn - 1) / kTn);
+    most = std::max(most, fh_gemm_bf16_workspace_size(op, m, n, k));
+  }
+  return group_stream(tiles, k / kTk) ? stream_workspace_bytes() : most;
+}
+
+extern "C" int fh_gemm_bf16_grouped(int op, int count, const fh_gemm_problem* problems, int64_t k,
+                                    void* workspace, hipStream_t stream) {
+  GemmArgs g;
+  if (int e = group_setup(op, count, problems, k, g)) return e;
+  if (!group_stream(g.tiles, g.total_steps)) {
+    for (int i = 0; i < count; ++i) {
+      const fh_gemm_problem& p = problems[i];
+      if (int e = fh_gemm_bf16(op, p.a, p.lda, p.b, p.ldb, p.c, p.ldc, p.residual, p.ldr, p.m, p.n, k,
+                               workspace, stream))
+        return e;
+    }
+    return FH_OK;
+  }
+  FH_REQUIRE(workspace && aligned16(workspace),
+             "gemm_bf16_grouped: workspace (fh_gemm_bf16_grouped_workspace_size bytes) required");
+  const int sg = stream_grid();
+  g.part = static_cast<float*>(workspace);
+  g.grid = sg;
+  g.full_rounds = g.tiles / sg;
+  g.tail_tiles = g.tiles - g.full_rounds * sg;
+  g.tail_iters = static_cast<int64_t>(g.tail_tiles) * g.total_steps;
+  g.steps_per_slice = g.total_steps;
+  g.slab_chunks = g.tail_tiles % (sg / 8) == 0 ? g.tail_tiles / (sg / 8) : 0;
+  switch (op) {
+    case FH_GEMM_NT: hipLaunchKernelGGL((k_gemm<false, false, EPI_STREAM>), dim3(sg), dim3(256), 0, stream, g); break;
+    case FH_GEMM_NN: hipLaunchKernelGGL((k_gemm<false, true, EPI_STREAM>), dim3(sg), dim3(256), 0, stream, g); break;
+    default: hipLaunchKernelGGL((k_gemm<true, true, EPI_STREAM>), dim3(sg), dim3(256), 0, stream, g); break;
+  }
+  if (g.tail_tiles > 0)
+    hipLaunchKernelGGL(k_gemm_fixup, dim3(g.tail_tiles, kTm / kFixRows), dim3(256), 0, stream, g);
+  return check_launch("fh_gemm_bf16_grouped");
 }
 
 extern "C" int fh_gemm_bf16_rope(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc,

@@ -37,7 +37,8 @@ from dataclasses import dataclass
 import torch
 
 from . import ops
-from .projections import linear, linear_dgrad, linear_residual, linear_rope, linear_wgrad, linear_wgrad_into
+from .projections import (linear, linear_dgrad, linear_residual, linear_rope, linear_wgrad, linear_wgrad_group,
+                          linear_wgrad_into)
 from .weight_packing import packed
 
 
@@ -240,6 +241,22 @@ class _WgradStream:
             out.record_stream(self.main)
         return out
 
+    def mm_tn_group(self, items: list) -> list | None:
+        """linear_wgrad_group (several a^T @ b in one launch) on the side stream,
+        or in order on the main stream; None when the group is not taken."""
+        if not _use_side_stream:
+            return linear_wgrad_group(items)
+        self.side.wait_stream(self.main)
+        with torch.cuda.stream(self.side):
+            outs = linear_wgrad_group(items)
+        for a, b, _ in items:
+            a.record_stream(self.side)
+            b.record_stream(self.side)
+        for o in outs or ():
+            if o is not None:
+                o.record_stream(self.main)
+        return outs
+
     def join(self) -> None:
         if _use_side_stream:
             self.main.wait_stream(self.side)
@@ -271,8 +288,6 @@ def layer_backward(dout2: torch.Tensor, x2: torch.Tensor, cos: torch.Tensor, sin
     dgu = torch.empty_like(acts.gu)
     ops.swiglu_bwd(dp, acts.gu[:, :F_], acts.gu[:, F_:], dgu[:, :F_], dgu[:, F_:], p_out=dp)
     acts.gu = None
-    dwd = wg_stream.mm_tn(dout2, dp, grad_target(wd))
-    del dp
     dwgu = wg_stream.mm_tn(dgu, acts.z, grad_target(wg, wu))
     dz = linear_dgrad(dgu, _cat_rows(wg, wu))
     del dgu
@@ -282,12 +297,22 @@ def layer_backward(dout2: torch.Tensor, x2: torch.Tensor, cos: torch.Tensor, sin
     del dz
     acts.h = None
     # attention output projection
-    dwo = wg_stream.mm_tn(dh, acts.o, grad_target(wo))
     do = linear_dgrad(dh, wo)
     dqkv = attn_bwd(do, acts.qkv, acts.o, acts.lse, batch, seq, shp, cos, sin)
     del do
-    acts.o = acts.lse = acts.qkv = None
-    dwqkv = wg_stream.mm_tn(dqkv, acts.y1, grad_target(wq, wk, wv))
+    acts.lse = acts.qkv = None
+    # The down, o and q/k/v weight gradients (few output tiles each, the same
+    # tokens) run as one grouped GEMM once dqkv exists.
+    done = wg_stream.mm_tn_group([(dout2, dp, grad_target(wd)), (dh, acts.o, grad_target(wo)),
+                                  (dqkv, acts.y1, grad_target(wq, wk, wv))])
+    if done is None:  # not all hand-written: one by one
+        dwd = wg_stream.mm_tn(dout2, dp, grad_target(wd))
+        dwo = wg_stream.mm_tn(dh, acts.o, grad_target(wo))
+        dwqkv = wg_stream.mm_tn(dqkv, acts.y1, grad_target(wq, wk, wv))
+    else:
+        dwd, dwo, dwqkv = done
+    del dp
+    acts.o = None
     dy1 = linear_dgrad(dqkv, _cat_rows(wq, wk, wv))
     del dqkv
     acts.y1 = None

@@ -433,6 +433,43 @@ def gemm(op: str, a: torch.Tensor, b: torch.Tensor, *, residual: torch.Tensor | 
     return c
 
 
+def gemm_grouped(op: str, items: list) -> list:
+    """Up to three GEMMs of layout `op` with one k in one fh_gemm_bf16_grouped
+    call: each item is (a, b, residual, out) with gemm()'s meaning (residual
+    and out may be None; out may be residual itself).  Returns the outputs."""
+    if not 1 <= len(items) <= 3:
+        raise ValueError(f"gemm_grouped({op}): between 1 and 3 problems, got {len(items)}")
+    probs = (_lib.FhGemmProblem * len(items))()
+    outs, ks = [], set()
+    for i, (a, b, residual, out) in enumerate(items):
+        _require_gpu(a, b, residual, out)
+        if not gemm_supported(op, a, b):
+            raise ValueError(f"gemm_grouped({op}): unsupported operands {tuple(a.shape)} {a.stride()} x "
+                             f"{tuple(b.shape)} {b.stride()} ({a.dtype}, {b.dtype})")
+        m, n, k = gemm_dims(op, a, b)
+        ks.add(k)
+        c = torch.empty(m, n, dtype=a.dtype, device=a.device) if out is None else out
+        for t, name in ((c, "out"), (residual, "residual")):
+            if t is None:
+                continue
+            if t.dtype != torch.bfloat16 or tuple(t.shape) != (m, n) or t.stride(1) != 1:
+                raise ValueError(f"gemm_grouped({op}): {name} must be a bf16 [{m}, {n}] row-major view")
+            if t.stride(0) % 8 or t.data_ptr() % 16:
+                raise ValueError(f"gemm_grouped({op}): {name} must be 16-byte aligned with a row stride % 8 == 0")
+        probs[i] = _lib.FhGemmProblem(_ptr(a), a.stride(0), _ptr(b), b.stride(0), _ptr(c), c.stride(0),
+                                      _ptr(residual), 0 if residual is None else residual.stride(0), m, n)
+        outs.append(c)
+    if len(ks) != 1:
+        raise ValueError(f"gemm_grouped({op}): the problems' k differ: {sorted(ks)}")
+    k = ks.pop()
+    code = _GEMM_OPS[op]
+    a0 = items[0][0]
+    nbytes = _lib.lib().fh_gemm_bf16_grouped_workspace_size(code, len(items), probs, k)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=a0.device) if nbytes else None
+    _lib.call("fh_gemm_bf16_grouped", code, len(items), probs, k, _ptr(ws), _stream(a0))
+    return outs
+
+
 def gemm_rope(a: torch.Tensor, b: torch.Tensor, n_rot_heads: int, head_dim: int, seq_len: int,
               cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
     """a [m,k] @ b[n,k]^T (the q/k/v projection) with the rotary embedding of

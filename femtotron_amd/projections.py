@@ -6,7 +6,8 @@ i.e. ``F.linear(x, W)`` with W [out, in] and no bias.  Its three GEMMs are:
 
     forward          y  = x W^T        fh_gemm_bf16 FH_GEMM_NT   (linear)
     input gradient   dx = dy W         fh_gemm_bf16 FH_GEMM_NN   (linear_dgrad)
-    weight gradient  dW = dy^T x       fh_gemm_bf16 FH_GEMM_TN   (linear_wgrad)
+    weight gradient  dW = dy^T x       fh_gemm_bf16 FH_GEMM_TN   (linear_wgrad; three of
+                                       them in one fh_gemm_bf16_grouped launch: linear_wgrad_group)
 
 plus ``residual + x W^T`` with the residual add fused into the forward GEMM's
 epilogue (linear_residual; modeling_llama.py:323 rounds the projection output
@@ -177,6 +178,23 @@ def layer_gemm_forms(tokens: int, hidden: int, q_width: int, kv_width: int, ffn:
     for out_f, in_f in projs:
         forms += [("nt", tokens, out_f, in_f), ("nn", tokens, in_f, out_f), ("tn", out_f, in_f, tokens)]
     return forms
+
+
+def linear_wgrad_group(items: list) -> list | None:
+    """dW_i = dy_i^T x_i for up to three projections whose dy and x share one
+    token count, in one hand-written launch (fh_gemm_bf16_grouped): the layer's
+    q/k/v, o and down weight gradients have few output tiles each and fill the
+    CUs together.  Each item is (dy, x, grad), grad the parameter's existing
+    bf16 gradient to accumulate into (linear_wgrad_into's rule) or None.
+    Returns the new gradients (None where accumulated), or None when the
+    dispatch would not run every one of them hand-written (the caller then runs
+    them one by one)."""
+    if not all(_choose_hand("tn", dy, x) for dy, x, _ in items):
+        return None
+    for _ in items:
+        _count(True)
+    outs = ops.gemm_grouped("tn", [(dy, x, g, g) for dy, x, g in items])
+    return [None if g is not None else o for (_, _, g), o in zip(items, outs)]
 
 
 def measure_dispatch(workloads: dict, path: str | Path = TABLE_FILE, *, iters: int = 10, reps: int = 5,

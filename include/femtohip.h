@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define FH_ABI_VERSION 5
+#define FH_ABI_VERSION 6
 
 typedef enum fh_dtype {
   FH_BF16 = 0, /* bfloat16 storage, fp32 arithmetic */
@@ -374,6 +374,42 @@ size_t fh_gemm_bf16_workspace_size(int op, int64_t m, int64_t n, int64_t k);
 int fh_gemm_bf16(int op, const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
                  int64_t ldc, const void* residual, int64_t ldr, int64_t m, int64_t n,
                  int64_t k, void* workspace, hipStream_t stream);
+
+/* Up to three GEMMs of one layout and one k in one launch: problem i is
+ * fh_gemm_bf16(op, a, lda, b, ldb, c, ldc, residual, ldr, m, n, k) of its
+ * fields, with the same roundings, requirements and residual rules.  The
+ * layer's weight gradients that read the same tokens (k = tokens: q/k/v, o and
+ * down, each with few output tiles) run together this way
+ * (femtotron/parallel/tensor_parallel/linear.py:66-80, 194-214 backward,
+ * accumulated as fh_gemm_bf16's residual == C).  When the problems' tiles
+ * together fill more than one round of the CUs they share one launch in the
+ * stream form (every CU an equal share of the group's k-steps, problem by
+ * problem; split tiles summed in k order from fp32 segments in `workspace`);
+ * otherwise each runs as its own fh_gemm_bf16 call.  Bitwise deterministic
+ * (the form depends only on the problems' sizes, k and the CU count); a
+ * problem's result may differ in the last bit from its own fh_gemm_bf16 call,
+ * whose form may split k differently.  The problems' outputs must not overlap
+ * each other's operands or outputs.  The reference runs each of these
+ * weight-gradient matmuls on its own.
+ */
+typedef struct fh_gemm_problem {
+  const void* a;
+  int64_t lda;
+  const void* b;
+  int64_t ldb;
+  void* c;
+  int64_t ldc;
+  const void* residual;
+  int64_t ldr;
+  int64_t m;
+  int64_t n;
+} fh_gemm_problem;
+
+/* Workspace bytes for fh_gemm_bf16_grouped (reads the problems' m and n only;
+ * 0 for invalid sizes or when none is needed). */
+size_t fh_gemm_bf16_grouped_workspace_size(int op, int count, const fh_gemm_problem* problems, int64_t k);
+int fh_gemm_bf16_grouped(int op, int count, const fh_gemm_problem* problems, int64_t k, void* workspace,
+                         hipStream_t stream);
 
 /* The q/k/v projection with the rotary embedding in its epilogue: C = A B^T
  * (FH_GEMM_NT, no residual) and then, on columns [0, rot_cols) of C (the q and

@@ -164,6 +164,60 @@ def test_residual_epilogue_rounds_like_the_unfused_add(op, m, n, k):
     assert torch.equal(inplace, fused)
 
 
+@pytest.mark.parametrize("shapes,k,one_launch", [
+    # the layer's q/k/v, o and down weight gradients at config 3: 80 + 64 + 176
+    # tiles, one stream launch (a whole round, then 64 tail tiles in XCD slabs)
+    ([(2560, 2048), (2048, 2048), (2048, 5632)], 16384, True),
+    ([(2560, 2048), (2048, 2048), (2048, 5632)], 256, True),       # 4 k-steps
+    ([(6144, 4096), (4096, 4096), (4096, 14336)], 1024, True),     # config 4's: six whole rounds, no tail
+    ([(520, 264), (1032, 776)], 8192, False),                      # ragged, too few tiles: one call each
+])
+def test_grouped_tn_matches_each_product_and_accumulates(shapes, k, one_launch):
+    """fh_gemm_bf16_grouped: every problem within the product's bound, bitwise
+    repeatable, and with residual == C the accumulating epilogue
+    to_bf16(R + to_bf16(A^T B)) bit for bit (whole tiles in the GEMM, split ones
+    in the fixup); a group whose tiles do not fill a round runs as separate
+    fh_gemm_bf16 calls."""
+    g = torch.Generator(device=DEV).manual_seed(k + len(shapes))
+    ops_ = [_operands("tn", m, n, k, g) for m, n in shapes]
+    probs = (_lib.FhGemmProblem * len(shapes))()
+    for i, ((a, b), (m, n)) in enumerate(zip(ops_, shapes)):
+        probs[i] = _lib.FhGemmProblem(a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), None, n, None, 0, m, n)
+    ws = _lib.lib().fh_gemm_bf16_grouped_workspace_size(_lib.FH_GEMM_TN, len(shapes), probs, k)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count // 8 * 8
+    if one_launch:
+        assert ws == 2 * cus * 256 * 256 * 4
+    outs = ops.gemm_grouped("tn", [(a, b, None, None) for a, b in ops_])
+    for (a, b), c in zip(ops_, outs):
+        _check("tn", a, b, c, exact=True)
+    again = ops.gemm_grouped("tn", [(a, b, None, None) for a, b in ops_])
+    assert all(torch.equal(x, y) for x, y in zip(outs, again))
+    if not one_launch:  # separate calls: each is its own fh_gemm_bf16
+        assert all(torch.equal(c, ops.gemm("tn", a, b)) for (a, b), c in zip(ops_, outs))
+    rs = [torch.randn(m, n, device=DEV, generator=g).to(BF) for m, n in shapes]
+    acc = [r.clone() for r in rs]
+    got = ops.gemm_grouped("tn", [(a, b, x, x) for (a, b), x in zip(ops_, acc)])
+    for r, x, y, c in zip(rs, acc, got, outs):
+        assert y.data_ptr() == x.data_ptr()
+        assert torch.equal(x, (r.float() + c.float()).to(BF))
+
+
+def test_grouped_rejects_bad_arguments():
+    x = torch.randn(256, 256, device=DEV).to(BF)
+    with pytest.raises(ValueError):
+        ops.gemm_grouped("tn", [])
+    with pytest.raises(ValueError):
+        ops.gemm_grouped("tn", [(x, x, None, None)] * 4)
+    with pytest.raises(ValueError):  # the problems' k differ
+        ops.gemm_grouped("tn", [(x, x, None, None), (x[:128], x[:128], None, None)])
+    probs = (_lib.FhGemmProblem * 1)()
+    probs[0] = _lib.FhGemmProblem(x.data_ptr(), 256, x.data_ptr(), 256, x.data_ptr(), 256, None, 0, 256, 256)
+    st = _lib.lib().fh_gemm_bf16_grouped(_lib.FH_GEMM_TN, 4, probs, 256, None, None)
+    assert st == 1 and b"between 1 and 3" in _lib.lib().fh_last_error()
+    st = _lib.lib().fh_gemm_bf16_grouped(_lib.FH_GEMM_TN, 1, probs, 96, None, None)
+    assert st == 1 and b"multiple of 64" in _lib.lib().fh_last_error()
+
+
 def test_gemm_rejects_unsupported_operands():
     a = torch.randn(128, 96, device=DEV).to(BF)  # k = 96 is not a multiple of 64
     b = torch.randn(256, 96, device=DEV).to(BF)
