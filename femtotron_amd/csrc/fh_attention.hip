@@ -713,20 +713,17 @@ __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves
   // One struct fixes the layout: the tiles the loop reads first, below 64 KB,
   // so that their base is a read's immediate offset (placed after the 64 KB
   // exchange buffer, every tile read added its base in a VGPR).
+  // Two items per stage (IPB): the barrier that ends a stage comes once per
+  // two items, halving the waits for the slowest wave.
   struct Lds {
-    char sq0[TILE], sq1[TILE], sg0[TILE], sg1[TILE];
-    float sl0[BQ], sl1[BQ], sd0[BQ], sd1[BQ];  // -lse*log2(e) and delta
-    float xchg[2][NWH][ND * 16][64];           // [0]: dV of half 0, [1]: dK of half 1
+    char sq0a[TILE], sq0b[TILE], sq1a[TILE], sq1b[TILE];
+    char sg0a[TILE], sg0b[TILE], sg1a[TILE], sg1b[TILE];
+    float sl0a[BQ], sl0b[BQ], sl1a[BQ], sl1b[BQ];  // -lse*log2(e)
+    float sd0a[BQ], sd0b[BQ], sd1a[BQ], sd1b[BQ];  // delta
+    float xchg[2][NWH][ND * 16][64];               // [0]: dV of half 0, [1]: dK of half 1
   };
+  static_assert(8 * TILE <= 65536, "every tile read's base fits a ds_read immediate");
   __shared__ __align__(16) Lds lds;
-  char(&sq0)[TILE] = lds.sq0;
-  char(&sq1)[TILE] = lds.sq1;
-  char(&sg0)[TILE] = lds.sg0;
-  char(&sg1)[TILE] = lds.sg1;
-  float(&sl0)[BQ] = lds.sl0;
-  float(&sl1)[BQ] = lds.sl1;
-  float(&sd0)[BQ] = lds.sd0;
-  float(&sd1)[BQ] = lds.sd1;
   auto& xchg = lds.xchg;
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
@@ -780,15 +777,17 @@ __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves
     const int n_it = group * (qt_end - qt0);
     QTileDma<HD, BQ, NT> pre;
     pre.start(qt_end, ldq, lddo, wave, lane);
-    pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, sq0, sg0, sl0, sd0, wave, lane);
+    pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, lds.sq0a, lds.sg0a, lds.sl0a, lds.sd0a, wave, lane);
+    if (n_it > 1)
+      pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, lds.sq0b, lds.sg0b, lds.sl0b, lds.sd0b, wave, lane);
     wait_loads();
     __syncthreads();
     int cqt = qt_end - 1, chh = 0;  // query tile and head of the current item
-    // Item IT from stage (QC, GC, LC, DC); item IT + 1 into stage (QN, GN, LN, DN).
-#define FH_DKDV_ITER(IT, QC, GC, LC, DC, QN, GN, LN, DN)                                          \
+    // Item IT from (QC, GC, LC, DC), and item IT + 2 into (QN, GN, LN, DN).
+#define FH_DKDV_ITEM(IT, QC, GC, LC, DC, QN, GN, LN, DN)                                          \
   {                                                                                               \
     refresh_offsets(a_off, b0, b8);                                                               \
-    if ((IT) + 1 < n_it)                                                                          \
+    if ((IT) + 2 < n_it)                                                                          \
       pre.fetch(qg, ldq, gg, lddo, lg, dg, S, qt0, group, QN, GN, LN, DN, wave, lane);            \
     const int qh = cqt * BQ + hrow; /* first query of this wave's half */                         \
     if ((IT) < n_it && qh + 31 >= kw) /* some query of the half reaches this wave's keys */      \
@@ -798,14 +797,21 @@ __global__ __launch_bounds__(DkdvFusedTiles<HD>::NT) __attribute__((amdgpu_waves
       chh = 0;                                                                                    \
       --cqt;                                                                                      \
     }                                                                                             \
-    wait_loads();                                              \
-    __syncthreads();                                                                              \
   }
-    for (int it = 0; it < n_it; it += 2) {
-      FH_DKDV_ITER(it, sq0, sg0, sl0, sd0, sq1, sg1, sl1, sd1)
-      FH_DKDV_ITER(it + 1, sq1, sg1, sl1, sd1, sq0, sg0, sl0, sd0)
+    // Stage 0 holds items it, it + 1 while items it + 2, it + 3 are loaded
+    // into stage 1; each wave waits for its own loads before the barrier that
+    // ends the pair.
+    for (int it = 0; it < n_it; it += 4) {
+      FH_DKDV_ITEM(it, lds.sq0a, lds.sg0a, lds.sl0a, lds.sd0a, lds.sq1a, lds.sg1a, lds.sl1a, lds.sd1a)
+      FH_DKDV_ITEM(it + 1, lds.sq0b, lds.sg0b, lds.sl0b, lds.sd0b, lds.sq1b, lds.sg1b, lds.sl1b, lds.sd1b)
+      wait_loads();
+      __syncthreads();
+      FH_DKDV_ITEM(it + 2, lds.sq1a, lds.sg1a, lds.sl1a, lds.sd1a, lds.sq0a, lds.sg0a, lds.sl0a, lds.sd0a)
+      FH_DKDV_ITEM(it + 3, lds.sq1b, lds.sg1b, lds.sl1b, lds.sd1b, lds.sq0b, lds.sg0b, lds.sl0b, lds.sd0b)
+      wait_loads();
+      __syncthreads();
     }
-#undef FH_DKDV_ITER
+#undef FH_DKDV_ITEM
 
     // Sum the halves: half 0 hands over its dV, half 1 its dK.
     float(*mine)[64] = xchg[half][wq];
