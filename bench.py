@@ -562,14 +562,23 @@ def projection_gemm_rows(torch, c: dict, iters: int, sel: bool, fused_attention:
         for op, a, b, lib, per_layer in (("nt", x, w, lambda: torch.mm(x, w.t()), fwd_per_layer),
                                          ("nn", dy, w, lambda: torch.mm(dy, w), 1),
                                          ("tn", dy, x, lambda: torch.mm(dy.t(), x), 1)):
-            ms_hand = event_ms(torch, lambda i=0: ops.gemm(op, a, b), iters, warm=True)
-            ms_lib = event_ms(torch, lambda i=0: lib(), iters, warm=True)
+            # the down projection's forward is linear_residual: the hand-written
+            # GEMM's residual epilogue against the library GEMM + fh_add
+            res = op == "nt" and name == "down"
+            if res:
+                r_, o_ = rnd(T, n_out), torch.empty(T, n_out, device=x.device, dtype=x.dtype)
+                ms_hand = event_ms(torch, lambda i=0: ops.gemm(op, a, b, residual=r_, out=o_), iters, warm=True)
+                ms_lib = event_ms(torch, lambda i=0: ops.add(r_, lib(), out=o_), iters, warm=True)
+            else:
+                ms_hand = event_ms(torch, lambda i=0: ops.gemm(op, a, b), iters, warm=True)
+                ms_lib = event_ms(torch, lambda i=0: lib(), iters, warm=True)
             hand = projections.gemm_policy() != "library" and (
                 projections.gemm_policy() == "hand"
-                or ops.gemm_dims(op, a, b) not in projections._library_shapes()[op])
+                or ops.gemm_dims(op, a, b) not in projections._library_shapes()["nt_res" if res else op])
             ms = ms_hand if hand else ms_lib
             out.append(dict(kernel=f"gemm_{op}_{name}", m_n_k=list(ops.gemm_dims(op, a, b)),
-                            path="fh_gemm_bf16 (k_gemm)" if hand else "library (torch.mm)",
+                            path=("fh_gemm_bf16 (k_gemm)" if hand else "library (torch.mm)")
+                            + (" with the residual add (epilogue / fh_add)" if res else ""),
                             launches_per_step=per_layer * L, flop_per_launch=flop,
                             ms_per_launch=round(ms, 4), hand_ms=round(ms_hand, 4),
                             library_ms=round(ms_lib, 4),

@@ -10,8 +10,10 @@ i.e. ``F.linear(x, W)`` with W [out, in] and no bias.  Its three GEMMs are:
                                        them in one fh_gemm_bf16_grouped launch: linear_wgrad_group)
 
 plus ``residual + x W^T`` with the residual add fused into the forward GEMM's
-epilogue (linear_residual; modeling_llama.py:323 rounds the projection output
-to bf16, then the sum), and the q/k/v projection followed by the rotary
+epilogue (linear_residual, the down projection; modeling_llama.py:323 rounds
+the projection output to bf16, then the sum: routed by its own table entry,
+``nt_res``, which compares the hand-written GEMM with that epilogue against
+the library GEMM followed by fh_add), and the q/k/v projection followed by the rotary
 embedding of its k heads (linear_rope: the GEMM, then fh_rope_fwd; the
 attention forward rotates q as it loads it).  fh_gemm_bf16_rope, the
 rotation in the GEMM's epilogue, measured slower than the plain GEMM and the
@@ -81,7 +83,7 @@ def reset_gemm_dispatch_counts() -> None:
 def _library_shapes() -> dict[str, set]:
     global _table
     if _table is None:
-        shapes: dict[str, set] = {"nt": set(), "nn": set(), "tn": set()}
+        shapes: dict[str, set] = {"nt": set(), "nn": set(), "tn": set(), "nt_res": set()}
         if TABLE_FILE.is_file():
             data = json.loads(TABLE_FILE.read_text())
             for op in shapes:
@@ -133,7 +135,7 @@ def linear_residual(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor) ->
     """residual + to_dtype(x @ w^T), written into `residual`'s memory (the
     hand-written GEMM's residual epilogue; otherwise the library GEMM followed
     by fh_add into `residual`)."""
-    if _count(residual.is_contiguous() and _choose_hand("nt", x, w)):
+    if _count(residual.is_contiguous() and _choose_hand("nt", x, w, "nt_res")):
         return ops.gemm("nt", x, w, residual=residual, out=residual)
     m = torch.mm(x, w.t())
     if not residual.is_contiguous():
@@ -211,7 +213,7 @@ def measure_dispatch(workloads: dict, path: str | Path = TABLE_FILE, *, iters: i
 
     dev, bf = "cuda", torch.bfloat16
     g = torch.Generator(device=dev).manual_seed(0)
-    lib_faster: dict[str, list] = {"nt": [], "nn": [], "tn": []}
+    lib_faster: dict[str, list] = {"nt": [], "nn": [], "tn": [], "nt_res": []}
     rows = []
 
     def one(fn) -> float:
@@ -249,9 +251,27 @@ def measure_dispatch(workloads: dict, path: str | Path = TABLE_FILE, *, iters: i
             log(f"[gemm-dispatch] {name} {op} m={m} n={n} k={k}: hand {t_hand:.1f} us, "
                 f"library {t_lib:.1f} us")
             del a, b
+        # The down projection's residual form (linear_residual): the hand-written
+        # GEMM with the residual add in its epilogue against the library GEMM
+        # followed by fh_add.
+        m, n, k = T, H, F
+        a = torch.randn(m, k, device=dev, generator=g).to(bf)
+        b = torch.randn(n, k, device=dev, generator=g).to(bf)
+        r = torch.randn(m, n, device=dev, generator=g).to(bf)
+        out = torch.empty_like(r)
+        t_hand, t_lib = timed_pair(lambda: ops.gemm("nt", a, b, residual=r, out=out),
+                                   lambda: ops.add(r, torch.mm(a, b.t()), out=out))
+        rows.append(dict(workload=name, op="nt_res", m=m, n=n, k=k, hand_us=round(t_hand, 1),
+                         library_us=round(t_lib, 1)))
+        if t_lib * LIBRARY_MARGIN < t_hand and [m, n, k] not in lib_faster["nt_res"]:
+            lib_faster["nt_res"].append([m, n, k])
+        log(f"[gemm-dispatch] {name} nt_res m={m} n={n} k={k}: hand + residual epilogue {t_hand:.1f} us, "
+            f"library + fh_add {t_lib:.1f} us")
+        del a, b, r, out
     data = {"note": "shapes (m, n, k of fh_gemm_bf16) where the tuned library GEMM measured at least 2% "
                     "faster than the hand-written kernel on an MI355X (medians of alternating runs); "
-                    "everything else runs hand-written",
+                    "everything else runs hand-written. nt_res: the down projection with its residual "
+                    "add (hand-written epilogue against library GEMM + fh_add)",
             "library": lib_faster, "measurements": rows}
     Path(path).write_text(json.dumps(data, indent=1) + "\n")
     global _table
