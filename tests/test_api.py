@@ -241,3 +241,23 @@ def test_linear_weight_accepts_tensor_parallel_wrappers_at_world_size_1():
     for bad in (Col(ws=2), Col(gather=True), Col(bias=True), Row(ws=2), Row(scatter=True),
                 torch.nn.Linear(8, 4)):
         assert _linear_weight(bad) is None
+
+
+def test_dispatch_table_routes_the_residual_form_by_its_own_entry():
+    """The shipped table carries the four forms (nt, nn, tn and the down
+    projection's residual form nt_res) and linear_residual consults nt_res."""
+    import inspect
+    import json
+
+    from femtotron_amd import projections
+    table = projections._library_shapes()
+    assert set(table) == {"nt", "nn", "tn", "nt_res"}
+    data = json.loads(projections.TABLE_FILE.read_text())
+    measured = {(r["op"], r["m"], r["n"], r["k"]) for r in data["measurements"]}
+    for op, shapes in table.items():
+        for m, n, k in shapes:
+            assert (op, m, n, k) in measured, (op, m, n, k)
+    # every nt_res entry is a down projection (n = hidden, k = ffn) measured as such
+    assert all(r["op"] != "nt_res" or (r["m"], r["n"], r["k"]) in {(m, n, k) for _, m, n, k in measured if _ == "nt"}
+               for r in data["measurements"])
+    assert '"nt_res"' in inspect.getsource(projections.linear_residual)

@@ -116,6 +116,29 @@ def test_fused_layer_at_least_as_accurate_as_reference_bf16(name, c, B, S):
         assert eg <= 1.25 * er + 1e-3, f"{name} {tag}: fused err {eg:.2e} vs reference bf16 err {er:.2e}"
 
 
+@pytest.mark.parametrize("policy", ["hand", "library"])
+@pytest.mark.parametrize("name,c,B,S", [("tinyllama-2048tok", CFG3, 1, 2048), ("llama3-512tok", CFG4, 1, 512)])
+def test_fused_layer_under_each_gemm_policy_matches_stock_checkpoint(policy, name, c, B, S):
+    """Every projection GEMM on the hand-written kernel (NT forward and
+    recompute, the down projection's residual epilogue, NN, TN and the grouped
+    weight gradients), or every one on the library: the layer still matches
+    the HF layer under torch.utils.checkpoint, and the routing counters show
+    that the policy held."""
+    from femtotron_amd import projections
+    projections.reset_gemm_dispatch_counts()
+    projections.set_gemm_policy(policy)
+    try:
+        got = _run_layer(c, B, S, torch.bfloat16, fused=True)
+        counts = projections.gemm_dispatch_counts()
+    finally:
+        projections.set_gemm_policy("auto")
+    torch.cuda.synchronize()
+    ref = _run_layer(c, B, S, torch.bfloat16, fused=False)
+    _compare(got, ref, BF16_RTOL, BF16_ATOL, f"{name}-{policy}")
+    # forward 4 (q/k/v, o, gate/up, down) + recompute 3 + backward 4 NN and 4 TN
+    assert counts == ({"hand": 15, "library": 0} if policy == "hand" else {"hand": 0, "library": 15}), counts
+
+
 def test_weight_gradients_on_side_stream_match_serial_bitwise():
     """The weight-gradient GEMMs give the same bits whether they run in series
     with the input-gradient chain (the default) or on a side stream: every
