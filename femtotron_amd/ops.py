@@ -464,6 +464,9 @@ def gemm_grouped(op: str, items: list) -> list:
     k = ks.pop()
     code = _GEMM_OPS[op]
     a0 = items[0][0]
+    if any(t is not None and t.device != a0.device for item in items for t in item) or \
+            any(o.device != a0.device for o in outs):
+        raise ValueError(f"gemm_grouped({op}): every operand and output must be on {a0.device}")
     nbytes = _lib.lib().fh_gemm_bf16_grouped_workspace_size(code, len(items), probs, k)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=a0.device) if nbytes else None
     _lib.call("fh_gemm_bf16_grouped", code, len(items), probs, k, _ptr(ws), _stream(a0))
