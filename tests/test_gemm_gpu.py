@@ -164,39 +164,43 @@ def test_residual_epilogue_rounds_like_the_unfused_add(op, m, n, k):
     assert torch.equal(inplace, fused)
 
 
-@pytest.mark.parametrize("shapes,k,one_launch", [
+@pytest.mark.parametrize("op,shapes,k,one_launch", [
     # the layer's q/k/v, o and down weight gradients at config 3: 80 + 64 + 176
     # tiles, one stream launch (a whole round, then 64 tail tiles in XCD slabs)
-    ([(2560, 2048), (2048, 2048), (2048, 5632)], 16384, True),
-    ([(2560, 2048), (2048, 2048), (2048, 5632)], 256, True),       # 4 k-steps
-    ([(6144, 4096), (4096, 4096), (4096, 14336)], 1024, True),     # config 4's: six whole rounds, no tail
-    ([(520, 264), (1032, 776)], 8192, False),                      # ragged, too few tiles: one call each
+    ("tn", [(2560, 2048), (2048, 2048), (2048, 5632)], 16384, True),
+    ("tn", [(2560, 2048), (2048, 2048), (2048, 5632)], 256, True),       # 4 k-steps
+    ("tn", [(6144, 4096), (4096, 4096), (4096, 14336)], 1024, True),     # config 4's: six whole rounds, no tail
+    ("tn", [(520, 264), (1032, 776)], 8192, False),                      # ragged, too few tiles: one call each
+    ("tn", [(2600, 2056), (2048, 2048), (2048, 5640)], 4096, True),      # ragged edge tiles in one launch
+    ("nn", [(4096, 2048), (4096, 2560)], 2048, True),                    # the other layouts: 128 + 160 tiles
+    ("nt", [(4096, 2048), (4104, 2568)], 2048, True),
 ])
-def test_grouped_tn_matches_each_product_and_accumulates(shapes, k, one_launch):
+def test_grouped_matches_each_product_and_accumulates(op, shapes, k, one_launch):
     """fh_gemm_bf16_grouped: every problem within the product's bound, bitwise
     repeatable, and with residual == C the accumulating epilogue
     to_bf16(R + to_bf16(A^T B)) bit for bit (whole tiles in the GEMM, split ones
     in the fixup); a group whose tiles do not fill a round runs as separate
     fh_gemm_bf16 calls."""
     g = torch.Generator(device=DEV).manual_seed(k + len(shapes))
-    ops_ = [_operands("tn", m, n, k, g) for m, n in shapes]
+    ops_ = [_operands(op, m, n, k, g) for m, n in shapes]
     probs = (_lib.FhGemmProblem * len(shapes))()
     for i, ((a, b), (m, n)) in enumerate(zip(ops_, shapes)):
         probs[i] = _lib.FhGemmProblem(a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), None, n, None, 0, m, n)
-    ws = _lib.lib().fh_gemm_bf16_grouped_workspace_size(_lib.FH_GEMM_TN, len(shapes), probs, k)
+    code = {"nt": _lib.FH_GEMM_NT, "nn": _lib.FH_GEMM_NN, "tn": _lib.FH_GEMM_TN}[op]
+    ws = _lib.lib().fh_gemm_bf16_grouped_workspace_size(code, len(shapes), probs, k)
     cus = torch.cuda.get_device_properties(0).multi_processor_count // 8 * 8
     if one_launch:
         assert ws == 2 * cus * 256 * 256 * 4
-    outs = ops.gemm_grouped("tn", [(a, b, None, None) for a, b in ops_])
+    outs = ops.gemm_grouped(op, [(a, b, None, None) for a, b in ops_])
     for (a, b), c in zip(ops_, outs):
-        _check("tn", a, b, c, exact=True)
-    again = ops.gemm_grouped("tn", [(a, b, None, None) for a, b in ops_])
+        _check(op, a, b, c, exact=True)
+    again = ops.gemm_grouped(op, [(a, b, None, None) for a, b in ops_])
     assert all(torch.equal(x, y) for x, y in zip(outs, again))
     if not one_launch:  # separate calls: each is its own fh_gemm_bf16
-        assert all(torch.equal(c, ops.gemm("tn", a, b)) for (a, b), c in zip(ops_, outs))
+        assert all(torch.equal(c, ops.gemm(op, a, b)) for (a, b), c in zip(ops_, outs))
     rs = [torch.randn(m, n, device=DEV, generator=g).to(BF) for m, n in shapes]
     acc = [r.clone() for r in rs]
-    got = ops.gemm_grouped("tn", [(a, b, x, x) for (a, b), x in zip(ops_, acc)])
+    got = ops.gemm_grouped(op, [(a, b, x, x) for (a, b), x in zip(ops_, acc)])
     for r, x, y, c in zip(rs, acc, got, outs):
         assert y.data_ptr() == x.data_ptr()
         assert torch.equal(x, (r.float() + c.float()).to(BF))
