@@ -237,6 +237,8 @@ struct RunPlan {
   __device__ __forceinline__ void load(int64_t k_off, int jj, uint32_t lds_slot) const {
     dma16(off[KO ? 0 : jj], run[jj] + k_off, lds_slot);
   }
+  // load() with M0 already holding lds_slot (set_m0 at least one instruction earlier).
+  __device__ __forceinline__ void load_m0(int64_t k_off, int jj) const { dma16_m0(off[KO ? 0 : jj], run[jj] + k_off); }
 };
 
 __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
@@ -327,6 +329,13 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* ring, int t, 
     if constexpr (OP == 0) pa.load(k0 * pa.k_bytes, jj, lds_slot);
     else pb.load(k0 * pb.k_bytes, jj, lds_slot);
   };
+  // The loop's form: M0 set one MFMA earlier (set_m0), so the load needs no s_nop.
+  auto dma_m0 = [&](auto op_tag, int step, int jj) __attribute__((always_inline)) {
+    constexpr int OP = decltype(op_tag)::value;
+    const int64_t k0 = static_cast<int64_t>(s_begin + min(step, nst - 1)) * kTk;
+    if constexpr (OP == 0) pa.load_m0(k0 * pa.k_bytes, jj);
+    else pb.load_m0(k0 * pb.k_bytes, jj);
+  };
   using OpA = std::integral_constant<int, 0>;
   using OpB = std::integral_constant<int, 1>;
 
@@ -395,7 +404,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* ring, int t, 
 #pragma unroll
     for (int p = 0; p < 64; ++p) {
       if ((p & 3) == 0) rd1(s, sB, 1, 1, p >> 2);
-      if ((p & 7) == 2) dma(OpA(), x + 2, fA, p >> 3);
+      if ((p & 7) == 1) set_m0(ring0 + fA * kSlot + (p >> 3) * 1024);
+      if ((p & 7) == 2) dma_m0(OpA(), x + 2, p >> 3);
       mf1(0, p);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -405,7 +415,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* ring, int t, 
 #pragma unroll
     for (int p = 0; p < 64; ++p) {
       if ((p & 3) == 0) rd1(nA, nB, 0, 0, p >> 2);
-      if ((p & 7) == 2) dma(OpB(), x + 2, s, p >> 3);
+      if ((p & 7) == 1) set_m0(ring0 + s * kSlot + (p >> 3) * 1024);
+      if ((p & 7) == 2) dma_m0(OpB(), x + 2, p >> 3);
       mf1(1, p);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -665,7 +676,8 @@ __device__ __forceinline__ void gemm_persist(const GemmArgs& g, char* ring, int 
 #pragma unroll
       for (int p = 0; p < 64; ++p) {
         if ((p & 3) == 0) rd1(s, sB, 1, 1, p >> 2);
-        if ((p & 7) == 2) dma16(offa[p >> 3], srcA, dA + (p >> 3) * 1024);
+        if ((p & 7) == 1) set_m0(dA + (p >> 3) * 1024);
+        if ((p & 7) == 2) dma16_m0(offa[p >> 3], srcA);
         mf1(0, p);
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -675,7 +687,8 @@ __device__ __forceinline__ void gemm_persist(const GemmArgs& g, char* ring, int 
 #pragma unroll
       for (int p = 0; p < 64; ++p) {
         if ((p & 3) == 0) rd1(nA, nB, 0, 0, p >> 2);
-        if ((p & 7) == 2) dma16(offb[p >> 3], srcB, dB + (p >> 3) * 1024);
+        if ((p & 7) == 1) set_m0(dB + (p >> 3) * 1024);
+        if ((p & 7) == 2) dma16_m0(offb[p >> 3], srcB);
         mf1(1, p);
         __builtin_amdgcn_sched_barrier(0);
       }

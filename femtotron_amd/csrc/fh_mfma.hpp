@@ -134,12 +134,22 @@ __device__ __forceinline__ void dma_tile(const uint16_t* src, int64_t ld, int r0
 // One 1 KB direct-to-LDS copy as inline asm: lane i loads the 16 bytes at
 // sbase + voff into LDS at lds + 16 i.  M0 carries the LDS address, set in the
 // same statement; nothing else in these kernels uses M0, which the compiler
-// reserves (hence the diagnostic it would print for the clobber).
+// reserves (hence the diagnostic it would print for the clobber).  An LDS DMA
+// that reads M0 right after an SALU write of it needs one wait state (gfx9;
+// the compiler puts the same s_nop before the loads it emits itself).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
                : "memory", "m0");
+}
+
+// dma16 in two statements for loops that put an MFMA between them (its issue
+// is the wait state): set_m0(lds), then dma16_m0(voff, sbase).  Volatile asm
+// keeps the two in order; nothing between them may write M0.
+__device__ __forceinline__ void set_m0(uint32_t lds) { asm volatile("s_mov_b32 m0, %0" ::"s"(lds) : "m0"); }
+__device__ __forceinline__ void dma16_m0(uint32_t voff, const void* sbase) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase) : "memory");
 }
 #pragma clang diagnostic pop
 
