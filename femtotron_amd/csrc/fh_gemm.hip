@@ -145,14 +145,6 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return c;
 }
 
-// The first MFMA of an accumulator: C = 0 as an inline constant, so the
-// accumulators need no zeroing by VALU writes.
-__device__ __forceinline__ f32x4 mfma16z(bf16x8 a, bf16x8 b) {
-  f32x4 c;
-  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
-  return c;
-}
-
 // 16x16x32 KC fragment: lane i reads row i%16, k chunk i/16 of a k32 step
 // (chunk 4 ks + i/16 of the row's eight; rows o..o+15 of the [256 x 64] tile,
 // o a multiple of 16, share swz<64>, which depends on row bits 1..3 only).
