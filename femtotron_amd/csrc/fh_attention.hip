@@ -679,7 +679,7 @@ __device__ __forceinline__ void dkdv_tile(const char* Q, const char* G, const fl
     const int lo = ki - qh - 4 * hl, hi = ki < S ? S - qh - 4 * hl : lo;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const bool dead = (acc_row(j, 0) < lo) | (acc_row(j, 0) >= hi);
+      const bool dead = static_cast<int>(acc_row(j, 0) < lo) | static_cast<int>(acc_row(j, 0) >= hi);
       x[j] = dead ? 0.f : x[j];
       y[j] = dead ? 0.f : y[j];
     }
