@@ -951,7 +951,7 @@ __global__ __launch_bounds__(DkdvTiles<HD>::NT) __attribute__((amdgpu_waves_per_
             const int lo = ki - q0 - 32 * u - 4 * hl, hi = ki < S ? S - q0 - 32 * u - 4 * hl : lo;
 #pragma unroll
             for (int j = 0; j < 16; ++j)
-              x[u][j] = ((acc_row(j, 0) < lo) | (acc_row(j, 0) >= hi)) ? 0.f : x[u][j];
+              x[u][j] = (static_cast<int>(acc_row(j, 0) < lo) | static_cast<int>(acc_row(j, 0) >= hi)) ? 0.f : x[u][j];
           }
 #pragma unroll
           for (int g = 0; g < 4; ++g)
