@@ -68,6 +68,12 @@ struct Elem<uint16_t> {
   __device__ __forceinline__ static Raw ldraw(const uint16_t* p) {
     return *reinterpret_cast<const uint4*>(p);
   }
+  // ldraw as a non-temporal (streaming) load: data read once.
+  __device__ __forceinline__ static Raw ldraw_stream(const uint16_t* p) {
+    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+    const v4u t = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    return make_uint4(t.x, t.y, t.z, t.w);
+  }
   __device__ __forceinline__ static void unpack(const Raw& q, float v[8]) {
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
@@ -110,6 +116,12 @@ struct Elem<float> {
   };
   __device__ __forceinline__ static Raw ldraw(const float* p) {
     return Raw{*reinterpret_cast<const float4*>(p), *reinterpret_cast<const float4*>(p + 4)};
+  }
+  __device__ __forceinline__ static Raw ldraw_stream(const float* p) {
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    const v4f a = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(p));
+    const v4f b = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(p + 4));
+    return Raw{make_float4(a.x, a.y, a.z, a.w), make_float4(b.x, b.y, b.z, b.w)};
   }
   __device__ __forceinline__ static void unpack(const Raw& q, float v[8]) {
     v[0] = q.a.x; v[1] = q.a.y; v[2] = q.a.z; v[3] = q.a.w;

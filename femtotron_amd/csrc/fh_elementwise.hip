@@ -55,6 +55,15 @@ __device__ __forceinline__ void row_col(int64_t idx, int cpr, const FastDiv& fd,
   }
 }
 
+// SwiGLU's inputs are read once: non-temporal loads.  Kernel-only, warm
+// step shapes (T = 16384, F = 5632): forward 95.6 -> 82.6 us, backward 200 ->
+// 197 us; cold at config 2: forward 54.5 -> 55.0, backward 110 -> 102 us.  The
+// same loads in the add and RMSNorm kernels measured no different.
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::Raw sw_load(const T* p) {
+  return Elem<T>::ldraw_stream(p);
+}
+
 inline bool wide(int64_t n) { return n >= (int64_t(1) << 32); }
 
 // One thread = 8 rotation pairs (i, i + d/2) of up to kRopeHG heads of one
@@ -146,8 +155,8 @@ __global__ __launch_bounds__(256) void k_swiglu_fwd(const T* __restrict__ g,
       int64_t r;
       int c;
       row_col<WIDE>(idx, cpr, fd, r, c);
-      gr[k] = Elem<T>::ldraw(g + r * ld_gu + c);
-      ur[k] = Elem<T>::ldraw(u + r * ld_gu + c);
+      gr[k] = sw_load<T>(g + r * ld_gu + c);
+      ur[k] = sw_load<T>(u + r * ld_gu + c);
     }
   }
 #pragma unroll
@@ -190,9 +199,9 @@ __global__ __launch_bounds__(256) void k_swiglu_bwd(const T* dp, int64_t ld_dp,
       int64_t r;
       int c;
       row_col<WIDE>(idx, cpr, fd, r, c);
-      dr[k] = Elem<T>::ldraw(dp + r * ld_dp + c);
-      gr[k] = Elem<T>::ldraw(g + r * ld_gu + c);
-      ur[k] = Elem<T>::ldraw(u + r * ld_gu + c);
+      dr[k] = sw_load<T>(dp + r * ld_dp + c);
+      gr[k] = sw_load<T>(g + r * ld_gu + c);
+      ur[k] = sw_load<T>(u + r * ld_gu + c);
     }
   }
 #pragma unroll
