@@ -117,6 +117,13 @@ struct GemmArgs {
   GemmProblem grp[kMaxGroup];
 };
 
+// Two bf16 sums res + c of packed pairs, each rounded to bf16 (the residual
+// add of a bf16 projection output: torch's bf16 + bf16).
+__device__ __forceinline__ uint32_t add_bf16x2(uint32_t res, uint32_t c) {
+  return pk_bf16(__uint_as_float(res << 16) + __uint_as_float(c << 16),
+                 __uint_as_float(res & 0xffff0000u) + __uint_as_float(c & 0xffff0000u));
+}
+
 // 8 outputs of the forward rotation (rope_fwd_one) from this chunk x, its
 // partner chunk p (hd/2 columns away in the head), and the cos / signed sin
 // chunks of its own columns.
@@ -526,12 +533,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* ring, int t, 
       if (mrow >= g.m || col >= g.n) continue;
       if (EPI == EPI_RESIDUAL || (EPI == EPI_STREAM && g.r != nullptr)) {
         const uint4 rv = *reinterpret_cast<const uint4*>(g.r + mrow * g.ldr + col);
-        auto add2 = [](uint32_t res, uint32_t c) {
-          return pk_bf16(__uint_as_float(res << 16) + __uint_as_float(c << 16),
-                         __uint_as_float(res & 0xffff0000u) + __uint_as_float(c & 0xffff0000u));
-        };
-        *reinterpret_cast<uint4*>(g.c + mrow * g.ldc + col) =
-            make_uint4(add2(rv.x, v.x), add2(rv.y, v.y), add2(rv.z, v.z), add2(rv.w, v.w));
+        *reinterpret_cast<uint4*>(g.c + mrow * g.ldc + col) = make_uint4(
+            add_bf16x2(rv.x, v.x), add_bf16x2(rv.y, v.y), add_bf16x2(rv.z, v.z), add_bf16x2(rv.w, v.w));
       } else {
         *reinterpret_cast<uint4*>(g.c + mrow * g.ldc + col) = v;
       }
@@ -587,7 +590,7 @@ __device__ __forceinline__ const char* whole_base(const uint16_t* base, int64_t 
 // this saves, per tile, the prologue (two stages loaded and the first waited
 // for), the output's round trip through LDS with its barriers, and the gap
 // between a CU's consecutive workgroups.
-template <bool A_KO, bool B_KO>
+template <bool A_KO, bool B_KO, bool RESID>
 __device__ __forceinline__ void gemm_persist(const GemmArgs& g, char* ring, int lid) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -696,8 +699,22 @@ __device__ __forceinline__ void gemm_persist(const GemmArgs& g, char* ring, int 
     // which lane g holds 8 consecutive columns, 8 (g/2) .. +7 of block
     // i + g%2: one 16-byte store (64 contiguous bytes per row and store).
     // The form runs whole tiles only.
-    uint16_t* cp = g.c + static_cast<int64_t>(m0 + wm16 + (lane & 15)) * g.ldc + n0 + wn16 +
-                   16 * ((lane >> 4) & 1) + 8 * (lane >> 5);
+    const int64_t lane_row = m0 + wm16 + (lane & 15);
+    const int lane_col = n0 + wn16 + 16 * ((lane >> 4) & 1) + 8 * (lane >> 5);
+    uint16_t* cp = g.c + lane_row * g.ldc + lane_col;
+    // RESID: C = bf16(R + bf16(A B^T)) (R may be C itself: each lane reads its
+    // own chunks before it writes them).  All 32 residual chunks are loaded
+    // before the first store, so no load waits behind a store that might
+    // alias it.
+    uint4 rv[RESID ? 32 : 1];
+    if constexpr (RESID) {
+      const uint16_t* rp = g.r + lane_row * g.ldr + lane_col;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          rv[4 * j + q] = *reinterpret_cast<const uint4*>(rp + static_cast<int64_t>(16 * j) * g.ldr + 32 * q);
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j)
 #pragma unroll
@@ -705,8 +722,12 @@ __device__ __forceinline__ void gemm_persist(const GemmArgs& g, char* ring, int 
         const f32x4 v0 = acc[2 * q][j], v1 = acc[2 * q + 1][j];
         const auto lo = __builtin_amdgcn_permlane16_swap(pk_bf16(v0[0], v0[1]), pk_bf16(v1[0], v1[1]), false, false);
         const auto hi = __builtin_amdgcn_permlane16_swap(pk_bf16(v0[2], v0[3]), pk_bf16(v1[2], v1[3]), false, false);
-        *reinterpret_cast<uint4*>(cp + static_cast<int64_t>(16 * j) * g.ldc + 32 * q) =
-            make_uint4(lo[0], hi[0], lo[1], hi[1]);
+        uint4 o = make_uint4(lo[0], hi[0], lo[1], hi[1]);
+        if constexpr (RESID) {
+          const uint4 r = rv[4 * j + q];
+          o = make_uint4(add_bf16x2(r.x, o.x), add_bf16x2(r.y, o.y), add_bf16x2(r.z, o.z), add_bf16x2(r.w, o.w));
+        }
+        *reinterpret_cast<uint4*>(cp + static_cast<int64_t>(16 * j) * g.ldc + 32 * q) = o;
       }
     __builtin_amdgcn_sched_barrier(0);
     if (!more) break;
@@ -783,11 +804,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
 // The persistent form (gemm_persist): G = gridDim.x workgroups, a multiple of
 // 8, at most the number of tiles.
-template <bool A_KO, bool B_KO>
+template <bool A_KO, bool B_KO, bool RESID>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_gemm_persist(GemmArgs g) {
   __shared__ __align__(16) char ring[kRing * kSlot];
   const int nb8 = gridDim.x >> 3;
-  gemm_persist<A_KO, B_KO>(g, ring, (blockIdx.x & 7) * nb8 + (blockIdx.x >> 3));
+  gemm_persist<A_KO, B_KO, RESID>(g, ring, (blockIdx.x & 7) * nb8 + (blockIdx.x >> 3));
 }
 
 // Rows blockIdx.y * 16 .. +15 of tail tile blockIdx.x of a stream GEMM: if
@@ -1056,13 +1077,19 @@ int gemm_run(int op, GemmArgs& g, int slices, bool stream_form, void* workspace,
   }
   g.steps_per_slice = (g.total_steps + slices - 1) / slices;
 #if FH_GEMM_PERSIST
-  if (slices == 1 && g.r == nullptr && g.rope.cos == nullptr && g.total_steps >= 2 && g.m % kTm == 0 &&
-      g.n % kTn == 0 && g.lda < (int64_t(1) << 24) && g.ldb < (int64_t(1) << 24) && g.tiles > stream_grid()) {
+  // The residual epilogue in this form: the forward (NT) layout only.
+  if (slices == 1 && (g.r == nullptr || op == FH_GEMM_NT) && g.rope.cos == nullptr && g.total_steps >= 2 &&
+      g.m % kTm == 0 && g.n % kTn == 0 && g.lda < (int64_t(1) << 24) && g.ldb < (int64_t(1) << 24) &&
+      g.tiles > stream_grid()) {
     g.grid = stream_grid();
+    if (g.r != nullptr) {
+      hipLaunchKernelGGL((k_gemm_persist<false, false, true>), dim3(g.grid), dim3(256), 0, stream, g);
+      return FH_OK;
+    }
     switch (op) {
-      case FH_GEMM_NT: hipLaunchKernelGGL((k_gemm_persist<false, false>), dim3(g.grid), dim3(256), 0, stream, g); break;
-      case FH_GEMM_NN: hipLaunchKernelGGL((k_gemm_persist<false, true>), dim3(g.grid), dim3(256), 0, stream, g); break;
-      default: hipLaunchKernelGGL((k_gemm_persist<true, true>), dim3(g.grid), dim3(256), 0, stream, g); break;
+      case FH_GEMM_NT: hipLaunchKernelGGL((k_gemm_persist<false, false, false>), dim3(g.grid), dim3(256), 0, stream, g); break;
+      case FH_GEMM_NN: hipLaunchKernelGGL((k_gemm_persist<false, true, false>), dim3(g.grid), dim3(256), 0, stream, g); break;
+      default: hipLaunchKernelGGL((k_gemm_persist<true, true, false>), dim3(g.grid), dim3(256), 0, stream, g); break;
     }
     return FH_OK;
   }

@@ -136,6 +136,23 @@ def test_stream_form_residual_epilogue_rounds_like_the_unfused_add(op, m, n, k):
     assert torch.equal(inplace, fused)
 
 
+@pytest.mark.parametrize("m,n,k", [(16384, 2048, 5632), (6144, 3072, 512)])
+def test_persistent_form_residual_epilogue_rounds_like_the_unfused_add(m, n, k):
+    """The persistent form's residual epilogue (the down projection at config
+    3: 512 tiles, two whole rounds; 288 tiles: a partial second round) gives
+    to_bf16(R + to_bf16(A.B^T)) bit for bit, also in place (R = C)."""
+    g = torch.Generator(device=DEV).manual_seed(m + k)
+    a, b = _operands("nt", m, n, k, g)
+    r = torch.randn(m, n, device=DEV, generator=g).to(BF)
+    product = ops.gemm("nt", a, b)
+    _check("nt", a, b, product, exact=True)
+    fused = ops.gemm("nt", a, b, residual=r)
+    assert torch.equal(fused, (r.float() + product.float()).to(BF))
+    inplace = r.clone()
+    ops.gemm("nt", a, b, residual=inplace, out=inplace)
+    assert torch.equal(inplace, fused)
+
+
 def test_split_k_path_is_used_and_matches():
     # 512 x 512 outputs are 4 tiles: the k range is split into slices
     m = n = 512
