@@ -92,10 +92,10 @@ def parse_args():
     ap.add_argument("--tune-gemms", default=None, metavar="CSV",
                     help="run TunableOp's search for every projection GEMM of --workload, write "
                          "the results to CSV and exit")
-    ap.add_argument("--gemm", choices=("auto", "hand", "library"), default="auto",
-                    help="projection GEMMs: per-shape choice from the measured table "
-                         "(femtotron_amd/tuned/gemm_dispatch_gfx950.json), the hand-written "
-                         "fh_gemm_bf16 wherever it applies, or the library GEMM")
+    ap.add_argument("--gemm", choices=("hand", "auto", "library"), default="hand",
+                    help="projection GEMMs: the hand-written fh_gemm_bf16 wherever it applies (the "
+                         "default), the per-shape choice of the measured table "
+                         "(femtotron_amd/tuned/gemm_dispatch_gfx950.json), or the library GEMM")
     ap.add_argument("--wgrad-stream", choices=("serial", "side"), default="serial",
                     help="weight-gradient GEMMs in series with the input-gradient chain (measured "
                          "faster with the hand-written GEMMs) or on a side stream next to it")
@@ -108,6 +108,9 @@ def parse_args():
     ap.add_argument("--stock-attention", action="store_true",
                     help="under --ac selective keep HF's LlamaAttention outside the checkpoints "
                          "(no fuse_attention)")
+    ap.add_argument("--no-auto-gemm-step", action="store_true",
+                    help="under --gemm hand, skip the second timing of the step with the measured "
+                         "table's routing (--gemm auto)")
     ap.add_argument("--no-chain", action="store_true",
                     help="skip the BASELINE config 2 op-level table of the memory-bound chain")
     ap.add_argument("--no-optimizer", action="store_true",
@@ -970,6 +973,20 @@ def main() -> int:
     gemm_counts = {k: v // n_steps for k, v in gemm_counts.items()}
     log(f"fused: {sec * 1e3:.2f} ms/step, {tok_s:.0f} tokens/s; projection GEMMs per step: "
         f"{gemm_counts['hand']} hand-written, {gemm_counts['library']} library")
+    auto_step = None
+    if args.gemm == "hand" and not args.no_auto_gemm_step:
+        # The same step with the forward (NT) GEMMs the measured table gives the
+        # library on it: a reported comparison, not the metric.
+        projections.set_gemm_policy("auto")
+        projections.reset_gemm_dispatch_counts()
+        asec = time_steps(torch, model, ids, args.steps, args.warmup, materialize_logits=not fused_head)
+        acounts_g = {k: v // n_steps for k, v in projections.gemm_dispatch_counts().items()}
+        projections.set_gemm_policy("hand")
+        auto_step = {"tokens_per_s": round(T / asec, 1), "ms_per_step": round(asec * 1e3, 3),
+                     "projection_gemms_per_step": acounts_g,
+                     "note": "the same step under --gemm auto (the library where the table measured it "
+                             "faster), timed after the metric's steps"}
+        log(f"same step, --gemm auto: {asec * 1e3:.2f} ms/step, {T / asec:.0f} tokens/s")
 
     log("per-kernel HIP-event timings at the step's shapes")
     rows, mfma = kernel_table(torch, c, args.kernel_iters, args.ac, boundary=bool(boundary),
@@ -1102,6 +1119,7 @@ def main() -> int:
         "mfma_kernels": mfma,
         "gemms": {"policy": args.gemm,
                   "projection_gemms_per_step": gemm_counts,
+                  "step_under_auto_policy": auto_step,
                   "hand_written": "fh_gemm_bf16 (femtotron_amd/csrc/fh_gemm.hip)",
                   "library": ("hipBLASLt/rocBLAS, TunableOp solutions from femtotron_amd/tuned/"
                               "tunableop_gfx950.csv" if tuned else "hipBLASLt default heuristics"),

@@ -261,3 +261,24 @@ def test_dispatch_table_routes_the_residual_form_by_its_own_entry():
     assert all(r["op"] != "nt_res" or (r["m"], r["n"], r["k"]) in {(m, n, k) for _, m, n, k in measured if _ == "nt"}
                for r in data["measurements"])
     assert '"nt_res"' in inspect.getsource(projections.linear_residual)
+
+
+def test_default_gemm_policy_is_the_hand_written_kernel(monkeypatch):
+    """Out of the box every projection GEMM the kernel supports runs on
+    fh_gemm_bf16; the measured table is consulted only under policy 'auto'
+    (operand checks stubbed: no device here, no kernel runs)."""
+    import torch
+
+    from femtotron_amd import ops, projections
+    assert projections.gemm_policy() == "hand"
+    monkeypatch.setattr(ops, "gemm_supported", lambda op, a, b: True)
+    x = torch.empty(16384, 2048, dtype=torch.bfloat16, device="meta")
+    w = torch.empty(11264, 2048, dtype=torch.bfloat16, device="meta")
+    listed = ops.gemm_dims("nt", x, w) in projections._library_shapes()["nt"]
+    assert listed, "the shipped table lists the TinyLlama gate/up forward GEMM"
+    assert projections._choose_hand("nt", x, w)
+    projections.set_gemm_policy("auto")
+    try:
+        assert not projections._choose_hand("nt", x, w)
+    finally:
+        projections.set_gemm_policy("hand")

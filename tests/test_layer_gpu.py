@@ -126,12 +126,13 @@ def test_fused_layer_under_each_gemm_policy_matches_stock_checkpoint(policy, nam
     that the policy held."""
     from femtotron_amd import projections
     projections.reset_gemm_dispatch_counts()
+    before = projections.gemm_policy()
     projections.set_gemm_policy(policy)
     try:
         got = _run_layer(c, B, S, torch.bfloat16, fused=True)
         counts = projections.gemm_dispatch_counts()
     finally:
-        projections.set_gemm_policy("auto")
+        projections.set_gemm_policy(before)
     torch.cuda.synchronize()
     ref = _run_layer(c, B, S, torch.bfloat16, fused=False)
     _compare(got, ref, BF16_RTOL, BF16_ATOL, f"{name}-{policy}")
