@@ -265,6 +265,55 @@ __device__ __forceinline__ void kv_block_loop(const uint16_t* kb_ptr, int64_t ld
   }
 }
 
+// kv_block_loop with three LDS stages (the forward): block kb + 2's K and V are
+// loaded while block kb is multiplied, so each block's loads have two blocks'
+// time to land.  The barrier that ends a block waits for block kb + 1's loads
+// only (vmcnt: the vector memory counter retires a wave's loads in issue
+// order, and block kb + 2's loads are the wave's last ones), not for the ones
+// still in flight into the third stage.
+template <int BN, int HD, int NW, class Body, class Pre>
+__device__ __forceinline__ void kv_block_loop3(const uint16_t* kb_ptr, int64_t ldk, const uint16_t* vb_ptr,
+                                               int64_t ldv, int nkb, int S, char* sk0, char* sk1, char* sk2,
+                                               char* sv0, char* sv1, char* sv2, int wave, int lane, Body&& body,
+                                               Pre&& pre) {
+  using Dma = TileDma<BN, HD, NW>;
+  Dma dk, dv;
+  dk.init(ldk, wave, lane);
+  dv.init(ldv, wave, lane);
+  // Loads this wave issues per block (K and V alike, in either of TileDma's paths).
+  int per_wave = 0;
+#pragma unroll
+  for (int i = 0; i < Dma::PER; ++i) per_wave += (i * NW + wave < Dma::RUNS) ? 1 : 0;
+  // The loads as inline asm (load_asm): the compiler, which cannot see the
+  // waits below retire a stage's loads, would otherwise wait for every load
+  // in flight before reading a stage.
+  auto load = [&](int r0, char* KN, char* VN) __attribute__((always_inline)) {
+    dk.load_asm(kb_ptr, ldk, r0, S - 1, KN, wave, lane);
+    dv.load_asm(vb_ptr, ldv, r0, S - 1, VN, wave, lane);
+  };
+  load(0, sk0, sv0);
+  if (nkb > 1) load(BN, sk1, sv1);
+  pre();
+  // vmcnt(0) as the builtin, which the compiler's own wait placement sees: it
+  // then knows pre()'s loads have landed and puts no waits for them in the loop.
+  __builtin_amdgcn_s_waitcnt(0x0f70);
+  __syncthreads();
+  auto step = [&](int kb, const char* K, const char* V, char* KN, char* VN) __attribute__((always_inline)) {
+    const bool ahead = kb + 2 < nkb;
+    if (ahead) load((kb + 2) * BN, KN, VN);
+    if (kb < nkb) body(kb, K, V);
+    if (ahead && per_wave == 1) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    else if (ahead && per_wave == 2) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else wait_loads();
+    lds_barrier();
+  };
+  for (int kb = 0; kb < nkb; kb += 3) {
+    step(kb, sk0, sv0, sk2, sv2);
+    step(kb + 1, sk1, sv1, sk0, sv0);
+    step(kb + 2, sk2, sv2, sk1, sv1);
+  }
+}
+
 // One 64-key block of the forward for one wave: raw scores from K (LDS),
 // online softmax update of (m, l, oacc), then oacc += P V (V from LDS).
 template <int HD, int QT>
@@ -359,7 +408,10 @@ __global__ __launch_bounds__(256 * HPB) __attribute__((amdgpu_waves_per_eu(2))) 
     uint16_t* qout, int64_t ldqo) {
   constexpr int QT = FwdTiles<HD>::QT;
   constexpr int BM = 4 * 32 * QT, BN = 64, NS = HD / 16, ND = HD / 32, TILE = BN * 2 * HD;
-  __shared__ __align__(16) char sk0[TILE], sk1[TILE], sv0[TILE], sv1[TILE];
+  // Three K/V stages up to head_dim 64 (48 KB); at 128 three stages (96 KB)
+  // would leave room for one workgroup per CU, so two.
+  constexpr int STAGES = HD <= 64 ? 3 : 2, TILE3 = STAGES == 3 ? TILE : 16;
+  __shared__ __align__(16) char sk0[TILE], sk1[TILE], sk2[TILE3], sv0[TILE], sv1[TILE], sv2[TILE3];
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const XcdOrder ord = xcd_order();
@@ -402,15 +454,18 @@ __global__ __launch_bounds__(256 * HPB) __attribute__((amdgpu_waves_per_eu(2))) 
   const int nkb = (kend + BN - 1) / BN;
   const uint16_t* kb_ptr = k + tok0 * ldk + static_cast<int64_t>(kvh) * HD;
   const uint16_t* vb_ptr = v + tok0 * ldv + static_cast<int64_t>(kvh) * HD;
-  kv_block_loop<BN, HD, true, 4 * HPB>(kb_ptr, ldk, vb_ptr, ldv, nkb, S, sk0, sk1, sv0, sv1, wave, lane,
-                        [&](int kb, const char* K, const char* V) __attribute__((always_inline)) {
-                          refresh_offsets(a_off, b0, b8);
-                          const int k0 = kb * BN;
-                          if (k0 <= qw + 32 * QT - 1)  // some key of the block precedes some query of the wave
-                            fwd_block<HD, QT>(K, V, qf, oacc, m, l, a_off, b0, b8, k0, qw, l32, hl, S,
-                                              scale_log2);
-                        },
-                        load_q);
+  auto body = [&](int kb, const char* K, const char* V) __attribute__((always_inline)) {
+    refresh_offsets(a_off, b0, b8);
+    const int k0 = kb * BN;
+    if (k0 <= qw + 32 * QT - 1)  // some key of the block precedes some query of the wave
+      fwd_block<HD, QT>(K, V, qf, oacc, m, l, a_off, b0, b8, k0, qw, l32, hl, S, scale_log2);
+  };
+  if constexpr (STAGES == 3)
+    kv_block_loop3<BN, HD, 4 * HPB>(kb_ptr, ldk, vb_ptr, ldv, nkb, S, sk0, sk1, sk2, sv0, sv1, sv2, wave, lane,
+                                    body, load_q);
+  else
+    kv_block_loop<BN, HD, true, 4 * HPB>(kb_ptr, ldk, vb_ptr, ldv, nkb, S, sk0, sk1, sv0, sv1, wave, lane, body,
+                                         load_q);
 #pragma unroll
   for (int u = 0; u < QT; ++u) {
     const int qi = qw + 32 * u + l32;

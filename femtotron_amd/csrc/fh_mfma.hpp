@@ -144,6 +144,28 @@ __device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t
                : "memory", "m0");
 }
 
+// dma_tile with its loads as inline asm (dma16: the row base r0 in SGPRs, each
+// lane's clamped row as a 32-bit offset from it; r0 <= last).  The compiler
+// does not see these loads: the caller waits for them (vmcnt) itself.
+template <int ROWS, int HD, int NW>
+__device__ __forceinline__ void dma_tile_asm(const uint16_t* src, int64_t ld, int r0, int last, char* dst,
+                                             int wave, int lane) {
+  typedef __attribute__((address_space(3))) char* lptr;
+  constexpr int CPR = HD / 8, RPR = 64 / CPR, RUNS = ROWS / RPR;
+  static_assert(64 % CPR == 0 && ROWS % RPR == 0, "the tile is whole 1 KB runs");
+  const void* base = src + static_cast<int64_t>(r0) * ld;
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lptr)dst));
+#pragma unroll
+  for (int j0 = 0; j0 < RUNS; j0 += NW) {
+    const int j = j0 + wave;  // wave-uniform
+    if (RUNS % NW == 0 || j < RUNS) {
+      const int r = j * RPR + lane / CPR, c = (lane % CPR) ^ swz<HD>(r);
+      const int64_t rr = min(r0 + r, last) - r0;
+      dma16(static_cast<uint32_t>((rr * ld + c * 8) * 2), base, lds0 + j * 1024);
+    }
+  }
+}
+
 // dma16 in two statements for loops that put an MFMA between them (its issue
 // is the wait state): set_m0(lds), then dma16_m0(voff, sbase).  Volatile asm
 // keeps the two in order; nothing between them may write M0.
@@ -205,7 +227,7 @@ struct TileDma {
         if (RUNS % NW == 0 || j < RUNS) dma16(off[i], base, lds0 + j * 1024);
       }
     } else {
-      dma_tile<ROWS, HD, NW>(src, ld, r0, last, dst, wave, lane);
+      dma_tile_asm<ROWS, HD, NW>(src, ld, r0, last, dst, wave, lane);
     }
   }
 };
