@@ -136,18 +136,21 @@ def test_stream_form_residual_epilogue_rounds_like_the_unfused_add(op, m, n, k):
     assert torch.equal(inplace, fused)
 
 
-@pytest.mark.parametrize("m,n,k", [(16384, 2048, 5632), (6144, 3072, 512)])
-def test_persistent_form_residual_epilogue_rounds_like_the_unfused_add(m, n, k):
+@pytest.mark.parametrize("m,n,k,pad", [(16384, 2048, 5632, 0), (6144, 3072, 512, 0), (6144, 3072, 512, 64)])
+def test_persistent_form_residual_epilogue_rounds_like_the_unfused_add(m, n, k, pad):
     """The persistent form's residual epilogue (the down projection at config
-    3: 512 tiles, two whole rounds; 288 tiles: a partial second round) gives
+    3: 512 tiles, two whole rounds; 288 tiles: a partial second round; with
+    pad, R and C views of wider rows, ldr != ldc != n) gives
     to_bf16(R + to_bf16(A.B^T)) bit for bit, also in place (R = C)."""
     g = torch.Generator(device=DEV).manual_seed(m + k)
     a, b = _operands("nt", m, n, k, g)
-    r = torch.randn(m, n, device=DEV, generator=g).to(BF)
+    r = torch.randn(m, n + pad, device=DEV, generator=g).to(BF)[:, :n]
     product = ops.gemm("nt", a, b)
     _check("nt", a, b, product, exact=True)
-    fused = ops.gemm("nt", a, b, residual=r)
+    out = torch.full((m, n + 2 * pad), 7.0, device=DEV, dtype=BF)
+    fused = ops.gemm("nt", a, b, residual=r, out=out[:, :n])
     assert torch.equal(fused, (r.float() + product.float()).to(BF))
+    assert pad == 0 or bool((out[:, n:] == 7.0).all()), "columns past n written"
     inplace = r.clone()
     ops.gemm("nt", a, b, residual=inplace, out=inplace)
     assert torch.equal(inplace, fused)
